@@ -1,0 +1,52 @@
+// Shared device/host helpers for the gfx950 (CDNA4) quantized-matmul library.
+//
+// Everything here is written for wave64 / MFMA on gfx950 only. Conventions:
+//   * all entry points are extern "C", take raw device pointers, and launch on
+//     the stream they are given (nullptr = the null stream);
+//   * floating-point contraction is disabled for the whole library
+//     (-ffp-contract=off); fused multiply-adds are written explicitly with
+//     __builtin_fmaf where they are wanted, so the packers keep the exact
+//     two-rounding arithmetic of the numpy formulas they restate.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// 16-byte vector that only promises 4-byte alignment (rows of the inline-scale
+// FP8 format start every 132 bytes).
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+#define FL_WAVE 64
+
+#define FL_DEV __device__ __forceinline__
+
+template <typename T, typename S>
+FL_DEV T bitcast(S s) {
+    static_assert(sizeof(T) == sizeof(S), "bitcast size");
+    return __builtin_bit_cast(T, s);
+}
+
+// v_mfma_f32_16x16x32_f16: D[16x16] += A[16x32] * B[32x16].
+// Operand layout (wave64): lane l holds A[l%16][8*(l/16) .. +7] and
+// B[8*(l/16) .. +7][l%16]; D lane l holds D[4*(l/16) + i][l%16], i = 0..3.
+FL_DEV f32x4 mfma_f16(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+FL_DEV f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+FL_DEV float half_bits_to_float(uint16_t h) { return (float)bitcast<f16>(h); }
+
+// Host-side launch error check: returns the HIP error of the last launch.
+static inline hipError_t fl_last_error() { return hipGetLastError(); }
+
+static inline int fl_ceil_div(int a, int b) { return (a + b - 1) / b; }

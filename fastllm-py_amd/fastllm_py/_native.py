@@ -1,0 +1,138 @@
+"""ctypes binding of native/libfastllm_kernels.so (the gfx950 HIP library).
+
+The library is the only compute path: when it is missing, or no ROCm device
+is visible, every kernel wrapper raises.  There is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.abspath(os.path.join(_HERE, "..", "native", "libfastllm_kernels.so"))
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+_B = ctypes.c_bool
+
+# name -> (restype, argtypes).  Mirrors include/fastllm_kernels.h.
+SIGNATURES: dict[str, tuple] = {
+    # INT4 Marlin ABI
+    "FastllmCudaGptqMarlinRepack": (_B, [_P, _P, _I, _I]),
+    "FastllmCudaGptqMarlinRepackStream": (_B, [_P, _P, _I, _I, _P]),
+    "FastllmCudaMarlinHalfInt4Gemm": (_B, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "FastllmCudaMarlinHalfInt4GemmStream": (_B, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P]),
+    "fastllm_int4_tile_unrepack": (_B, [_P, _P, _I, _I, _P]),
+    # packers / unpackers
+    "fastllm_pack_gptq_qweight": (_I, [_P, _P, _I, _I, _P]),
+    "fastllm_build_marlin_scales_zeros": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "fastllm_quantize_int4_group": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "fastllm_dequantize_int4_group": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "fastllm_quantize_int4_marlin": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "fastllm_quantize_int4_rowmajor": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "fastllm_dequantize_int4_rowmajor": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "fastllm_fp8_e4m3_encode": (_I, [_P, _P, ctypes.c_long, _P]),
+    "fastllm_fp8_e4m3_decode": (_I, [_P, _P, ctypes.c_long, _P]),
+    "fastllm_quantize_fp8_block": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "fastllm_dequantize_fp8_block": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+}
+
+
+def check_rc(rc, name: str):
+    """Raise on a non-zero int return code / False bool return (reference
+    wrappers raise RuntimeError on failure, marlin.py:187-188, fp8.py:93-94)."""
+    if rc is False or (not isinstance(rc, bool) and rc != 0):
+        raise RuntimeError(f"{name} failed (rc={rc})")
+
+_lib = None
+
+
+def load():
+    """Load and bind the library (raises FileNotFoundError when not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise FileNotFoundError(
+            f"libfastllm_kernels.so not found at {LIB_PATH}; run "
+            "python fastllm-py_amd/build_native.py")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        if hasattr(lib, name):
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def lib():
+    return _lib or load()
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except Exception:
+        return False
+
+
+# ---------------------------------------------------------------- tensors
+def torch():
+    import torch as _t
+    return _t
+
+
+def require_device():
+    t = torch()
+    if not t.cuda.is_available():
+        raise RuntimeError("fastllm_py: no ROCm GPU visible; the HIP kernels are the only path")
+
+
+def is_tensor(x) -> bool:
+    t = torch()
+    return isinstance(x, t.Tensor)
+
+
+def to_device(x, dtype=None):
+    """numpy/torch -> contiguous CUDA tensor (optionally cast)."""
+    t = torch()
+    require_device()
+    if isinstance(x, np.ndarray):
+        x = t.from_numpy(np.ascontiguousarray(x))
+    elif not isinstance(x, t.Tensor):
+        x = t.as_tensor(np.asarray(x))
+    if dtype is not None and x.dtype != dtype:
+        x = x.to(dtype)
+    if not x.is_cuda:
+        x = x.cuda()
+    return x.contiguous()
+
+
+def ptr(x) -> int:
+    return int(x.data_ptr())
+
+
+def current_stream_handle() -> int:
+    t = torch()
+    return int(t.cuda.current_stream().cuda_stream)
+
+
+def stream_handle(stream) -> int:
+    """torch.cuda.Stream / raw int handle / None (null stream) -> int."""
+    if stream is None:
+        return 0
+    if isinstance(stream, int):
+        return stream
+    return int(stream.cuda_stream)
+
+
+def as_output(x, like_numpy: bool):
+    """Return x as numpy when the caller passed numpy (xp=np style)."""
+    if like_numpy:
+        return x.cpu().numpy()
+    return x

@@ -1,0 +1,212 @@
+"""INT4 (uint4, AWQ-style zero point) group-32/128 weight-only GEMM, Marlin ABI.
+
+Drop-in for the reference's ``fastllm_py/kernels/marlin.py`` with PyTorch-ROCm
+tensors as the buffers (reference: fastllm_py/kernels/marlin.py:1-299).  The
+functions keep their names, argument order and meaning:
+
+* ``size_m`` activation rows, ``size_k`` input features (groups run along it),
+  ``size_n`` output features;
+* ``C[size_m, size_n] = A[size_m, size_k] @ dequant(W).T`` with
+  ``dequant(W)[n, k] = scale[g, n] * (q[n, k] - zero[g, n])``.
+
+Every computation runs in ``native/libfastllm_kernels.so`` (gfx950 HIP).  The
+host-prep helpers (``pack_gptq_qweight``, ``build_marlin_scales_zeros``)
+accept numpy or torch input: numpy in (``xp=np``, the reference default) gives
+numpy out, computed on the GPU and copied back; torch in gives a device tensor.
+The repacked weight is this library's own tile layout (same u32 count as the
+GPTQ input, as ``marlin_repack``'s callers assume).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .. import _native as nat
+
+# Marlin's fixed 64-column permutation tables (the caller-visible scale/zero
+# layout; fastllm_py/kernels/marlin.py:41-51).
+_SCALE_PERM = np.array([8 * j + i for i in range(8) for j in range(8)], dtype=np.int64)
+_ZP_INTERLEAVE = np.array([0, 2, 4, 6, 1, 3, 5, 7], dtype=np.int64)
+
+
+def _load():
+    return nat.load()
+
+
+def has_stream_gemm() -> bool:
+    return hasattr(_load(), "FastllmCudaMarlinHalfInt4GemmStream")
+
+
+def available() -> bool:
+    try:
+        _load()
+        return True
+    except Exception:
+        return False
+
+
+# --------------------------------------------------------------------------
+# weight-prep helpers (GPU kernels; reference does these in numpy)
+# --------------------------------------------------------------------------
+def pack_gptq_qweight(q_int4, xp=np):
+    """int4 weight [size_n, size_k] (values 0..15) -> uint32 [size_k//8, size_n].
+
+    Value k at bits 4*(k%8) of word [k//8, n] (marlin.py:113-127)."""
+    t = nat.torch()
+    size_n, size_k = q_int4.shape
+    assert size_k % 8 == 0, "size_k must be a multiple of 8"
+    numpy_in = isinstance(q_int4, np.ndarray)
+    if numpy_in:
+        q = nat.to_device(np.asarray(q_int4).astype(np.uint32))
+    else:
+        q = nat.to_device(q_int4)
+        if q.dtype != t.uint32:
+            q = q.to(t.int64).to(t.int32).view(t.uint32) if q.dtype != t.int32 else q.view(t.uint32)
+    out = t.empty((size_k // 8, size_n), dtype=t.uint32, device=q.device)
+    rc = _load().fastllm_pack_gptq_qweight(nat.ptr(q), nat.ptr(out), size_n, size_k,
+                                           nat.current_stream_handle())
+    nat.check_rc(rc, "fastllm_pack_gptq_qweight")
+    return nat.as_output(out, numpy_in)
+
+
+def build_marlin_scales_zeros(scale, zero_int, group_size, xp=np):
+    """Permute scales/zeros into the Marlin tile layout (marlin.py:130-159).
+
+    scale [size_n, num_groups] float, zero_int [size_n, num_groups] int (0..15)
+    -> (scales fp16 [num_groups, size_n], zeros u32 [num_groups, size_n//8])."""
+    t = nat.torch()
+    size_n, num_groups = scale.shape
+    assert size_n % 64 == 0, "size_n must be a multiple of 64"
+    numpy_in = isinstance(scale, np.ndarray)
+    s = nat.to_device(np.asarray(scale).astype(np.float32) if numpy_in else scale, t.float32)
+    if isinstance(zero_int, np.ndarray):
+        z = nat.to_device(np.asarray(zero_int).astype(np.int64).astype(np.int32))
+    else:
+        z = nat.to_device(zero_int).to(t.int64).to(t.int32)
+    scales = t.empty((num_groups, size_n), dtype=t.float16, device=s.device)
+    zeros = t.empty((num_groups, size_n // 8), dtype=t.uint32, device=s.device)
+    rc = _load().fastllm_build_marlin_scales_zeros(
+        nat.ptr(s), nat.ptr(z), nat.ptr(scales), nat.ptr(zeros), size_n, num_groups,
+        nat.current_stream_handle())
+    nat.check_rc(rc, "fastllm_build_marlin_scales_zeros")
+    return nat.as_output(scales, numpy_in), nat.as_output(zeros, numpy_in)
+
+
+def make_workspace(size_n, xp=None):
+    """Zeroed int32 workspace, size max(1, (size_n//64)*16) (marlin.py:162-167)."""
+    t = nat.torch()
+    nat.require_device()
+    n = max(1, (size_n // 64) * 16)
+    return t.zeros(n, dtype=t.int32, device="cuda")
+
+
+# --------------------------------------------------------------------------
+# kernel calls
+# --------------------------------------------------------------------------
+def marlin_repack(std_qweight, size_k, size_n):
+    """Device repack of GPTQ u32 [size_k//8, size_n] into the tile layout.
+
+    Returns a flat uint32 device tensor with the same element count
+    (marlin.py:173-189); synchronizes like the reference."""
+    t = nat.torch()
+    lib = _load()
+    std = nat.to_device(std_qweight)
+    if std.dtype != t.uint32:
+        std = std.to(t.int64).to(t.int32).view(t.uint32) if std.dtype != t.int32 else std.view(t.uint32)
+    out = t.empty(std.numel(), dtype=t.uint32, device=std.device)
+    ok = lib.FastllmCudaGptqMarlinRepack(nat.ptr(std), nat.ptr(out), int(size_k), int(size_n))
+    t.cuda.synchronize()
+    if not ok:
+        raise RuntimeError("FastllmCudaGptqMarlinRepack failed (check size_k/size_n tiling)")
+    return out
+
+
+def marlin_unrepack(tile_qweight, size_k, size_n):
+    """Inverse of marlin_repack: tile layout -> GPTQ u32 [size_k//8, size_n]."""
+    t = nat.torch()
+    src = nat.to_device(tile_qweight)
+    out = t.empty((size_k // 8, size_n), dtype=t.uint32, device=src.device)
+    ok = _load().fastllm_int4_tile_unrepack(nat.ptr(src), nat.ptr(out), int(size_k), int(size_n),
+                                            nat.current_stream_handle())
+    if not ok:
+        raise RuntimeError("fastllm_int4_tile_unrepack failed")
+    return out
+
+
+_workspaces: dict = {}  # (device_id, size_n) -> zeroed int32 workspace
+
+
+def get_workspace(size_n: int):
+    """Shared per-device workspace (marlin.py:195-202)."""
+    t = nat.torch()
+    key = (t.cuda.current_device(), size_n)
+    if key not in _workspaces:
+        _workspaces[key] = make_workspace(size_n)
+    return _workspaces[key]
+
+
+def gemm_fast(a_fp16, qweight, scales, zeros, size_n, size_k, stream=None, workspace=None):
+    """Lean GEMV/GEMM for the decode hot path (marlin.py:205-247).
+
+    Trusts that a_fp16 is a contiguous fp16 device tensor and that
+    qweight/scales/zeros were validated at load time.  stream: a
+    torch.cuda.Stream (or raw handle) to launch on through the stream entry;
+    None launches on the null stream.  Like the reference it does not check
+    the entry's return value."""
+    t = nat.torch()
+    lib = nat.lib()
+    size_m = a_fp16.shape[0]
+    group_size = size_k // scales.shape[0]
+    c = t.empty((size_m, size_n), dtype=t.float16, device=a_fp16.device)
+    ws = workspace if workspace is not None else get_workspace(size_n)
+    if stream is not None:
+        lib.FastllmCudaMarlinHalfInt4GemmStream(
+            nat.ptr(a_fp16), nat.ptr(qweight), nat.ptr(scales), nat.ptr(zeros), nat.ptr(c),
+            size_m, size_n, size_k, group_size, nat.ptr(ws), nat.stream_handle(stream))
+    else:
+        lib.FastllmCudaMarlinHalfInt4Gemm(
+            nat.ptr(a_fp16), nat.ptr(qweight), nat.ptr(scales), nat.ptr(zeros), nat.ptr(c),
+            size_m, size_n, size_k, group_size, nat.ptr(ws))
+    return c
+
+
+def marlin_gemm_int4(a_fp16, packed_weights, scales, zeros, workspace=None, size_n=None,
+                     sync=True):
+    """INT4 GEMM with validation (marlin.py:250-299).
+
+    a_fp16 [size_m, size_k] (cast to fp16), packed_weights from marlin_repack,
+    scales fp16 [num_groups, size_n], zeros u32 [num_groups, size_n//8].
+    Returns fp16 [size_m, size_n]; raises ValueError on bad shapes and
+    RuntimeError when the library rejects the call."""
+    t = nat.torch()
+    lib = _load()
+    a = nat.to_device(a_fp16, t.float16)
+    size_m, size_k = a.shape
+    num_groups = scales.shape[0]
+    if size_n is None:
+        size_n = scales.shape[1]
+    if workspace is None:
+        workspace = get_workspace(size_n)
+    group_size = size_k // num_groups
+
+    if size_n % 64 != 0 or size_k % 64 != 0:
+        raise ValueError(f"size_n({size_n}) and size_k({size_k}) must be multiples of 64")
+    if group_size not in (32, 128):
+        raise ValueError(f"group_size must be 32 or 128, got {group_size}")
+    if size_k % group_size != 0:
+        raise ValueError("size_k must be a multiple of group_size")
+
+    scales = nat.to_device(scales, t.float16)
+    zeros = nat.to_device(zeros)
+    if zeros.dtype != t.uint32:
+        zeros = zeros.to(t.int64).to(t.int32).view(t.uint32)
+    qw = nat.to_device(packed_weights)
+    c = t.empty((size_m, size_n), dtype=t.float16, device=a.device)
+    ok = lib.FastllmCudaMarlinHalfInt4Gemm(
+        nat.ptr(a), nat.ptr(qw), nat.ptr(scales), nat.ptr(zeros), nat.ptr(c),
+        size_m, size_n, size_k, group_size, nat.ptr(workspace))
+    if sync:
+        t.cuda.synchronize()
+    if not ok:
+        raise RuntimeError("FastllmCudaMarlinHalfInt4Gemm returned false "
+                           "(unsupported device or shape)")
+    return c

@@ -1,0 +1,129 @@
+"""Weight quantization: FP8-E4M3 128x128 block and INT4 group quantization.
+
+Same API as the reference's ``fastllm_py/quantizer.py`` (lines 13-129); the
+arithmetic runs in gfx950 HIP kernels (csrc/packers.hip) that reproduce the
+reference's numpy formulas bit for bit.  numpy input gives numpy output
+(computed on the GPU and copied back); torch input gives device tensors.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _native as nat
+
+FP8_E4M3_MAX = 448.0
+
+
+@dataclass
+class QuantizedTensor:
+    kind: str  # "fp8_e4m3_block" | "int4_group"
+    data: object  # uint8 array (numpy or torch)
+    scales: object  # float array
+    shape: tuple[int, int]  # original (out_features, in_features)
+    block_size: int
+    zeros: object = None  # int4 only
+
+
+def _f32_device(x):
+    t = nat.torch()
+    if isinstance(x, np.ndarray):
+        return nat.to_device(np.ascontiguousarray(x, dtype=np.float32))
+    return nat.to_device(x, t.float32)
+
+
+def _fp8_e4m3_encode(x, xp=np):
+    """float array -> uint8 e4m3fn bytes, the reference encoder
+    (quantizer.py:26-51, including its subnormal clip-to-7)."""
+    t = nat.torch()
+    numpy_in = isinstance(x, np.ndarray) or np.isscalar(x)
+    xd = _f32_device(np.asarray(x) if numpy_in else x)
+    out = t.empty(xd.shape, dtype=t.uint8, device=xd.device)
+    rc = nat.lib().fastllm_fp8_e4m3_encode(nat.ptr(xd), nat.ptr(out), xd.numel(),
+                                           nat.current_stream_handle())
+    nat.check_rc(rc, "fastllm_fp8_e4m3_encode")
+    return nat.as_output(out, numpy_in)
+
+
+def _fp8_e4m3_decode(b, xp=np):
+    """uint8 e4m3fn -> float32, exact (quantizer.py:54-62)."""
+    t = nat.torch()
+    numpy_in = isinstance(b, np.ndarray)
+    bd = nat.to_device(np.asarray(b).astype(np.uint8) if numpy_in else b, t.uint8)
+    out = t.empty(bd.shape, dtype=t.float32, device=bd.device)
+    rc = nat.lib().fastllm_fp8_e4m3_decode(nat.ptr(bd), nat.ptr(out), bd.numel(),
+                                           nat.current_stream_handle())
+    nat.check_rc(rc, "fastllm_fp8_e4m3_decode")
+    return nat.as_output(out, numpy_in)
+
+
+def quantize_fp8_block(w, block_size: int = 128, xp=np) -> QuantizedTensor:
+    """Per (bs x bs) 2-D block scaling (quantizer.py:65-85).
+
+    w: (out_features, in_features). scales: (ceil(out/bs), ceil(in/bs)) fp32;
+    data cropped to (out, in) uint8."""
+    t = nat.torch()
+    numpy_in = isinstance(w, np.ndarray)
+    wd = _f32_device(w)
+    out_f, in_f = wd.shape
+    bs = int(block_size)
+    q = t.empty((out_f, in_f), dtype=t.uint8, device=wd.device)
+    scales = t.empty(((out_f + bs - 1) // bs, (in_f + bs - 1) // bs), dtype=t.float32,
+                     device=wd.device)
+    rc = nat.lib().fastllm_quantize_fp8_block(nat.ptr(wd), nat.ptr(q), nat.ptr(scales), out_f,
+                                              in_f, bs, nat.current_stream_handle())
+    nat.check_rc(rc, "fastllm_quantize_fp8_block")
+    return QuantizedTensor("fp8_e4m3_block", nat.as_output(q, numpy_in),
+                           nat.as_output(scales, numpy_in), (out_f, in_f), bs)
+
+
+def dequantize_fp8_block(qt: QuantizedTensor, xp=np):
+    """decode(q) * block scale (quantizer.py:88-94)."""
+    t = nat.torch()
+    numpy_in = isinstance(qt.data, np.ndarray)
+    out_f, in_f = qt.shape
+    q = nat.to_device(qt.data, t.uint8)
+    s = _f32_device(qt.scales)
+    out = t.empty((out_f, in_f), dtype=t.float32, device=q.device)
+    rc = nat.lib().fastllm_dequantize_fp8_block(nat.ptr(q), nat.ptr(s), nat.ptr(out), out_f, in_f,
+                                                qt.block_size, nat.current_stream_handle())
+    nat.check_rc(rc, "fastllm_dequantize_fp8_block")
+    return nat.as_output(out, numpy_in)
+
+
+def quantize_int4_group(w, group_size: int = 128, xp=np) -> QuantizedTensor:
+    """Asymmetric INT4 with per-group min/max scaling along in_features
+    (quantizer.py:97-117).  data (out, in/2) uint8, even column in the low
+    nibble; scales and zeros (= group minimum) (out, in/group) float32."""
+    t = nat.torch()
+    numpy_in = isinstance(w, np.ndarray)
+    wd = _f32_device(w)
+    out_f, in_f = wd.shape
+    assert in_f % group_size == 0 and in_f % 2 == 0
+    packed = t.empty((out_f, in_f // 2), dtype=t.uint8, device=wd.device)
+    scales = t.empty((out_f, in_f // group_size), dtype=t.float32, device=wd.device)
+    zeros = t.empty_like(scales)
+    rc = nat.lib().fastllm_quantize_int4_group(nat.ptr(wd), nat.ptr(packed), nat.ptr(scales),
+                                               nat.ptr(zeros), out_f, in_f, group_size,
+                                               nat.current_stream_handle())
+    nat.check_rc(rc, "fastllm_quantize_int4_group")
+    return QuantizedTensor("int4_group", nat.as_output(packed, numpy_in),
+                           nat.as_output(scales, numpy_in), (out_f, in_f), group_size,
+                           zeros=nat.as_output(zeros, numpy_in))
+
+
+def dequantize_int4_group(qt: QuantizedTensor, xp=np):
+    """q * scale + zero (quantizer.py:120-129)."""
+    t = nat.torch()
+    numpy_in = isinstance(qt.data, np.ndarray)
+    out_f, in_f = qt.shape
+    p = nat.to_device(qt.data, t.uint8)
+    s = _f32_device(qt.scales)
+    z = _f32_device(qt.zeros)
+    out = t.empty((out_f, in_f), dtype=t.float32, device=p.device)
+    rc = nat.lib().fastllm_dequantize_int4_group(nat.ptr(p), nat.ptr(s), nat.ptr(z), nat.ptr(out),
+                                                 out_f, in_f, qt.block_size,
+                                                 nat.current_stream_handle())
+    nat.check_rc(rc, "fastllm_dequantize_int4_group")
+    return nat.as_output(out, numpy_in)

@@ -1,0 +1,164 @@
+/*
+ * libfastllm_kernels.so — MI355X (gfx950) quantized-weight matmul library.
+ *
+ * C ABI, drop-in for the ctypes entry points of the reference's
+ * native/libfastllm_kernels.so, plus entry points for the kernels the
+ * reference launches as CuPy RawKernels.  Every pointer is a device pointer
+ * on the calling thread's current HIP device; every `stream` argument is a
+ * hipStream_t (nullptr = the null stream).  The library allocates no device
+ * memory in any entry point below; callers own every buffer.
+ *
+ * Reference citations are path:line in codemk8/fastllm-py.
+ */
+#ifndef FASTLLM_KERNELS_H
+#define FASTLLM_KERNELS_H
+
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------
+ * INT4 group-32/128 weight-only GEMM, Marlin ABI
+ * ------------------------------------------------------------------------ */
+
+/* Repack GPTQ-packed INT4 (u32 [size_k/8, size_n], value k at bits 4*(k%8)
+ * of word [k/8, n]) into this library's tile layout, same u32 count.
+ * size_k % 64 == 0, size_n % 64 == 0.  Null stream, asynchronous.
+ * Replaces: FastllmCudaGptqMarlinRepack, bound at
+ * fastllm_py/kernels/marlin.py:68-70, called at :182. */
+bool FastllmCudaGptqMarlinRepack(const uint32_t *b_q_weight, uint32_t *out,
+                                 int size_k, int size_n);
+
+/* Same as FastllmCudaGptqMarlinRepack on an explicit stream.
+ * Replaces: FastllmCudaGptqMarlinRepackStream of the Marlin file the
+ * reference builds (documented in docs/fastllm-internals.md:399-401). */
+bool FastllmCudaGptqMarlinRepackStream(const uint32_t *b_q_weight,
+                                       uint32_t *out, int size_k, int size_n,
+                                       void *stream);
+
+/* C[size_m, size_n] (fp16) = A[size_m, size_k] (fp16) @ dequant(W)^T with
+ * dequant(W)[n,k] = scales[g,n] * (q[n,k] - zeros[g,n]), g = k/group_size.
+ * b_q_weight: tile layout from FastllmCudaGptqMarlinRepack.
+ * b_scales: fp16 [G, size_n], b_zeros: u32 [G, size_n/8], both in the Marlin
+ * permutation built by build_marlin_scales_zeros.
+ * Returns false (no launch) for size_n % 64, size_k % 64, group_size not in
+ * {32, 128}, size_k % group_size, a/b_q_weight not 16-byte aligned, or a
+ * non-gfx950 device.  workspace is accepted for ABI compatibility and is not
+ * written.  Null stream, asynchronous.
+ * Replaces: FastllmCudaMarlinHalfInt4Gemm, bound at
+ * fastllm_py/kernels/marlin.py:72-82, called at :238 and :285. */
+bool FastllmCudaMarlinHalfInt4Gemm(const void *a, const uint32_t *b_q_weight,
+                                   const void *b_scales,
+                                   const uint32_t *b_zeros, void *c,
+                                   int size_m, int size_n, int size_k,
+                                   int group_size, int *workspace);
+
+/* FastllmCudaMarlinHalfInt4Gemm on an explicit stream (graph-capturable).
+ * Replaces: FastllmCudaMarlinHalfInt4GemmStream,
+ * native/marlin_stream_entry.inc:8-33, bound at
+ * fastllm_py/kernels/marlin.py:86-93, called at :227. */
+bool FastllmCudaMarlinHalfInt4GemmStream(const void *a,
+                                         const uint32_t *b_q_weight,
+                                         const void *b_scales,
+                                         const uint32_t *b_zeros, void *c,
+                                         int size_m, int size_n, int size_k,
+                                         int group_size, int *workspace,
+                                         void *stream);
+
+/* Inverse of the repack: tile layout -> GPTQ u32 [size_k/8, size_n].
+ * No counterpart in the reference (its repacked layout is opaque); used to
+ * prove the repack is a bijection. */
+bool fastllm_int4_tile_unrepack(const uint32_t *tile_q, uint32_t *gptq_out,
+                                int size_k, int size_n, void *stream);
+
+/* ------------------------------------------------------------------------
+ * Packers / unpackers (GPU, bit-exact with the reference's numpy formulas).
+ * Return 0 on success, 1 on bad arguments, 2 on a launch error.  All are
+ * asynchronous on `stream`.  The reference computes these on the host with
+ * numpy (or CuPy through the same expressions); the cited function is the
+ * one each entry replaces.
+ * ------------------------------------------------------------------------ */
+
+/* q u32 [size_n, size_k] (values 0..15) -> u32 [size_k/8, size_n],
+ * value k at bits 4*(k%8).  Replaces: pack_gptq_qweight,
+ * fastllm_py/kernels/marlin.py:113-127. */
+int fastllm_pack_gptq_qweight(const uint32_t *q, uint32_t *out, int size_n,
+                              int size_k, void *stream);
+
+/* scale f32 [size_n, G], zero i32 [size_n, G] -> scales fp16 [G, size_n] and
+ * zeros u32 [G, size_n/8] in the Marlin 64-column permutation.
+ * Replaces: build_marlin_scales_zeros, fastllm_py/kernels/marlin.py:130-159. */
+int fastllm_build_marlin_scales_zeros(const float *scale, const int32_t *zero,
+                                      void *scales_out, uint32_t *zeros_out,
+                                      int size_n, int num_groups,
+                                      void *stream);
+
+/* w f32 [rows, cols] -> packed u8 [rows, cols/2], scales f32 and zeros
+ * (= group minimum) f32 [rows, cols/group_size].
+ * Replaces: quantize_int4_group, fastllm_py/quantizer.py:97-117. */
+int fastllm_quantize_int4_group(const float *w, uint8_t *packed, float *scales,
+                                float *zeros, int rows, int cols,
+                                int group_size, void *stream);
+
+/* q*scale + zero -> f32 [rows, cols].
+ * Replaces: dequantize_int4_group, fastllm_py/quantizer.py:120-129. */
+int fastllm_dequantize_int4_group(const uint8_t *packed, const float *scales,
+                                  const float *zeros, float *out, int rows,
+                                  int cols, int group_size, void *stream);
+
+/* Integer-zero-point RTN of the engine's Marlin packer: w f32 [size_n, size_k]
+ * -> q u8 [size_n, size_k], scale f32 [size_n, G], zero i32 [size_n, G].
+ * Replaces: the quantization in quantize_marlin_matrix,
+ * fastllm_py/moe.py:40-46. */
+int fastllm_quantize_int4_marlin(const float *w, uint8_t *q, float *scale,
+                                 int32_t *zero, int size_n, int size_k,
+                                 int group_size, void *stream);
+
+/* Row-major INT4 format, batched over `batch` matrices: w f32
+ * [batch, out_f, in_f] -> packed u8 [batch, out_f, in_f/2], scales/zeros fp16
+ * [batch, out_f, in_f/group_size].
+ * Replaces: quantize_int4_rowmajor / _quantize_int4_rowmajor_batched,
+ * fastllm_py/kernels/moe_int4.py:24-40,97-113. */
+int fastllm_quantize_int4_rowmajor(const float *w, uint8_t *packed,
+                                   void *scales, void *zeros, int batch,
+                                   int out_f, int in_f, int group_size,
+                                   void *stream);
+
+/* (q - zero) * scale -> f32 [batch, out_f, in_f].
+ * Replaces: dequantize_int4_rowmajor, fastllm_py/kernels/moe_int4.py:43-54. */
+int fastllm_dequantize_int4_rowmajor(const uint8_t *packed, const void *scales,
+                                     const void *zeros, float *out, int batch,
+                                     int out_f, int in_f, int group_size,
+                                     void *stream);
+
+/* f32 -> e4m3fn bytes with the reference's rounding and subnormal clip.
+ * Replaces: _fp8_e4m3_encode, fastllm_py/quantizer.py:26-51. */
+int fastllm_fp8_e4m3_encode(const float *x, uint8_t *out, long n,
+                            void *stream);
+
+/* e4m3fn bytes -> f32, exact.
+ * Replaces: _fp8_e4m3_decode, fastllm_py/quantizer.py:54-62. */
+int fastllm_fp8_e4m3_decode(const uint8_t *b, float *out, long n,
+                            void *stream);
+
+/* (block_size x block_size) block FP8: w f32 [rows, cols] -> q u8 [rows, cols]
+ * and scales f32 [ceil(rows/bs), ceil(cols/bs)].
+ * Replaces: quantize_fp8_block, fastllm_py/quantizer.py:65-85. */
+int fastllm_quantize_fp8_block(const float *w, uint8_t *q, float *scales,
+                               int rows, int cols, int block_size,
+                               void *stream);
+
+/* decode(q) * block scale -> f32 [rows, cols].
+ * Replaces: dequantize_fp8_block, fastllm_py/quantizer.py:88-94. */
+int fastllm_dequantize_fp8_block(const uint8_t *q, const float *scales,
+                                 float *out, int rows, int cols,
+                                 int block_size, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FASTLLM_KERNELS_H */
