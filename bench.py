@@ -63,57 +63,68 @@ def build_int4_layers(torch, copies):
     return layers
 
 
-def run_int4(torch, lib, layers, M, steps, warmup, stream):
-    """Time `steps` layer passes at batch M on `stream` (HIP events on that
-    stream).  Returns (ms_per_step, per-launch event durations by shape)."""
-    from fastllm_py import _native as nat
+def _graph_time(torch, stream, launch_seq, reps, warmup):
+    """Capture launch_seq() (a list of enqueue callbacks) in one HIP graph on
+    `stream`, replay it warmup times, then time `reps` replays with HIP
+    events on that stream.  Returns ms per replay."""
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        h = torch.cuda.current_stream().cuda_stream
+        for fn in launch_seq:
+            fn(h)
+    for _ in range(max(1, warmup)):
+        g.replay()
+    stream.synchronize()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        t0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        t1.record(stream)
+    stream.synchronize()
+    return t0.elapsed_time(t1) / reps
 
+
+def run_int4(torch, lib, layers, M, steps, warmup, stream):
+    """Time `steps` layer passes at batch M.  One HIP graph holds a pass over
+    every layer copy (4 GEMVs each); replays are timed with HIP events on the
+    launch stream.  Also times each shape alone (a graph of back-to-back
+    launches over the copies) for per-call figures.
+    Returns (ms_per_step, {shape: us_per_call})."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(2001 + M)
     xs = {K: torch.randn((M, K), generator=gen, device="cuda").to(torch.float16)
           for K in {k for _, _, k in QWEN3_8B}}
     outs = {name: torch.empty((M, N), dtype=torch.float16, device="cuda")
             for name, N, _ in QWEN3_8B}
-    h = nat.stream_handle(stream)
     fn = lib.FastllmCudaMarlinHalfInt4GemmStream
 
-    def launch(layer, name, N, K):
+    def launcher(layer, name, N, K):
         p = layer[name]
-        ok = fn(xs[K].data_ptr(), p["qweight"].data_ptr(), p["scales"].data_ptr(),
-                p["zeros"].data_ptr(), outs[name].data_ptr(), M, N, K, GS, None, h)
-        if not ok:
-            raise RuntimeError(f"INT4 GEMM rejected M={M} N={N} K={K}")
+        args = (xs[K].data_ptr(), p["qweight"].data_ptr(), p["scales"].data_ptr(),
+                p["zeros"].data_ptr(), outs[name].data_ptr(), M, N, K, GS, None)
 
+        def go(h):
+            if not fn(*args, h):
+                raise RuntimeError(f"INT4 GEMM rejected M={M} N={N} K={K}")
+        return go
+
+    # every timed graph holds >= 96 launches so graph-launch cost is amortised
     L = len(layers)
-    with torch.cuda.stream(stream):
-        for i in range(warmup):
-            for name, N, K in QWEN3_8B:
-                launch(layers[i % L], name, N, K)
-        stream.synchronize()
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        t0.record(stream)
-        for i in range(steps):
-            for name, N, K in QWEN3_8B:
-                launch(layers[i % L], name, N, K)
-        t1.record(stream)
-        stream.synchronize()
-        ms_step = t0.elapsed_time(t1) / steps
-        # per-launch durations (events bracketing every launch)
-        per = {name: [] for name, _, _ in QWEN3_8B}
-        evs = []
-        for i in range(steps):
-            for name, N, K in QWEN3_8B:
-                a = torch.cuda.Event(enable_timing=True)
-                b = torch.cuda.Event(enable_timing=True)
-                a.record(stream)
-                launch(layers[i % L], name, N, K)
-                b.record(stream)
-                evs.append((name, a, b))
-        stream.synchronize()
-        for name, a, b in evs:
-            per[name].append(a.elapsed_time(b))
-    return ms_step, {k: float(np.mean(v)) for k, v in per.items()}
+    rounds = max(1, -(-24 // L))
+    seq = [launcher(layers[c], name, N, K)
+           for _ in range(rounds) for c in range(L) for name, N, K in QWEN3_8B]
+    per_graph = rounds * L
+    reps = max(1, -(-steps // per_graph))
+    ms_step = _graph_time(torch, stream, seq, reps, max(1, warmup // per_graph)) / per_graph
+    per = {}
+    rounds1 = max(1, -(-96 // L))
+    for name, N, K in QWEN3_8B:
+        seq1 = [launcher(layers[c], name, N, K) for _ in range(rounds1) for c in range(L)]
+        per[name] = _graph_time(torch, stream, seq1, max(2, reps // 4), 1) / (rounds1 * L)
+    return ms_step, per, reps * per_graph
 
 
 # ------------------------------------------------------------- CPU baseline
@@ -182,28 +193,31 @@ def main():
     per_m = {}
     ms_list = [int(m) for m in args.ms.split(",")]
     for M in ms_list:
-        ms_step, per = run_int4(torch, lib, layers, M, args.steps, args.warmup, stream)
+        ms_step, per, steps_done = run_int4(torch, lib, layers, M, args.steps, args.warmup, stream)
+        if M == ms_list[0]:
+            steps_run = steps_done
         nbytes = sum(marlin_bytes(M, N, K) for _, N, K in QWEN3_8B)
         gbs = nbytes / (ms_step * 1e-3) / 1e9
         per_m[M] = {"ms_per_layer": ms_step, "GB/s": gbs,
-                    "us_per_call": {k: round(v * 1e3, 2) for k, v in per.items()},
+                    "us_per_call": {k: round(v * 1e3, 3) for k, v in per.items()},
                     "bytes_per_layer": nbytes}
         log(f"INT4 M={M}: {ms_step * 1e3:.1f} us/layer  {gbs:.0f} GB/s "
             f"({gbs / HBM_PEAK_GBS * 100:.1f}% of 8 TB/s)  per call us: "
             f"{ {k: round(v * 1e3, 2) for k, v in per.items()} }")
 
     head = per_m[ms_list[0]]
-    # roofline of the dominant kernel (the INT4 GEMV kernel, all four shapes at
-    # the headline M): mean algorithmic bytes per launch / mean launch duration
+    # roofline of the dominant kernel: the gate_up GEMV (24576x4096, 52% of the
+    # layer's bytes) at the headline M, timed alone as a graph of back-to-back
+    # launches over the rotating weight copies.
     M0 = ms_list[0]
-    bytes_per_launch = np.mean([marlin_bytes(M0, N, K) for _, N, K in QWEN3_8B])
-    dur_ms = np.mean(list(head["us_per_call"].values())) * 1e-3
-    achieved = bytes_per_launch / (dur_ms * 1e-3) / 1e9
+    bytes_per_launch = marlin_bytes(M0, 24576, 4096)
+    dur_us = head["us_per_call"]["gate_up"]
+    achieved = bytes_per_launch / (dur_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "int4_tile_mm<1,1,false>",
+                "kernel": "int4_gemv_nb<2,4,false,true> (gate_up 24576x4096, M=%d)" % M0,
                 "bytes_per_launch": int(bytes_per_launch),
-                "us_per_launch": round(dur_ms * 1e3, 3)}
+                "us_per_launch": round(dur_us, 3)}
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -215,7 +229,7 @@ def main():
         "value": round(head["GB/s"], 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps_run,
         "warmup": args.warmup,
         "ms_per_step": round(head["ms_per_layer"], 5),
         "higher_is_better": True,

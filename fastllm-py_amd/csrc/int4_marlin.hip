@@ -244,6 +244,314 @@ __global__ __launch_bounds__(1024) void int4_tile_mm(
     }
 }
 
+// (a & m) | c in one VALU op.
+FL_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
+    return r;
+}
+
+// Dequantize with the zero point folded into fp16 constants: zlo = -(1024+z),
+// zhi = -(64+z) as fp16 pairs (exact), magic_lo/hi = 0x64006400 / 0x54005400.
+FL_DEV f16x8 dequant_word_fast(uint32_t w, uint32_t zlo, uint32_t zhi, uint32_t mlo,
+                               uint32_t mhi) {
+    const uint32_t w8 = w >> 8;
+    const f16x2 p0 = bitcast<f16x2>(and_or(w, 0x000F000Fu, mlo)) + bitcast<f16x2>(zlo);
+    const f16x2 p1 = bitcast<f16x2>(and_or(w, 0x00F000F0u, mhi)) + bitcast<f16x2>(zhi);
+    const f16x2 p2 = bitcast<f16x2>(and_or(w8, 0x000F000Fu, mlo)) + bitcast<f16x2>(zlo);
+    const f16x2 p3 = bitcast<f16x2>(and_or(w8, 0x00F000F0u, mhi)) + bitcast<f16x2>(zhi);
+    const u32x4 r{bitcast<uint32_t>(p0), bitcast<uint32_t>(p1), bitcast<uint32_t>(p2),
+                  bitcast<uint32_t>(p3)};
+    return bitcast<f16x8>(r);
+}
+
+// fp16-pair bit patterns of -(1024+z) and -(64+z) for a zero point z in 0..15.
+FL_DEV void zero_bits(uint32_t z, uint32_t& zlo, uint32_t& zhi) {
+    const uint32_t lo = 0xE400u | z;         // -(1024 + z): exponent 10, mantissa z
+    const uint32_t hi = 0xD400u | (z << 4);  // -(64 + z): exponent 6, ulp 1/16
+    zlo = lo | (lo << 16);
+    zhi = hi | (hi << 16);
+}
+
+// Decode-shaped GEMV (M <= 16): one 16-row m-tile, W waves per workgroup on a
+// strip of T n-tiles; the full 128-k blocks of the strip are dealt to the
+// waves round-robin, NB at most per wave.
+//   * Each wave issues ALL of its weight, scale and zero loads before doing
+//     anything else (indices clamped so the issue is unconditional), so HBM
+//     latency is paid once per wave and a workgroup keeps W*NB KB in flight.
+//   * The M x K activations are staged once per workgroup in LDS (row stride
+//     K+8 halves).  MFMA rows >= M read row M-1: C rows are independent and
+//     rows >= M are never stored, so no masking is needed.
+//   * A trailing 64-k block (group 32 only) is done by wave 0 at the end.
+//   * Cross-wave reduction through LDS in fixed wave order.
+template <int T, int NB, bool G32, bool ALDS>
+__global__ __launch_bounds__(1024) void int4_gemv_nb(
+    const f16* __restrict__ A, const uint32_t* __restrict__ Wq, const uint16_t* __restrict__ S,
+    const uint32_t* __restrict__ Z, f16* __restrict__ C, int M, int N, int K) {
+    constexpr int SPB = G32 ? 4 : 1;  // scale groups per 128-k block
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int nwaves = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int strip = blockIdx.x;
+    const int nfull = K >> 7;
+    const int col = lane & 15;
+    const int kq = lane >> 4;
+    const int zwords = N >> 3;
+    const int lda = K + 8;
+    f16* As = reinterpret_cast<f16*>(smem);
+    float* red = reinterpret_cast<float*>(smem + (ALDS ? (((size_t)M * lda * 2 + 15) & ~(size_t)15) : 0));
+
+    const int nb = wave < nfull ? (nfull - wave + nwaves - 1) / nwaves : 0;
+
+    int spos[T], zw[T], zsh[T];
+    const uint32_t* tbase[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int n = (strip * T + t) * 16 + col;
+        spos[t] = marlin_scale_pos(n);
+        const int cl = n & 63;
+        zw[t] = ((n >> 6) << 3) + (cl & 7);
+        zsh[t] = 4 * slot_of(cl >> 3);
+        tbase[t] = Wq + (size_t)(strip * T + t) * (2 * (size_t)K);
+    }
+
+    // Activations are staged by the first `sw` waves (4 chunks of 8 halves
+    // per lane, indices clamped so every lane loads and stores) before those
+    // waves issue their weight loads; the other waves issue weight loads at
+    // once.  Loads retire in issue order, so had the staging loads followed
+    // the weight loads, the LDS barrier would have waited for every weight
+    // block.  M*K too large for that goes through a plain staging loop.
+    const int k8 = K >> 3;
+    const int nchunks = ALDS ? M * k8 : 0;
+    const int sw = (nchunks + 255) >> 8;
+    const bool early = sw <= nwaves;
+    if (ALDS && early && wave < sw) {
+        const float inv_k8 = 1.0f / (float)k8;
+        f16x8 ast[4];
+        int dst[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            int c = (wave * 64 + lane) * 4 + r;
+            c = c < nchunks ? c : nchunks - 1;
+            int m = (int)((float)c * inv_k8);
+            m -= (m * k8 > c) ? 1 : 0;
+            m += ((m + 1) * k8 <= c) ? 1 : 0;
+            const int c8 = c - m * k8;
+            ast[r] = *reinterpret_cast<const f16x8*>(A + (size_t)m * K + c8 * 8);
+            dst[r] = m * lda + c8 * 8;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) *reinterpret_cast<f16x8*>(As + dst[r]) = ast[r];
+    }
+
+    // One straight-line issue of every load this wave will need (block
+    // indices clamped into range: no guard, so nothing derived from the loaded
+    // values can be hoisted up here by the compiler).
+    u32x4 wv[NB][T];
+    uint32_t sv[NB][T][SPB], zv[NB][T][SPB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+        kb = kb < nfull ? kb : nfull - 1;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            wv[i][t] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(tbase[t] + kb * 256 + lane * 4));
+#pragma unroll
+            for (int g = 0; g < SPB; ++g) {
+                const size_t grp = (size_t)kb * SPB + g;
+                sv[i][t][g] = S[grp * N + spos[t]];
+                zv[i][t][g] = Z[grp * zwords + zw[t]];
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    if (ALDS) {
+        if (!early) {
+            for (int idx = threadIdx.x; idx < nchunks; idx += blockDim.x) {
+                const int m = idx / k8, c8 = idx - m * k8;
+                *reinterpret_cast<f16x8*>(As + (size_t)m * lda + c8 * 8) =
+                    *reinterpret_cast<const f16x8*>(A + (size_t)m * K + c8 * 8);
+            }
+        }
+        __syncthreads();
+    }
+
+    const uint32_t mlo = 0x64006400u, mhi = 0x54005400u;
+    const int arow_m = col < M ? col : M - 1;
+    const f16* arow = ALDS ? As + (size_t)arow_m * lda + 8 * kq : A + (size_t)arow_m * K + 8 * kq;
+    f32x4 acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Straight-line over all NB register slots (no per-block branch, so the
+    // compiler cannot hoist the scale/zero unpacking of later blocks next to
+    // their loads and wait on them early); slots past this wave's nb repeat
+    // its last block with a zero scale.
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const bool live = i < nb;
+        int kb = wave + (live ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+        kb = kb < nfull ? kb : nfull - 1;
+        f16x8 a[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            a[j] = *reinterpret_cast<const f16x8*>(arow + kb * 128 + 32 * j);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            if (!G32) {
+                uint32_t zlo, zhi;
+                zero_bits((zv[i][t][0] >> zsh[t]) & 0xFu, zlo, zhi);
+                f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    part = mfma_f16(a[j], dequant_word_fast(wv[i][t][j], zlo, zhi, mlo, mhi), part);
+                const float s = live ? (float)bitcast<f16>((uint16_t)sv[i][t][0]) : 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[t][e] = __builtin_fmaf(s, part[e], acc[t][e]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t zlo, zhi;
+                    zero_bits((zv[i][t][j] >> zsh[t]) & 0xFu, zlo, zhi);
+                    const f32x4 part = mfma_f16(a[j], dequant_word_fast(wv[i][t][j], zlo, zhi, mlo, mhi),
+                                                f32x4{0.f, 0.f, 0.f, 0.f});
+                    const float s = live ? (float)bitcast<f16>((uint16_t)sv[i][t][j]) : 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[t][e] = __builtin_fmaf(s, part[e], acc[t][e]);
+                }
+            }
+        }
+        // keep block i's work in its own scheduling region: blocks then wait
+        // only for their own loads, in arrival order
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    if (G32 && (K & 127) && wave == 0) {
+        // trailing 64-k block: two 32-k groups
+        f16x8 a[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            a[j] = *reinterpret_cast<const f16x8*>(arow + nfull * 128 + 32 * j);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const u32x2 w2 = *reinterpret_cast<const u32x2*>(tbase[t] + nfull * 256 + lane * 2);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const size_t grp = (size_t)nfull * 4 + j;
+                uint32_t zlo, zhi;
+                zero_bits((Z[grp * zwords + zw[t]] >> zsh[t]) & 0xFu, zlo, zhi);
+                const f32x4 part = mfma_f16(a[j], dequant_word_fast(w2[j], zlo, zhi, mlo, mhi),
+                                            f32x4{0.f, 0.f, 0.f, 0.f});
+                const float s = (float)bitcast<f16>(S[grp * N + spos[t]]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[t][e] = __builtin_fmaf(s, part[e], acc[t][e]);
+            }
+        }
+    }
+
+    // cross-wave reduction in fixed wave order; only rows < M are written
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+        *reinterpret_cast<f32x4*>(red + (wave * T + t) * 256 + lane * 4) = acc[t];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < T * 256; idx += blockDim.x) {
+        const int l = (idx & 255) >> 2, e = idx & 3, t = idx >> 8;
+        const int m = 4 * (l >> 4) + e;
+        if (m >= M) continue;
+        float v = 0.f;
+        for (int w = 0; w < nwaves; ++w) v += red[(w * T + t) * 256 + (idx & 255)];
+        C[(size_t)m * N + (strip * T + t) * 16 + (l & 15)] = (f16)v;
+    }
+}
+
+struct GemvCfg {
+    int tiles;  // n-tiles (16 columns) per workgroup: 1 or 2
+    int waves;  // waves per workgroup, 1..16
+    int nb;     // max full 128-k blocks per wave (register budget): 1,2,4,6,8
+};
+
+constexpr size_t kGemvLdsCap = 96 * 1024;  // activations staged in LDS up to this size
+
+template <int T, int NB, bool G32>
+hipError_t launch_gemv_nb(const f16* A, const uint32_t* Wq, const uint16_t* S, const uint32_t* Z,
+                          f16* C, int M, int N, int K, int waves, hipStream_t stream) {
+    const size_t abytes = (((size_t)M * (K + 8) * 2 + 15) & ~(size_t)15);
+    const bool alds = abytes <= kGemvLdsCap;
+    const size_t lds = (alds ? abytes : 0) + (size_t)waves * T * 256 * sizeof(float);
+    if (alds)
+        hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, true>), dim3(N / (16 * T)), dim3(64 * waves),
+                           lds, stream, A, Wq, S, Z, C, M, N, K);
+    else
+        hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, false>), dim3(N / (16 * T)), dim3(64 * waves),
+                           lds, stream, A, Wq, S, Z, C, M, N, K);
+    return hipGetLastError();
+}
+
+template <int T, bool G32>
+hipError_t dispatch_nb(int nb, const f16* A, const uint32_t* Wq, const uint16_t* S,
+                       const uint32_t* Z, f16* C, int M, int N, int K, int waves,
+                       hipStream_t stream) {
+    switch (nb) {
+        case 1: return launch_gemv_nb<T, 1, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
+        case 2: return launch_gemv_nb<T, 2, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
+        case 3: return launch_gemv_nb<T, 3, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
+        case 4: return launch_gemv_nb<T, 4, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
+        case 5: return launch_gemv_nb<T, 5, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
+        case 6: return launch_gemv_nb<T, 6, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
+        default: return launch_gemv_nb<T, 8, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
+    }
+}
+
+template <bool G32>
+hipError_t dispatch_gemv(const GemvCfg& c, const f16* A, const uint32_t* Wq, const uint16_t* S,
+                         const uint32_t* Z, f16* C, int M, int N, int K, hipStream_t stream) {
+    if (c.tiles == 2) return dispatch_nb<2, G32>(c.nb, A, Wq, S, Z, C, M, N, K, c.waves, stream);
+    return dispatch_nb<1, G32>(c.nb, A, Wq, S, Z, C, M, N, K, c.waves, stream);
+}
+
+// register-slot counts with a kernel instance (slots beyond a wave's share
+// are wasted work, so the launcher picks the exact count when it can)
+int nb_bucket(int need) {
+    if (need <= 6) return need < 1 ? 1 : need;
+    return 8;
+}
+
+// Launch heuristic for M <= 16, from a sweep on MI355X at the Qwen3-8B
+// shapes (graph-timed, weights rotated through HBM): wide outputs
+// (N >= 16384) take 2 n-tiles per strip and 8 waves while M <= 4; otherwise 16
+// waves, 2 n-tiles once N >= 6144 and M >= 4 (activation fragments then feed
+// two tiles).  The register-slot count is the exact per-wave block share.
+GemvCfg default_gemv_cfg(int M, int N, int K, bool g32) {
+    GemvCfg c;
+    c.tiles = ((N >= 16384) || (N >= 6144 && M >= 4)) ? 2 : 1;
+    if (N % (16 * c.tiles)) c.tiles = 1;
+    const int nfull = K / 128 > 0 ? K / 128 : 1;
+    const int cap = g32 ? 4 : 8;
+    int waves = (N >= 16384 && M <= 4) ? 8 : 16;
+    while (waves > 1 && nfull < waves) waves /= 2;  // at least one block per wave
+    while ((nfull + waves - 1) / waves > cap && waves < 16) waves *= 2;
+    c.waves = waves;
+    c.nb = nb_bucket((nfull + waves - 1) / waves);
+    if (c.nb > cap) c.nb = cap;
+    return c;
+}
+
+bool gemv_cfg_ok(const GemvCfg& c, int M, int N, int K, bool g32) {
+    if (c.tiles != 1 && c.tiles != 2) return false;
+    if (c.waves < 1 || c.waves > 16) return false;
+    if (N % (16 * c.tiles)) return false;
+    const int nfull = K / 128;
+    if (nfull < 1 && !(g32 && K == 64)) return false;
+    const int need = (nfull + c.waves - 1) / c.waves;
+    if (need > c.nb || c.nb > (g32 ? 4 : 8)) return false;
+    if (c.nb == 7) return false;
+    (void)M;
+    return true;
+}
+
 template <int T, int MT, bool G32>
 hipError_t launch_tile_mm(const f16* A, const uint32_t* Wq, const f16* S, const uint32_t* Z, f16* C,
                           int M, int N, int K, int nwaves, hipStream_t stream) {
@@ -276,9 +584,8 @@ hipError_t dispatch_mt(int MT, int T, const f16* A, const uint32_t* Wq, const f1
     }
 }
 
-bool int4_marlin_abi_gemm(const void* a, const uint32_t* q, const void* scales,
-                          const uint32_t* zeros, void* c, int M, int N, int K, int group_size,
-                          hipStream_t stream) {
+bool int4_args_ok(const void* a, const uint32_t* q, const void* scales, const uint32_t* zeros,
+                  void* c, int M, int N, int K, int group_size) {
     if (M <= 0 || N <= 0 || K <= 0) return false;
     if (group_size != 32 && group_size != 128) return false;
     if (K % group_size != 0 || N % 64 != 0 || K % 64 != 0) return false;
@@ -286,29 +593,57 @@ bool int4_marlin_abi_gemm(const void* a, const uint32_t* q, const void* scales,
     if (!fl_aligned(a, 16) || !fl_aligned(q, 16) || !fl_aligned(c, 2) || !fl_aligned(scales, 2) ||
         !fl_aligned(zeros, 4))
         return false;
-    if (!fl_current_device_supported()) return false;
+    return fl_current_device_supported();
+}
+
+bool report(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        fprintf(stderr, "%s launch error: %s\n", what, hipGetErrorString(e));
+        return false;
+    }
+    return true;
+}
+
+// M > 16: slabs of up to 64 rows through the multi-m-tile kernel.
+bool int4_gemm_large_m(const f16* A, const uint32_t* q, const f16* S, const uint32_t* Z, f16* C,
+                       int M, int N, int K, bool g32, hipStream_t stream) {
     const int nkb = (K + 127) / 128;
-    const bool g32 = group_size == 32;
-    const f16* A = static_cast<const f16*>(a);
-    f16* Cp = static_cast<f16*>(c);
     for (int m0 = 0; m0 < M; m0 += 64) {
         const int Mc = (M - m0) < 64 ? (M - m0) : 64;
         const int MT = (Mc + 15) / 16;
-        const int T = 1;
         int nwaves = 16 / MT;
         if (nwaves > nkb) nwaves = nkb;
         if (nwaves < 1) nwaves = 1;
         const hipError_t e =
-            g32 ? dispatch_mt<true>(MT, T, A + (size_t)m0 * K, q, static_cast<const f16*>(scales),
-                                    zeros, Cp + (size_t)m0 * N, Mc, N, K, nwaves, stream)
-                : dispatch_mt<false>(MT, T, A + (size_t)m0 * K, q, static_cast<const f16*>(scales),
-                                     zeros, Cp + (size_t)m0 * N, Mc, N, K, nwaves, stream);
-        if (e != hipSuccess) {
-            fprintf(stderr, "FastllmCudaMarlinHalfInt4Gemm launch error: %s\n", hipGetErrorString(e));
-            return false;
-        }
+            g32 ? dispatch_mt<true>(MT, 1, A + (size_t)m0 * K, q, S, Z, C + (size_t)m0 * N, Mc, N,
+                                    K, nwaves, stream)
+                : dispatch_mt<false>(MT, 1, A + (size_t)m0 * K, q, S, Z, C + (size_t)m0 * N, Mc,
+                                     N, K, nwaves, stream);
+        if (!report(e, "FastllmCudaMarlinHalfInt4Gemm")) return false;
     }
     return true;
+}
+
+bool int4_marlin_abi_gemm(const void* a, const uint32_t* q, const void* scales,
+                          const uint32_t* zeros, void* c, int M, int N, int K, int group_size,
+                          hipStream_t stream, const GemvCfg* forced) {
+    if (!int4_args_ok(a, q, scales, zeros, c, M, N, K, group_size)) return false;
+    const bool g32 = group_size == 32;
+    const f16* A = static_cast<const f16*>(a);
+    f16* Cp = static_cast<f16*>(c);
+    if (M > 16)
+        return int4_gemm_large_m(A, q, static_cast<const f16*>(scales), zeros, Cp, M, N, K, g32,
+                                 stream);
+    GemvCfg cfg = forced ? *forced : default_gemv_cfg(M, N, K, g32);
+    if (!gemv_cfg_ok(cfg, M, N, K, g32)) {
+        if (forced) return false;
+        return int4_gemm_large_m(A, q, static_cast<const f16*>(scales), zeros, Cp, M, N, K, g32,
+                                 stream);
+    }
+    const uint16_t* S = static_cast<const uint16_t*>(scales);
+    const hipError_t e = g32 ? dispatch_gemv<true>(cfg, A, q, S, zeros, Cp, M, N, K, stream)
+                             : dispatch_gemv<false>(cfg, A, q, S, zeros, Cp, M, N, K, stream);
+    return report(e, "FastllmCudaMarlinHalfInt4Gemm");
 }
 
 bool int4_repack(const uint32_t* src, uint32_t* dst, int K, int N, bool inverse,
@@ -357,7 +692,7 @@ bool FastllmCudaMarlinHalfInt4Gemm(const void* a, const uint32_t* b_q_weight, co
                                    int size_k, int group_size, int* workspace) {
     (void)workspace;
     return int4_marlin_abi_gemm(a, b_q_weight, b_scales, b_zeros, c, size_m, size_n, size_k,
-                                group_size, nullptr);
+                                group_size, nullptr, nullptr);
 }
 
 bool FastllmCudaMarlinHalfInt4GemmStream(const void* a, const uint32_t* b_q_weight,
@@ -366,7 +701,16 @@ bool FastllmCudaMarlinHalfInt4GemmStream(const void* a, const uint32_t* b_q_weig
                                          int* workspace, void* stream) {
     (void)workspace;
     return int4_marlin_abi_gemm(a, b_q_weight, b_scales, b_zeros, c, size_m, size_n, size_k,
-                                group_size, (hipStream_t)stream);
+                                group_size, (hipStream_t)stream, nullptr);
+}
+
+bool fastllm_int4_gemm_config(const void* a, const uint32_t* b_q_weight, const void* b_scales,
+                              const uint32_t* b_zeros, void* c, int size_m, int size_n, int size_k,
+                              int group_size, int tiles, int waves, int nb, void* stream) {
+    GemvCfg cfg{tiles, waves, nb};
+    if (size_m > 16) return false;
+    return int4_marlin_abi_gemm(a, b_q_weight, b_scales, b_zeros, c, size_m, size_n, size_k,
+                                group_size, (hipStream_t)stream, &cfg);
 }
 
 }  // extern "C"

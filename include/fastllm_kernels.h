@@ -68,6 +68,20 @@ bool FastllmCudaMarlinHalfInt4GemmStream(const void *a,
                                          int group_size, int *workspace,
                                          void *stream);
 
+/* FastllmCudaMarlinHalfInt4GemmStream with an explicit launch configuration
+ * for size_m <= 16: `tiles` 16-column n-tiles per workgroup (1 or 2), `waves`
+ * waves per workgroup (1..16), `nb` the register budget in 128-k blocks per
+ * wave (1, 2, 4, 6 or 8; at least ceil((size_k/128)/waves); 4 at most for
+ * group 32).
+ * Returns false for configurations the shape cannot take.  No counterpart in
+ * the reference (Marlin picks its tiling internally); used to tune the
+ * default launch table. */
+bool fastllm_int4_gemm_config(const void *a, const uint32_t *b_q_weight,
+                              const void *b_scales, const uint32_t *b_zeros,
+                              void *c, int size_m, int size_n, int size_k,
+                              int group_size, int tiles, int waves, int nb,
+                              void *stream);
+
 /* Inverse of the repack: tile layout -> GPTQ u32 [size_k/8, size_n].
  * No counterpart in the reference (its repacked layout is opaque); used to
  * prove the repack is a bijection. */
