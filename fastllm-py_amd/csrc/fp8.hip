@@ -1,0 +1,374 @@
+// FP8-E4M3 weight-only GEMV/GEMM on gfx950.
+//
+// Two weight formats (reference: native/fastllm_fp8_block128.cu,
+// fastllm_py/kernels/fp8.py, fastllm_py/quantizer.py:65-94):
+//   * "inline" 1x128: every weight row is [128 codes][f32 scale] x K/128,
+//     row stride perRow = K + 4K/128 bytes; one scale per (row, 128-k block).
+//     This is the reference .so's C ABI (fastllm_fp8_block128_*).
+//   * "128x128": codes [N, K] row-major, scales f32 [ceil(N/128), ceil(K/128)]
+//     (quantize_fp8_block's format); K may end in a 64-wide block.
+//
+//   C[M, N] = A[M, K] @ dequant(W)^T (+ bias), A/C fp16 or bf16.
+//
+// Kernel: same decomposition as the INT4 GEMV (strip of T 16-row weight
+// tiles per workgroup, waves splitting the 128-k blocks, every load of a wave
+// issued up front, activations staged in LDS, fixed-order LDS reduction).  A
+// lane of the v_mfma_f32_16x16x32_{f16,bf16} B operand owns weight row
+// 16t + lane%16 and reads bytes [16q, 16q+16) and [64+16q, 64+16q+16) of each
+// 128-byte block (q = lane/16); its A fragments are taken at the same k
+// offsets, so the MFMA k order is a permutation applied to both operands.
+// e4m3 codes become fp16/bf16 exactly through v_cvt_scalef32_pk_*_fp8
+// (scale 1.0); the block scale multiplies the fp32 partial.
+#include "common.cuh"
+#include "device.cuh"
+#include "fp8_codec.cuh"
+#include "gemv_common.cuh"
+
+namespace {
+
+template <bool BF16>
+FL_DEV u32x4 fp8x8_to_16(uint32_t w0, uint32_t w1) {
+    if (BF16) {
+        return u32x4{bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
+                     bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
+                     bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
+                     bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+    } else {
+        return u32x4{bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false)),
+                     bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true)),
+                     bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false)),
+                     bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true))};
+    }
+}
+
+template <bool BF16>
+FL_DEV f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+    if (BF16) return mfma_bf16(bitcast<bf16x8>(a), bitcast<bf16x8>(b), c);
+    return mfma_f16(bitcast<f16x8>(a), bitcast<f16x8>(b), c);
+}
+
+template <bool BF16>
+FL_DEV uint16_t f32_to_act(float v) {
+    if (BF16) return bitcast<uint16_t>((__bf16)v);
+    return bitcast<uint16_t>((f16)v);
+}
+template <bool BF16>
+FL_DEV float act_to_f32(uint16_t v) {
+    if (BF16) return (float)bitcast<__bf16>(v);
+    return (float)bitcast<f16>(v);
+}
+
+// INLINE: row stride `rs` bytes, block stride 132, scale after the codes.
+// !INLINE: row stride rs (= K), block stride 128, scales [N/128, nks].
+// ALDS: activations staged in LDS (M x K small enough); otherwise MFMA A
+// fragments are read from global memory (L2) at use.
+template <int T, int NB, bool INLINE, bool BF16, bool ALDS>
+__global__ __launch_bounds__(1024) void fp8_gemv_nb(
+    const uint16_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ Sc,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int rs,
+    int nks) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int BSTRIDE = INLINE ? 132 : 128;
+    const int nwaves = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int strip = blockIdx.x;
+    const int nfull = K >> 7;
+    const int col = lane & 15;
+    const int kq = lane >> 4;
+    const int lda = K + 8;
+    uint16_t* As = reinterpret_cast<uint16_t*>(smem);
+    float* red = reinterpret_cast<float*>(smem + (ALDS ? (((size_t)M * lda * 2 + 15) & ~(size_t)15) : 0));
+
+    const int nb = wave < nfull ? (nfull - wave + nwaves - 1) / nwaves : 0;
+    const int sw = ALDS ? stage_waves(M, K) : 0;
+    const bool early = sw <= nwaves;
+    if (ALDS && early && wave < sw) stage_rows_early(A, As, M, K, lda, wave, lane);
+
+    const uint8_t* rbase[T];
+    int nrow[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int n = (strip * T + t) * 16 + col;
+        nrow[t] = n;
+        rbase[t] = W + (size_t)(n < N ? n : N - 1) * rs;
+    }
+
+    u32x4 lo[NB][T], hi[NB][T];
+    float sv[NB][T];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+        kb = kb < nfull ? kb : nfull - 1;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const uint8_t* bp = rbase[t] + (size_t)kb * BSTRIDE;
+            lo[i][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(bp + 16 * kq));
+            hi[i][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(bp + 64 + 16 * kq));
+            if (INLINE)
+                sv[i][t] = *reinterpret_cast<const float*>(bp + 128);
+            else
+                sv[i][t] = Sc[(size_t)(((strip * T + t) * 16) >> 7) * nks + kb];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (ALDS) {
+        if (!early) stage_rows_loop(A, As, M, K, lda);
+        __syncthreads();
+    }
+
+    const int arow_m = col < M ? col : M - 1;
+    const uint16_t* arow = ALDS ? As + (size_t)arow_m * lda + 16 * kq : A + (size_t)arow_m * K + 16 * kq;
+    f32x4 acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const bool live = i < nb;
+        int kb = wave + (live ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+        kb = kb < nfull ? kb : nfull - 1;
+        const uint16_t* ak = arow + kb * 128;
+        const u32x4 a0 = *reinterpret_cast<const u32x4*>(ak);
+        const u32x4 a1 = *reinterpret_cast<const u32x4*>(ak + 8);
+        const u32x4 a2 = *reinterpret_cast<const u32x4*>(ak + 64);
+        const u32x4 a3 = *reinterpret_cast<const u32x4*>(ak + 72);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+            part = mfma16<BF16>(a0, fp8x8_to_16<BF16>(lo[i][t][0], lo[i][t][1]), part);
+            part = mfma16<BF16>(a1, fp8x8_to_16<BF16>(lo[i][t][2], lo[i][t][3]), part);
+            part = mfma16<BF16>(a2, fp8x8_to_16<BF16>(hi[i][t][0], hi[i][t][1]), part);
+            part = mfma16<BF16>(a3, fp8x8_to_16<BF16>(hi[i][t][2], hi[i][t][3]), part);
+            const float s = live ? sv[i][t] : 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[t][e] = __builtin_fmaf(s, part[e], acc[t][e]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    if (!INLINE && (K & 127) && wave == 0) {
+        // trailing 64-wide block: bytes [16q, 16q+16) only
+        const uint16_t* ak = arow + nfull * 128;
+        const u32x4 a0 = *reinterpret_cast<const u32x4*>(ak);
+        const u32x4 a1 = *reinterpret_cast<const u32x4*>(ak + 8);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const uint8_t* bp = rbase[t] + (size_t)nfull * BSTRIDE;
+            const u32x4 w = *reinterpret_cast<const u32x4_a4*>(bp + 16 * kq);
+            f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+            part = mfma16<BF16>(a0, fp8x8_to_16<BF16>(w[0], w[1]), part);
+            part = mfma16<BF16>(a1, fp8x8_to_16<BF16>(w[2], w[3]), part);
+            const float s = Sc[(size_t)(((strip * T + t) * 16) >> 7) * nks + nfull];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[t][e] = __builtin_fmaf(s, part[e], acc[t][e]);
+        }
+    }
+
+    reduce_and_store<T>(red, acc, M, wave, nwaves, lane, [&](int m, int t, int c, float v) {
+        const int n = (strip * T + t) * 16 + c;
+        if (n >= N) return;
+        if (bias) v += act_to_f32<BF16>(bias[n]);
+        C[(size_t)m * N + n] = f32_to_act<BF16>(v);
+    });
+}
+
+struct Fp8Cfg {
+    int tiles, waves, nb;
+};
+
+Fp8Cfg fp8_cfg(int M, int N, int K) {
+    Fp8Cfg c;
+    const int nfull = K / 128 > 0 ? K / 128 : 1;
+    c.tiles = (N >= 8192 && N % 32 == 0) ? 2 : 1;
+    (void)M;
+    int waves = 16;
+    while (waves > 1 && nfull < waves) waves /= 2;
+    while ((nfull + waves - 1) / waves > 6 && waves < 16) waves *= 2;
+    c.waves = waves;
+    int need = (nfull + waves - 1) / waves;
+    c.nb = need <= 6 ? (need < 1 ? 1 : need) : 8;
+    return c;
+}
+
+constexpr size_t kFp8LdsCap = 96 * 1024;
+
+template <int T, int NB, bool INLINE, bool BF16>
+hipError_t launch_fp8(const uint16_t* A, const uint8_t* W, const float* Sc, const uint16_t* bias,
+                      uint16_t* C, int M, int N, int K, int rs, int nks, int waves,
+                      hipStream_t st) {
+    const size_t abytes = (((size_t)M * (K + 8) * 2 + 15) & ~(size_t)15);
+    const bool alds = abytes <= kFp8LdsCap;
+    const size_t lds = (alds ? abytes : 0) + (size_t)waves * T * 1024;
+    const int strips = (N + 16 * T - 1) / (16 * T);
+    if (alds)
+        hipLaunchKernelGGL((fp8_gemv_nb<T, NB, INLINE, BF16, true>), dim3(strips), dim3(64 * waves),
+                           lds, st, A, W, Sc, bias, C, M, N, K, rs, nks);
+    else
+        hipLaunchKernelGGL((fp8_gemv_nb<T, NB, INLINE, BF16, false>), dim3(strips),
+                           dim3(64 * waves), lds, st, A, W, Sc, bias, C, M, N, K, rs, nks);
+    return hipGetLastError();
+}
+
+template <int T, bool INLINE, bool BF16>
+hipError_t fp8_dispatch_nb(int nb, const uint16_t* A, const uint8_t* W, const float* Sc,
+                           const uint16_t* bias, uint16_t* C, int M, int N, int K, int rs, int nks,
+                           int waves, hipStream_t st) {
+    switch (nb) {
+        case 1: return launch_fp8<T, 1, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        case 2: return launch_fp8<T, 2, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        case 3: return launch_fp8<T, 3, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        case 4: return launch_fp8<T, 4, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        case 5: return launch_fp8<T, 5, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        case 6: return launch_fp8<T, 6, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        default: return launch_fp8<T, 8, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+    }
+}
+
+template <bool INLINE, bool BF16>
+hipError_t fp8_gemm(const uint16_t* A, const uint8_t* W, const float* Sc, const uint16_t* bias,
+                    uint16_t* C, int M, int N, int K, int rs, int nks, hipStream_t st) {
+    // decode-shaped kernel, 16 activation rows per launch
+    for (int m0 = 0; m0 < M; m0 += 16) {
+        const int Mc = (M - m0) < 16 ? (M - m0) : 16;
+        const Fp8Cfg c = fp8_cfg(Mc, N, K);
+        const uint16_t* Am = A + (size_t)m0 * K;
+        uint16_t* Cm = C + (size_t)m0 * N;
+        const hipError_t e =
+            c.tiles == 2
+                ? fp8_dispatch_nb<2, INLINE, BF16>(c.nb, Am, W, Sc, bias, Cm, Mc, N, K, rs, nks,
+                                                   c.waves, st)
+                : fp8_dispatch_nb<1, INLINE, BF16>(c.nb, Am, W, Sc, bias, Cm, Mc, N, K, rs, nks,
+                                                   c.waves, st);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+// ---------------------------------------------- inline 1x128 quantization
+// One wave per (row, 128-column block): scale = amax/448 (1 if not > 0), codes
+// = satfinite-RNE e4m3 of x * (1/scale) (native/fastllm_fp8_block128.cu:52-97).
+template <bool BF16>
+__global__ void fp8_inline_quantize_k(const uint16_t* __restrict__ in, uint8_t* __restrict__ out,
+                                      int rows, int cols, int packed_row_bytes) {
+    const int lane = threadIdx.x & 63;
+    const int bpr = cols / 128;
+    const long total = (long)rows * bpr;
+    for (long task = (long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); task < total;
+         task += (long)gridDim.x * (blockDim.x >> 6)) {
+        const int row = (int)(task / bpr), blk = (int)(task % bpr);
+        const uint16_t* src = in + (size_t)row * cols + blk * 128;
+        const float v0 = act_to_f32<BF16>(src[2 * lane]);
+        const float v1 = act_to_f32<BF16>(src[2 * lane + 1]);
+        float m = fmaxf(fabsf(v0), fabsf(v1));
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        float scale = m / 448.0f;
+        if (!(scale > 0.0f)) scale = 1.0f;
+        const float inv = 1.0f / scale;
+        uint8_t* dst = out + (size_t)row * packed_row_bytes + (size_t)blk * 132;
+        const uint16_t pair = (uint16_t)e4m3_encode_rne_sat(v0 * inv) |
+                              ((uint16_t)e4m3_encode_rne_sat(v1 * inv) << 8);
+        // 132-byte block stride: 2-byte stores are aligned, 4-byte ones are
+        reinterpret_cast<uint16_t*>(dst)[lane] = pair;
+        if (lane == 0) *reinterpret_cast<float*>(dst + 128) = scale;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+int fastllm_fp8_block128_packed_row_bytes(int m) { return m + (m / 128) * (int)sizeof(float); }
+
+static int fp8_inline_quantize(const void* input, void* output, int rows, int columns, int isBf16,
+                               hipStream_t st) {
+    if (!input || !output || rows <= 0 || columns <= 0 || (columns % 128) != 0) return 1;
+    if (!fl_current_device_supported()) return 2;
+    const long tasks = (long)rows * (columns / 128);
+    long grid = (tasks + 3) / 4;
+    const long cap = (long)fl_current_device_cu_count() * 32;
+    if (grid > cap) grid = cap;
+    const int prb = fastllm_fp8_block128_packed_row_bytes(columns);
+    if (isBf16)
+        hipLaunchKernelGGL(fp8_inline_quantize_k<true>, dim3((unsigned)grid), dim3(256), 0, st,
+                           (const uint16_t*)input, (uint8_t*)output, rows, columns, prb);
+    else
+        hipLaunchKernelGGL(fp8_inline_quantize_k<false>, dim3((unsigned)grid), dim3(256), 0, st,
+                           (const uint16_t*)input, (uint8_t*)output, rows, columns, prb);
+    return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+int fastllm_fp8_block128_quantize(const void* input, void* output, int rows, int columns,
+                                  int isBf16) {
+    const int rc = fp8_inline_quantize(input, output, rows, columns, isBf16, nullptr);
+    if (rc) return rc;
+    const hipError_t e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+        fprintf(stderr, "fastllm_fp8_block128_quantize kernel error: %s\n", hipGetErrorString(e));
+        return 3;
+    }
+    return 0;
+}
+
+int fastllm_fp8_block128_quantize_stream(const void* input, void* output, int rows, int columns,
+                                         int isBf16, void* stream) {
+    return fp8_inline_quantize(input, output, rows, columns, isBf16, (hipStream_t)stream);
+}
+
+static int fp8_inline_gemv(const void* A, const void* weight, void* C, const void* bias, int n,
+                           int m, int k, int perRow, int isBf16, hipStream_t st) {
+    if (n <= 0 || m <= 0 || k <= 0 || (m % 128) != 0 || !A || !weight || !C) return 1;
+    if (perRow < fastllm_fp8_block128_packed_row_bytes(m) || (perRow & 3)) return 1;
+    if (!fl_aligned(A, 16) || !fl_aligned(weight, 4)) return 1;
+    if (!fl_current_device_supported()) return 2;
+    const hipError_t e =
+        isBf16 ? fp8_gemm<true, true>((const uint16_t*)A, (const uint8_t*)weight, nullptr,
+                                      (const uint16_t*)bias, (uint16_t*)C, n, k, m, perRow, 0, st)
+               : fp8_gemm<true, false>((const uint16_t*)A, (const uint8_t*)weight, nullptr,
+                                       (const uint16_t*)bias, (uint16_t*)C, n, k, m, perRow, 0, st);
+    if (e != hipSuccess) {
+        fprintf(stderr, "fastllm_fp8_block128_gemv launch error: %s\n", hipGetErrorString(e));
+        return 2;
+    }
+    return 0;
+}
+
+int fastllm_fp8_block128_gemv_fp16(const void* A, const void* weight, void* C, const void* bias,
+                                   int n, int m, int k, int perRow) {
+    const int rc = fp8_inline_gemv(A, weight, C, bias, n, m, k, perRow, 0, nullptr);
+    if (rc) return rc;
+    const hipError_t e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+        fprintf(stderr, "fastllm_fp8_block128_gemv_fp16 kernel error: %s\n", hipGetErrorString(e));
+        return 2;
+    }
+    return 0;
+}
+
+int fastllm_fp8_block128_gemv_stream(const void* A, const void* weight, void* C, const void* bias,
+                                     int n, int m, int k, int perRow, int isBf16, void* stream) {
+    return fp8_inline_gemv(A, weight, C, bias, n, m, k, perRow, isBf16, (hipStream_t)stream);
+}
+
+int fastllm_fp8_b128x128_gemv(const void* A, const uint8_t* Wq, const float* scales,
+                              const void* bias, void* C, int M, int N, int K, int isBf16,
+                              void* stream) {
+    if (M <= 0 || N <= 0 || K <= 0 || (K % 64) != 0 || !A || !Wq || !scales || !C) return 1;
+    if (K < 128) return 1;
+    if (!fl_aligned(A, 16) || !fl_aligned(Wq, 16) || (K % 16) != 0) return 1;
+    if (!fl_current_device_supported()) return 2;
+    const int nks = (K + 127) / 128;
+    const hipError_t e =
+        isBf16 ? fp8_gemm<false, true>((const uint16_t*)A, Wq, scales, (const uint16_t*)bias,
+                                       (uint16_t*)C, M, N, K, K, nks, (hipStream_t)stream)
+               : fp8_gemm<false, false>((const uint16_t*)A, Wq, scales, (const uint16_t*)bias,
+                                        (uint16_t*)C, M, N, K, K, nks, (hipStream_t)stream);
+    if (e != hipSuccess) {
+        fprintf(stderr, "fastllm_fp8_b128x128_gemv launch error: %s\n", hipGetErrorString(e));
+        return 2;
+    }
+    return 0;
+}
+
+}  // extern "C"

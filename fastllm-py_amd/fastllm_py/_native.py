@@ -39,6 +39,13 @@ SIGNATURES: dict[str, tuple] = {
     "fastllm_fp8_e4m3_decode": (_I, [_P, _P, ctypes.c_long, _P]),
     "fastllm_quantize_fp8_block": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "fastllm_dequantize_fp8_block": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    # FP8 GEMV
+    "fastllm_fp8_block128_quantize": (_I, [_P, _P, _I, _I, _I]),
+    "fastllm_fp8_block128_quantize_stream": (_I, [_P, _P, _I, _I, _I, _P]),
+    "fastllm_fp8_block128_packed_row_bytes": (_I, [_I]),
+    "fastllm_fp8_block128_gemv_fp16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I]),
+    "fastllm_fp8_block128_gemv_stream": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "fastllm_fp8_b128x128_gemv": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
 }
 
 

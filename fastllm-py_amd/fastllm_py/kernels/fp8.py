@@ -1,0 +1,111 @@
+"""FP8-E4M3 block-scaled GEMV (small-batch decode path) on gfx950.
+
+Drop-in for the reference's ``fastllm_py/kernels/fp8.py`` (lines 1-142) with
+PyTorch-ROCm tensors as buffers.  Two weight formats:
+
+* the reference .so's interleaved inline-scale layout (``quantize`` /
+  ``fp8_gemv``): each weight row is ``[128 e4m3 codes][fp32 scale]`` repeated
+  ``m/128`` times, ``perRow = m + 4*m/128`` bytes;
+* the separate-scale 128x128 block format of ``quantizer.quantize_fp8_block``
+  (``fp8_gemv_block``), with fp16 or bf16 activations and in-features that
+  need only be a multiple of 64.
+
+GEMV semantics: ``C[n, k] = A[n, m] @ dequant(W).T`` with ``k`` output rows.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from .. import _native as nat
+
+
+def _load():
+    return nat.load()
+
+
+def available() -> bool:
+    try:
+        _load()
+        return True
+    except Exception:
+        return False
+
+
+def packed_row_bytes(m: int) -> int:
+    """Bytes per weight row in the inline layout = m + (m/128)*4 (fp8.py:68-70)."""
+    return _load().fastllm_fp8_block128_packed_row_bytes(int(m))
+
+
+def quantize(weight_fp16, is_bf16: bool = False):
+    """[k(out), m(in)] fp16/bf16 device weight -> uint8 [k, perRow] inline layout
+    (fp8.py:73-95).  m % 128 == 0.  Scale per (row, 128-block) = amax/448;
+    codes are round-to-nearest-even, saturating e4m3 of x * (1/scale)."""
+    t = nat.torch()
+    lib = _load()
+    w = nat.to_device(weight_fp16)
+    k, m = w.shape
+    if m % 128 != 0:
+        raise ValueError(f"in-features m ({m}) must be a multiple of 128")
+    want = t.bfloat16 if is_bf16 else t.float16
+    if w.dtype != want:
+        w = w.to(want)
+    per_row = packed_row_bytes(m)
+    out = t.empty((k, per_row), dtype=t.uint8, device=w.device)
+    rc = lib.fastllm_fp8_block128_quantize(nat.ptr(w), nat.ptr(out), k, m, 1 if is_bf16 else 0)
+    if rc != 0:
+        raise RuntimeError(f"fastllm_fp8_block128_quantize failed (rc={rc})")
+    return out
+
+
+def fp8_gemv(x_fp16, weight_fp8_block128, scales=None, out=None, k=None):
+    """Inline-layout FP8 GEMV/GEMM (fp8.py:98-142): fp16 [n, m] activations,
+    uint8 weight [k, perRow] (or flat with k given).  Returns fp16 [n, k]."""
+    t = nat.torch()
+    lib = _load()
+    if scales is not None:
+        raise ValueError("FP8_E4M3_BLOCK_128 stores scales inline; pass scales=None")
+    x = nat.to_device(x_fp16, t.float16)
+    n, m = x.shape
+    per_row = packed_row_bytes(m)
+    w = nat.to_device(weight_fp8_block128)
+    if w.dim() == 2:
+        k = w.shape[0]
+        if w.shape[1] != per_row:
+            raise ValueError(f"weight row bytes {w.shape[1]} != expected perRow {per_row}")
+    else:
+        if k is None:
+            raise ValueError("k must be given when weight is 1-D")
+        if w.numel() != k * per_row:
+            raise ValueError("flat weight size does not match k*perRow")
+    if out is None:
+        out = t.empty((n, k), dtype=t.float16, device=x.device)
+    rc = lib.fastllm_fp8_block128_gemv_fp16(nat.ptr(x), nat.ptr(w), nat.ptr(out), None, n, m, k,
+                                            per_row)
+    if rc != 0:
+        raise RuntimeError(f"fastllm_fp8_block128_gemv_fp16 failed (rc={rc})")
+    return out
+
+
+def fp8_gemv_block(x, q, scales, out=None, bias=None, stream=None):
+    """128x128-block FP8 GEMV: x [M, K] fp16/bf16, q uint8 [N, K], scales fp32
+    [ceil(N/128), ceil(K/128)] (quantizer.quantize_fp8_block's format).
+    Returns [M, N] in x's dtype.  K % 64 == 0, K >= 128."""
+    t = nat.torch()
+    lib = _load()
+    x = nat.to_device(x)
+    if x.dtype not in (t.float16, t.bfloat16):
+        x = x.to(t.bfloat16)
+    M, K = x.shape
+    qd = nat.to_device(q, t.uint8)
+    N = qd.shape[0]
+    sd = nat.to_device(scales, t.float32)
+    if out is None:
+        out = t.empty((M, N), dtype=x.dtype, device=x.device)
+    b = nat.to_device(bias, x.dtype) if bias is not None else None
+    h = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
+    rc = lib.fastllm_fp8_b128x128_gemv(nat.ptr(x), nat.ptr(qd), nat.ptr(sd),
+                                       nat.ptr(b) if b is not None else None, nat.ptr(out),
+                                       M, N, K, 1 if x.dtype == t.bfloat16 else 0, h)
+    if rc != 0:
+        raise RuntimeError(f"fastllm_fp8_b128x128_gemv failed (rc={rc})")
+    return out

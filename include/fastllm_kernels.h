@@ -171,6 +171,59 @@ int fastllm_dequantize_fp8_block(const uint8_t *q, const float *scales,
                                  float *out, int rows, int cols,
                                  int block_size, void *stream);
 
+/* ------------------------------------------------------------------------
+ * FP8-E4M3 block-scaled GEMV
+ * Return 0 on success, 1 on bad arguments, 2 on a device/launch error
+ * (3 for a quantize kernel error), like the reference entries.
+ * ------------------------------------------------------------------------ */
+
+/* Quantize a [rows, columns] fp16 (isBf16 == 0) or bf16 device matrix into
+ * the inline layout: per row, [128 e4m3 codes][f32 scale] x columns/128;
+ * scale = amax/448 (1 if not > 0), codes = satfinite round-to-nearest-even
+ * e4m3 of x * (1/scale).  columns % 128 == 0.  Null stream; synchronizes.
+ * Replaces: fastllm_fp8_block128_quantize, native/fastllm_fp8_block128.cu:226,
+ * bound at fastllm_py/kernels/fp8.py:45-47. */
+int fastllm_fp8_block128_quantize(const void *input, void *output, int rows,
+                                  int columns, int isBf16);
+
+/* fastllm_fp8_block128_quantize on an explicit stream, asynchronous.  No
+ * counterpart in the reference (its entry always synchronizes); for callers
+ * that capture graphs. */
+int fastllm_fp8_block128_quantize_stream(const void *input, void *output,
+                                         int rows, int columns, int isBf16,
+                                         void *stream);
+
+/* m + (m/128)*4.  Replaces: fastllm_fp8_block128_packed_row_bytes,
+ * native/fastllm_fp8_block128.cu:262, bound at fastllm_py/kernels/fp8.py:49-50. */
+int fastllm_fp8_block128_packed_row_bytes(int m);
+
+/* C[n, k] (fp16) = A[n, m] (fp16) @ dequant(W)[k, m]^T (+ bias[k] fp16).
+ * W: k rows of perRow bytes in the inline layout; m % 128 == 0; any n.
+ * Null stream; synchronizes.  Replaces: fastllm_fp8_block128_gemv_fp16,
+ * native/fastllm_fp8_block128.cu:273, bound at fastllm_py/kernels/fp8.py:52-55. */
+int fastllm_fp8_block128_gemv_fp16(const void *A, const void *weight, void *C,
+                                   const void *bias, int n, int m, int k,
+                                   int perRow);
+
+/* fastllm_fp8_block128_gemv_fp16 on an explicit stream (asynchronous), with
+ * bf16 activations/outputs/bias when isBf16 != 0.  No counterpart in the
+ * reference .so (the reference has the bf16 kernel pair only inside upstream
+ * fastllm, docs/fastllm-internals.md:597-612). */
+int fastllm_fp8_block128_gemv_stream(const void *A, const void *weight,
+                                     void *C, const void *bias, int n, int m,
+                                     int k, int perRow, int isBf16,
+                                     void *stream);
+
+/* C[M, N] = A[M, K] @ dequant(Wq)^T (+ bias[N]) for the separate-scale
+ * 128x128 block format of quantize_fp8_block: Wq u8 [N, K] row-major, scales
+ * f32 [ceil(N/128), ceil(K/128)].  A, C, bias fp16 (isBf16 == 0) or bf16.
+ * K % 64 == 0 and K >= 128 (a trailing 64-wide block is allowed); any N, M.
+ * Asynchronous on `stream`.  No counterpart in the reference's C ABI: it is
+ * the GPU consumer of fastllm_py/quantizer.py:65-94's format. */
+int fastllm_fp8_b128x128_gemv(const void *A, const uint8_t *Wq,
+                              const float *scales, const void *bias, void *C,
+                              int M, int N, int K, int isBf16, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
