@@ -9,7 +9,7 @@
 // become rint(|x| * 512) clipped to 7 (so |x| in [7.5*2^-9, 2^-6) encodes
 // 0x07, not 0x08); sign bit of the clipped fp32 copied to bit 7.
 __host__ __device__ inline uint8_t e4m3_encode_ref(float x) {
-    const float xc = fminf(fmaxf(x, -448.0f), 448.0f);
+    const float xc = x < -448.0f ? -448.0f : (x > 448.0f ? 448.0f : x);  // np.clip
     uint32_t f;
     __builtin_memcpy(&f, &xc, 4);
     const uint32_t sign = (f >> 24) & 0x80u;

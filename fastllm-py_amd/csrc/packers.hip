@@ -47,7 +47,9 @@ FL_DEV float rtn_scale(float mn, float mx) {
     return s == 0.0f ? 1.0f : s;
 }
 
-FL_DEV float clip015(float v) { return fminf(fmaxf(v, 0.0f), 15.0f); }
+// np.clip(v, 0, 15): replaces only values strictly outside the range, so a
+// -0.0 (rint of a small negative) stays -0.0 like in numpy.
+FL_DEV float clip015(float v) { return v < 0.0f ? 0.0f : (v > 15.0f ? 15.0f : v); }
 
 // ------------------------------------------------------------ A3: int4 group
 // q = clip(rint((g - wmin) / scale), 0, 15); even column in the low nibble;

@@ -46,6 +46,13 @@ SIGNATURES: dict[str, tuple] = {
     "fastllm_fp8_block128_gemv_fp16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "fastllm_fp8_block128_gemv_stream": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "fastllm_fp8_b128x128_gemv": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    # row-major INT4 / router / fused MoE
+    "fastllm_int4_rowmajor_gemv": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "fastllm_gate_matvec": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "fastllm_route_topk": (_I, [_P, _I, _I, _I, _I, _I, _F, _P, _I, _I, _P, _P, _P, _P, _P,
+                                _P, _P, _P, _P, _P, _P]),
+    "fastllm_moe_int4_fused": (_I, [_P, _I, _I, _I, _I, _I] + [_P] * 9 + [_I] + [_P] * 9 +
+                               [_P, _P, _I, _P, _I, _P, _P, _P, _I, _P, _P]),
 }
 
 

@@ -224,6 +224,82 @@ int fastllm_fp8_b128x128_gemv(const void *A, const uint8_t *Wq,
                               const float *scales, const void *bias, void *C,
                               int M, int N, int K, int isBf16, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Row-major INT4 GEMV, router, fused selective INT4 MoE
+ * (kernels the reference launches as CuPy RawKernels).  Return 0 on
+ * success, 1 on bad arguments, 2 on a device/launch error.  Asynchronous.
+ * ------------------------------------------------------------------------ */
+
+/* y[M, out_f] = x[M, in_f] @ dequant(W)^T for the row-major INT4 format
+ * (qweight u8 [out_f, in_f/2], scales/zeros fp16 [out_f, in_f/group]).
+ * x fp32 (x_fp32 = 1) or fp16, y fp32 (y_fp32 = 1) or fp16.  in_f % 128 == 0,
+ * in_f <= 16384, group in {32, 64, 128}.
+ * Replaces: gemv_int4 (fastllm_py/kernels/moe_int4.py:57-94,490-506) and
+ * dgemv (fastllm_py/graph_decode.py:170-216,748-765). */
+int fastllm_int4_rowmajor_gemv(const void *x, int x_fp32, const uint8_t *qweight,
+                               const void *scales, const void *zeros, void *y,
+                               int y_fp32, int M, int out_f, int in_f,
+                               int group_size, void *stream);
+
+/* logits[T, E] = x[T, hidden] (f32) @ gate_w[E, hidden]^T (fp16), fp32
+ * accumulate; with shared_gate_w (fp16 [hidden]) also shared_logit[T].
+ * Replaces: gate_matvec (fastllm_py/kernels/moe_int4.py:139-169) and the
+ * shared-gate matvec of fastllm_py/graph_decode.py:695-697. */
+int fastllm_gate_matvec(const float *x, const void *gate_w,
+                        const void *shared_gate_w, float *logits,
+                        float *shared_logit, int T, int E, int hidden,
+                        void *stream);
+
+/* Top-k routing of logits[T, E] (fp32), E <= 256, top_k <= 16, with numpy's
+ * float32 exp/sum arithmetic: scoring 0 = softmax, 1 = sigmoid (+ optional
+ * e_score_bias[E] on the selection value); n_group/topk_group = DeepSeek
+ * group-limited selection; norm = renormalise over the k weights (+1e-20);
+ * times routed_scaling.  Ties at the k-th value go to the lower expert index.
+ * Outputs: topk_ids/topk_w [T, top_k] (descending selection), optional dense
+ * rw [T, E]; optional shared_coef[T] = sigmoid(shared_logit); optional
+ * expert-major lists (all or none): n_active[1], active[E] ascending,
+ * offsets[E+1], tok[T*top_k] ascending within an expert, tokw[T*top_k].
+ * Replaces: route_topk (fastllm_py/expert_router.py:22-71) and
+ * _route_topk_kernel (fastllm_py/graph_decode.py:242-285). */
+int fastllm_route_topk(const float *logits, int T, int E, int top_k,
+                       int scoring, int norm, float routed_scaling,
+                       const float *e_score_bias, int n_group, int topk_group,
+                       int *topk_ids, float *topk_w, float *rw,
+                       const float *shared_logit, float *shared_coef,
+                       int *n_active, int *active, int *offsets, int *tok,
+                       float *tokw, void *stream);
+
+/* Fused selective INT4 MoE FFN for T <= 16 tokens (x fp32 [T, hidden],
+ * hidden % 128 == 0, hidden <= 2048):
+ *   y[t] = sum_s coef(s, t) * down_e(silu(gate_e x_t) * up_e x_t)
+ *          + shared_coef[t] * shared(x_t)          (y fp32 [T, hidden])
+ * over the slots s < n_active (device count) or host_active (when n_active
+ * is null) with expert ids active[s]; coef(s, t) = rw[t, active[s]] (dense
+ * rw [T, E]) or slot_coef[s, t].  Experts in the row-major INT4 stacked
+ * format: gq/gs/gz, uq/us/uz (E, inter, hidden/2 | hidden/group), dq/ds/dz
+ * (E, hidden, inter/2 | inter/group); shared expert the same with E = 1 and
+ * shared_inter (0 = none; shared_coef null = 1).  inter_buf: fp16 scratch of
+ * (max_active + 1) * T * inter_pad elements, inter_pad >= max(inter,
+ * shared_inter).  Two launches (gate/up+SwiGLU, down+combine), fixed
+ * combine order, no atomics.
+ * Replaces: fused_moe_weighted (fastllm_py/kernels/moe_int4.py:175-294),
+ * fused_moe_ffn2 (:300-396), fused_moe_ffn (:402-487) and the routed+shared
+ * part of _moe_branch (fastllm_py/graph_decode.py:688-699). */
+int fastllm_moe_int4_fused(const float *x, int T, int hidden, int group_size,
+                           int E, int inter, const uint8_t *gq, const void *gsc,
+                           const void *gz, const uint8_t *uq, const void *usc,
+                           const void *uz, const uint8_t *dq, const void *dsc,
+                           const void *dz, int shared_inter, const uint8_t *sgq,
+                           const void *sgs, const void *sgz,
+                           const uint8_t *suq, const void *sus,
+                           const void *suz, const uint8_t *sdq,
+                           const void *sds, const void *sdz,
+                           const float *shared_coef, const int *n_active,
+                           int host_active, const int *active, int max_active,
+                           const float *rw, const float *slot_coef,
+                           void *inter_buf, int inter_pad, float *y,
+                           void *stream);
+
 #ifdef __cplusplus
 }
 #endif
