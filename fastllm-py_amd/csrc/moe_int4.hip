@@ -215,7 +215,21 @@ __global__ void gate_matvec_k(const float* __restrict__ x, const uint16_t* __res
 //   (second largest + largest) selection value, others -inf;
 //   top-k by (value desc, index asc), weights p[idx], optional
 //   w / (sum(w) + 1e-20) in selection order, times `scale`.
-// Up to 256 experts (4 per lane), k <= 32.
+// Up to 256 experts (4 per lane), k <= 16.
+//
+// Expert-major lists ("MoE lists"), consumed by the fused MoE kernels:
+//   n_active; active[s] expert of slot s; offsets[s..s+1] its entries;
+//   tok/tokw[p] token and weight of entry p (tokens ascending within a slot).
+constexpr int kMaxTopK = 16;
+
+struct MoeLists {
+    int* n_active;
+    int* active;
+    int* offsets;
+    int* tok;
+    float* tokw;
+};
+
 struct RouteArgs {
     const float* logits;
     const float* bias;
@@ -224,333 +238,461 @@ struct RouteArgs {
     float scale;
     int* topk_ids;
     float* topk_w;
-    float* rw;     // dense [T, E], optional
-    float* scoef;  // sigmoid(slogit) [T], optional
-    // expert-major lists (filled when the whole batch is one workgroup)
-    int* n_active;
-    int* active;
-    int* offsets;
-    int* tok;
-    float* tokw;
+    float* rw;       // dense [T, E], optional
+    float* scoef;    // sigmoid(slogit) [T], optional
+    MoeLists lists;  // built by route_k itself when the batch is one workgroup
 };
 
-__global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
-    __shared__ float ex[16][256];
-    __shared__ int cnt[256];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    const int t = blockIdx.x * (blockDim.x >> 6) + wv;
-    const int E = a.E;
-    if (t < a.T) {
-        float sel[4], p[4];
-        const float* s = a.logits + (size_t)t * E;
-        if (a.scoring == 0) {
-            float m = -__builtin_inff();
+// MoE lists from T*K routed entries (ids/ws token-major; each token's K
+// experts distinct, all < E <= 256).  One workgroup of >= 64 threads; the
+// first wave scans the expert counts, entries are placed with a stable
+// counting sort in chunks of blockDim.x.  cnt/base: E ints of LDS, chunk:
+// blockDim.x ints of LDS.
+FL_DEV void build_lists(const int* ids, const float* ws, int T, int K, int E, MoeLists L,
+                        int* cnt, int* base, int* chunk) {
+    const int TK = T * K;
+    const int tid = threadIdx.x, bd = blockDim.x;
+    for (int e = tid; e < E; e += bd) cnt[e] = 0;
+    __syncthreads();
+    for (int i = tid; i < TK; i += bd) atomicAdd(&cnt[ids[i]], 1);
+    __syncthreads();
+    if (tid < 64) {
+        int c[4], tot = 0, act = 0;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = lane + 64 * c;
-                if (e < E) m = fmaxf(m, s[e]);
-            }
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * tid + q;
+            c[q] = e < E ? cnt[e] : 0;
+            tot += c[q];
+            act += c[q] > 0 ? 1 : 0;
+        }
+        int it = tot, ia = act;
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = lane + 64 * c;
-                if (e < E) ex[wv][e] = np_expf(s[e] - m);
-            }
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            float z = 0.f;
-            if (lane == 0) z = np_sum_f32(ex[wv], E);
-            z = __shfl(z, 0, 64);
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = lane + 64 * c;
-                p[c] = (e < E) ? ex[wv][e] / z : 0.f;
-                sel[c] = (e < E) ? p[c] : -__builtin_inff();
-            }
-        } else {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = lane + 64 * c;
-                if (e < E) {
-                    const float d = 1.0f + np_expf(-s[e]);
-                    p[c] = 1.0f / d;
-                    sel[c] = a.bias ? p[c] + a.bias[e] : p[c] + 0.0f;
-                } else {
-                    p[c] = 0.f;
-                    sel[c] = -__builtin_inff();
-                }
+        for (int o = 1; o < 64; o <<= 1) {
+            const int vt = __shfl_up(it, o, 64), va = __shfl_up(ia, o, 64);
+            if (tid >= o) {
+                it += vt;
+                ia += va;
             }
         }
-        if (a.n_group > 1 && a.topk_group > 0 && a.topk_group < a.n_group) {
-            const int gsz = E / a.n_group;
+        int off = it - tot, na = ia - act;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = lane + 64 * c;
-                if (e < E) ex[wv][e] = sel[c];
-            }
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            // lane g scores group g: second largest + largest (ascending sum)
-            float gscore = -__builtin_inff();
-            if (lane < a.n_group) {
-                float b1 = -__builtin_inff(), b2 = -__builtin_inff();
-                for (int i = 0; i < gsz; ++i) {
-                    const float v = ex[wv][lane * gsz + i];
-                    if (v > b1) {
-                        b2 = b1;
-                        b1 = v;
-                    } else if (v > b2) {
-                        b2 = v;
-                    }
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * tid + q;
+            if (e < E) {
+                base[e] = off;
+                if (c[q] > 0) {
+                    L.active[na] = e;
+                    L.offsets[na] = off;
+                    ++na;
                 }
-                gscore = gsz >= 2 ? (0.0f + b2) + b1 : 0.0f + b1;
-            }
-            // keep topk_group groups: rank = #groups strictly better (ties -> lower index)
-            int rank = 0;
-            for (int g2 = 0; g2 < a.n_group; ++g2) {
-                const float o = __shfl(gscore, g2, 64);
-                rank += (o > gscore || (o == gscore && g2 < lane)) ? 1 : 0;
-            }
-            const int keep = (lane < a.n_group && rank < a.topk_group) ? 1 : 0;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = lane + 64 * c;
-                if (e < E) {
-                    const int kg = __shfl(keep, e / gsz, 64);
-                    if (!kg) sel[c] = -__builtin_inff();
-                }
+                off += c[q];
             }
         }
-        // top-k: value desc, index asc
-        int ids[16];
-        float ws[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            ids[i] = 0;
-            ws[i] = 0.f;
-            if (i >= a.K) continue;
-            float bv = -__builtin_inff();
-            int bi = 0x7fffffff;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = lane + 64 * c;
-                if (e < E && (sel[c] > bv || (sel[c] == bv && e < bi))) {
-                    bv = sel[c];
-                    bi = e;
-                }
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o, 64);
-                const int oi = __shfl_xor(bi, o, 64);
-                if (ov > bv || (ov == bv && oi < bi)) {
-                    bv = ov;
-                    bi = oi;
-                }
-            }
-            ids[i] = bi;
-            float pw = 0.f;
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = lane + 64 * c;
-                if (e == bi) {
-                    pw = p[c];
-                    sel[c] = -__builtin_inff();
-                }
-            }
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) pw += __shfl_xor(pw, o, 64);  // single nonzero lane
-            ws[i] = pw;
+        if (tid == 63) {
+            L.offsets[ia] = it;
+            *L.n_active = ia;
         }
-        if (a.norm) {
-            // numpy row sum of the k weights (selection order), + 1e-20
-            float den;
-            if (a.K < 8) {
-                den = 0.0f;
+    }
+    __syncthreads();
+    for (int c0 = 0; c0 < TK; c0 += bd) {
+        const int i = c0 + tid;
+        const int e = i < TK ? ids[i] : -1;
+        chunk[tid] = e;
+        __syncthreads();
+        if (i < TK) {
+            int r = 0;
+            for (int j = 0; j < tid; ++j) r += (chunk[j] == e) ? 1 : 0;
+            const int p = base[e] + r;
+            L.tok[p] = i / K;
+            L.tokw[p] = ws[i];
+        }
+        __syncthreads();
+        if (i < TK) atomicAdd(&base[e], 1);
+        __syncthreads();
+    }
+}
+
+// Route token t with one wave.  `exw` is the wave's 256-float LDS row;
+// lane i < K ends with the i-th selection (expert `my_id`, final weight
+// `my_w`), which it also stores to topk_ids/topk_w and to sids/sws[tl*K + i].
+FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw, int* sids,
+                        float* sws) {
+    const int E = a.E, K = a.K;
+    float sel[4], p[4];
+    const float* s = a.logits + (size_t)t * E;
+    if (a.scoring == 0) {
+        float m = -__builtin_inff();
 #pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    if (i < a.K) den += ws[i];
+        for (int c = 0; c < 4; ++c) {
+            const int e = lane + 64 * c;
+            if (e < E) m = fmaxf(m, s[e]);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int e = lane + 64 * c;
+            if (e < E) exw[e] = np_expf(s[e] - m);
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        const float z = np_sum_wave(exw, E, lane);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int e = lane + 64 * c;
+            p[c] = (e < E) ? exw[e] / z : 0.f;
+            sel[c] = (e < E) ? p[c] : -__builtin_inff();
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int e = lane + 64 * c;
+            if (e < E) {
+                const float d = 1.0f + np_expf(-s[e]);
+                p[c] = 1.0f / d;
+                sel[c] = a.bias ? p[c] + a.bias[e] : p[c] + 0.0f;
             } else {
-                // 8 accumulators, one more round of 8 when k == 16, then the
-                // leftover elements one by one (numpy's pairwise block)
-                float r[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) r[j] = ws[j];
-                if (a.K == 16) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) r[j] += ws[8 + j];
-                }
-                den = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-#pragma unroll
-                for (int i = 8; i < 16; ++i)
-                    if (i < a.K && a.K < 16) den += ws[i];
-            }
-            den = den + 1e-20f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) ws[i] = ws[i] / den;
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) ws[i] = ws[i] * a.scale;
-        if (lane == 0) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                if (i >= a.K) continue;
-                a.topk_ids[(size_t)t * a.K + i] = ids[i];
-                a.topk_w[(size_t)t * a.K + i] = ws[i];
-            }
-            if (a.scoef && a.slogit) a.scoef[t] = 1.0f / (1.0f + expf(-a.slogit[t]));
-        }
-        if (a.rw) {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = lane + 64 * c;
-                if (e < E) {
-                    float w = 0.f;
-#pragma unroll
-                    for (int i = 0; i < 16; ++i)
-                        if (i < a.K && ids[i] == e) w = ws[i];
-                    a.rw[(size_t)t * E + e] = w;
-                }
+                p[c] = 0.f;
+                sel[c] = -__builtin_inff();
             }
         }
     }
-    if (gridDim.x == 1 && a.n_active) {
-        // expert-major lists: experts ascending, tokens ascending within one
-        __syncthreads();
-        __threadfence_block();
-        const int TK = a.T * a.K;
-        for (int e = threadIdx.x; e < E; e += blockDim.x) {
-            int c = 0;
-            for (int i = 0; i < TK; ++i) c += (a.topk_ids[i] == e) ? 1 : 0;
-            cnt[e] = c;
+    if (a.n_group > 1 && a.topk_group > 0 && a.topk_group < a.n_group) {
+        const int gsz = E / a.n_group;
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int e = lane + 64 * c;
+            if (e < E) exw[e] = sel[c];
         }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            int na = 0, off = 0;
-            for (int e = 0; e < E; ++e) {
-                if (cnt[e] > 0) {
-                    a.active[na] = e;
-                    a.offsets[na] = off;
-                    off += cnt[e];
-                    cnt[e] = na;  // slot of expert e
-                    ++na;
-                } else {
-                    cnt[e] = -1;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        // lane g scores group g: second largest + largest (numpy sums the
+        // ascending top-2)
+        float gscore = -__builtin_inff();
+        if (lane < a.n_group) {
+            float b1 = -__builtin_inff(), b2 = -__builtin_inff();
+            for (int i = 0; i < gsz; ++i) {
+                const float v = exw[lane * gsz + i];
+                if (v > b1) {
+                    b2 = b1;
+                    b1 = v;
+                } else if (v > b2) {
+                    b2 = v;
                 }
             }
-            a.offsets[na] = off;
-            *a.n_active = na;
+            gscore = gsz >= 2 ? (0.0f + b2) + b1 : 0.0f + b1;
         }
-        __syncthreads();
-        for (int e = threadIdx.x; e < E; e += blockDim.x) {
-            const int slot = cnt[e];
-            if (slot < 0) continue;
-            int w = a.offsets[slot];
-            for (int tt = 0; tt < a.T; ++tt)
-                for (int i = 0; i < a.K; ++i)
-                    if (a.topk_ids[(size_t)tt * a.K + i] == e) {
-                        a.tok[w] = tt;
-                        a.tokw[w] = a.topk_w[(size_t)tt * a.K + i];
-                        ++w;
-                    }
+        // keep topk_group groups: rank = #groups strictly better (ties -> lower index)
+        int rank = 0;
+        for (int g2 = 0; g2 < a.n_group; ++g2) {
+            const float o = __shfl(gscore, g2, 64);
+            rank += (o > gscore || (o == gscore && g2 < lane)) ? 1 : 0;
+        }
+        const int keep = (lane < a.n_group && rank < a.topk_group) ? 1 : 0;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int e = lane + 64 * c;
+            const int kg = __shfl(keep, e < E ? e / gsz : 0, 64);
+            if (e < E && !kg) sel[c] = -__builtin_inff();
+        }
+    }
+    // top-k by (value desc, index asc); lane i keeps the i-th pick
+    int my_id = 0;
+    float my_w = 0.f;
+    for (int i = 0; i < K; ++i) {
+        float bv = -__builtin_inff();
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int e = lane + 64 * c;
+            if (e < E && (sel[c] > bv || (sel[c] == bv && e < bi))) {
+                bv = sel[c];
+                bi = e;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        bi = __builtin_amdgcn_readfirstlane(bi);
+        const int bc = bi >> 6;
+        const float pc = bc == 0 ? p[0] : (bc == 1 ? p[1] : (bc == 2 ? p[2] : p[3]));
+        const float pw = __shfl(pc, bi & 63, 64);
+        if (lane == (bi & 63)) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (c == bc) sel[c] = -__builtin_inff();
+        }
+        if (lane == i) {
+            my_id = bi;
+            my_w = pw;
+        }
+    }
+    if (a.norm) {
+        // numpy row sum of the k weights (selection order), + 1e-20: below 8
+        // a plain loop; else 8 accumulators (a second round of 8 when
+        // k == 16), their tree, then the leftovers one by one
+        float den;
+        if (K < 8) {
+            den = 0.0f;
+            for (int i = 0; i < K; ++i) den += __shfl(my_w, i, 64);
+        } else {
+            float r[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) r[j] = __shfl(my_w, j, 64);
+            if (K == 16) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) r[j] += __shfl(my_w, 8 + j, 64);
+            }
+            den = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+            if (K < 16)
+                for (int i = 8; i < K; ++i) den += __shfl(my_w, i, 64);
+        }
+        den = den + 1e-20f;
+        my_w = my_w / den;
+    }
+    my_w = my_w * a.scale;
+    if (lane < K) {
+        a.topk_ids[(size_t)t * K + lane] = my_id;
+        a.topk_w[(size_t)t * K + lane] = my_w;
+        sids[tl * K + lane] = my_id;
+        sws[tl * K + lane] = my_w;
+    }
+    if (lane == 0 && a.scoef && a.slogit) a.scoef[t] = 1.0f / (1.0f + expf(-a.slogit[t]));
+    if (a.rw) {
+        float w[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < K; ++i) {
+            const int id = __builtin_amdgcn_readfirstlane(__shfl(my_id, i, 64));
+            const float wi = __shfl(my_w, i, 64);
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (lane + 64 * c == id) w[c] = wi;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int e = lane + 64 * c;
+            if (e < E) a.rw[(size_t)t * E + e] = w[c];
         }
     }
 }
 
-// Expert-major lists for batches routed by several workgroups (same layout
-// as the single-workgroup path above).
+// One wave per token, 16 tokens per workgroup; the batch of one workgroup
+// also builds the MoE lists.
+__global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
+    __shared__ float ex[16][256];
+    __shared__ int sids[16 * kMaxTopK];
+    __shared__ float sws[16 * kMaxTopK];
+    __shared__ int cnt[256];
+    __shared__ int base[256];
+    __shared__ int chunk[1024];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = blockDim.x >> 6;
+    for (int tl = wv; tl < 16; tl += nw) {
+        const int t = blockIdx.x * 16 + tl;
+        if (t >= a.T) break;
+        route_token(a, t, tl, lane, ex[wv], sids, sws);
+    }
+    if (gridDim.x == 1 && a.lists.n_active) {
+        __syncthreads();
+        build_lists(sids, sws, a.T, a.K, a.E, a.lists, cnt, base, chunk);
+    }
+}
+
+// MoE lists for batches routed by several workgroups (entries read from the
+// router's topk_ids / topk_w).
 __global__ __launch_bounds__(1024) void route_lists_k(const int* __restrict__ ids,
                                                       const float* __restrict__ tw, int T, int K,
-                                                      int E, int* n_active, int* active,
-                                                      int* offsets, int* tok, float* tokw) {
-    __shared__ int cnt[1024];
-    const int TK = T * K;
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+                                                      int E, MoeLists L) {
+    __shared__ int cnt[256];
+    __shared__ int base[256];
+    __shared__ int chunk[1024];
+    build_lists(ids, tw, T, K, E, L, cnt, base, chunk);
+}
+
+// MoE lists from an explicit slot list: slot s is expert cand[s] (or s when
+// cand is null); token t is routed to it with weight rw[t, expert] (dense
+// weights) or coef[s, t] (per-slot weights) when that weight is nonzero.
+// Slots keep the given order; slots without tokens, or whose expert is
+// outside [0, E), are dropped.  T <= 16, S <= 256, one workgroup of 256.
+__global__ __launch_bounds__(256) void slot_lists_k(const float* __restrict__ rw,
+                                                    const float* __restrict__ coef,
+                                                    const int* __restrict__ cand, int T, int E,
+                                                    int S, MoeLists L) {
+    __shared__ int start[256];
+    const int s = threadIdx.x;
+    int e = -1;
+    if (s < S) {
+        e = cand ? cand[s] : s;
+        if (e < 0 || e >= E) e = -1;
         int c = 0;
-        for (int i = 0; i < TK; ++i) c += (ids[i] == e) ? 1 : 0;
-        cnt[e] = c;
+        if (e >= 0)
+            for (int t = 0; t < T; ++t) {
+                const float w = coef ? coef[(size_t)s * T + t] : rw[(size_t)t * E + e];
+                c += (w != 0.0f) ? 1 : 0;
+            }
+        start[s] = c;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         int na = 0, off = 0;
-        for (int e = 0; e < E; ++e) {
-            if (cnt[e] > 0) {
-                active[na] = e;
-                offsets[na] = off;
-                off += cnt[e];
-                cnt[e] = na;
+        for (int q = 0; q < S; ++q) {
+            const int c = start[q];
+            if (c > 0) {
+                L.active[na] = cand ? cand[q] : q;
+                L.offsets[na] = off;
+                start[q] = off;
+                off += c;
                 ++na;
             } else {
-                cnt[e] = -1;
+                start[q] = -1;
             }
         }
-        offsets[na] = off;
-        *n_active = na;
+        L.offsets[na] = off;
+        *L.n_active = na;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        const int slot = cnt[e];
-        if (slot < 0) continue;
-        int w = offsets[slot];
-        for (int tt = 0; tt < T; ++tt)
-            for (int i = 0; i < K; ++i)
-                if (ids[(size_t)tt * K + i] == e) {
-                    tok[w] = tt;
-                    tokw[w] = tw[(size_t)tt * K + i];
-                    ++w;
-                }
+    if (s < S && start[s] >= 0) {
+        int p = start[s];
+        for (int t = 0; t < T; ++t) {
+            const float w = coef ? coef[(size_t)s * T + t] : rw[(size_t)t * E + e];
+            if (w != 0.0f) {
+                L.tok[p] = t;
+                L.tokw[p] = w;
+                ++p;
+            }
+        }
     }
 }
 
 // ------------------------------------------------------- fused MoE layer
-// Expert set description shared by the two MoE kernels.
+// Stacked-expert tile layout (this library's device layout for the fused MoE;
+// build_stacked_experts produces it from the row-major format):
+//   qtile (rows/16, in/128, 1024) u8: block (R/16, kb) holds, at byte
+//     16 * (c + 16 * q), the 16 row-major bytes [64 kb + 16 q, +16) of row
+//     16 (R/16) + c -- what MFMA B-lane c + 16 q dequantizes -- so one wave
+//     load reads a whole 1 KB block;
+//   sz (rows/16, in/gs, 16) u32: scale bits | zero bits << 16 of row
+//     16 (R/16) + c, group g, at [R/16][g][c].
+// Rows of all experts are stacked (R = e * out + r); out % 16 == 0.
+__global__ void moe_tile_repack_k(const uint8_t* __restrict__ q, const uint16_t* __restrict__ s,
+                                  const uint16_t* __restrict__ z, uint8_t* __restrict__ qt,
+                                  uint32_t* __restrict__ sz, long rows, int in_f, int G) {
+    const long stride = (long)gridDim.x * blockDim.x;
+    const int cpr = in_f / 32;  // 16-byte chunks per row
+    const long nchunk = rows * cpr;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nchunk; i += stride) {
+        const long R = i / cpr;
+        const int c = (int)(i - R * cpr), kb = c >> 2, kq = c & 3;
+        const long dst = ((R >> 4) * (in_f / 128) + kb) * 1024 + ((R & 15) + 16 * kq) * 16;
+        *reinterpret_cast<u32x4*>(qt + dst) = *reinterpret_cast<const u32x4*>(q + R * (in_f / 2) + c * 16);
+    }
+    const long nsz = rows * G;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nsz; i += stride) {
+        const long R = i / G;
+        const int g = (int)(i - R * G);
+        sz[((R >> 4) * G + g) * 16 + (R & 15)] = (uint32_t)s[i] | ((uint32_t)z[i] << 16);
+    }
+}
+
+__global__ void moe_tile_unpack_k(const uint8_t* __restrict__ qt, const uint32_t* __restrict__ sz,
+                                  uint8_t* __restrict__ q, uint16_t* __restrict__ s,
+                                  uint16_t* __restrict__ z, long rows, int in_f, int G) {
+    const long stride = (long)gridDim.x * blockDim.x;
+    const int cpr = in_f / 32;
+    const long nchunk = rows * cpr;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nchunk; i += stride) {
+        const long R = i / cpr;
+        const int c = (int)(i - R * cpr), kb = c >> 2, kq = c & 3;
+        const long src = ((R >> 4) * (in_f / 128) + kb) * 1024 + ((R & 15) + 16 * kq) * 16;
+        *reinterpret_cast<u32x4*>(q + R * (in_f / 2) + c * 16) = *reinterpret_cast<const u32x4*>(qt + src);
+    }
+    const long nsz = rows * G;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nsz; i += stride) {
+        const long R = i / G;
+        const int g = (int)(i - R * G);
+        const uint32_t v = sz[((R >> 4) * G + g) * 16 + (R & 15)];
+        s[i] = (uint16_t)(v & 0xFFFFu);
+        z[i] = (uint16_t)(v >> 16);
+    }
+}
+
+// Expert set in the tile layout, shared by the two MoE kernels.
 struct MoeExperts {
-    const uint8_t* gq;  // gate qweight (E, inter, hidden/2)
-    const uint16_t* gs_;
-    const uint16_t* gz;
-    const uint8_t* uq;  // up
-    const uint16_t* us;
-    const uint16_t* uz;
-    const uint8_t* dq;  // down qweight (E, hidden, inter/2)
-    const uint16_t* ds;
-    const uint16_t* dz;
+    const uint8_t* gq;    // gate (E * inter / 16, hidden / 128, 1024)
+    const uint32_t* gsz;  // gate (E * inter / 16, hidden / gs, 16)
+    const uint8_t* uq;    // up, as gate
+    const uint32_t* usz;
+    const uint8_t* dq;    // down (E * hidden / 16, inter / 128, 1024)
+    const uint32_t* dsz;  // down (E * hidden / 16, inter / gs, 16)
     int inter;
 };
 
+// inter_buf (caller workspace) fp16 [max_entries + T][inter_pad] holds
+// silu(g) * u * w per list entry and, from row max_entries, per token of the
+// shared expert.  y is zeroed by the gate/up kernel and accumulated by the
+// down kernel with fp32 atomics.
 struct MoeArgs {
     const float* x;  // (T, hidden) fp32
-    int T, hidden, gs;
+    int T, hidden, gs, E;
     MoeExperts routed, shared;
-    int has_shared;
-    int E;
-    const int* n_active;  // device count of active slots (or null: host_active)
-    int host_active;
-    const int* active;    // expert id per slot
-    const float* rw;      // dense (T, E) weights (coef_mode 0)
-    const float* coef;    // per-slot (S, T) weights (coef_mode 1)
-    int coef_mode;
-    const float* scoef;   // shared-expert per-token coefficient (T), or null (1.0)
-    int max_active;       // slots reserved in inter_buf before the shared slot
-    int inter_pad;
-    uint16_t* inter_buf;  // fp16 (max_active + has_shared, T, inter_pad)
-    float* y;             // (T, hidden) fp32
+    int has_shared, pieces;  // shared-expert down projection split into `pieces` K ranges
+    const float* scoef;      // shared-expert per-token coefficient (T), or null (1.0)
+    const int* n_active;
+    const int* active;
+    const int* offsets;
+    const int* tok;
+    const float* tokw;
+    int max_slots, max_entries, inter_pad;
+    uint16_t* inter_buf;
+    float* y;  // (T, hidden) fp32
 };
 
-FL_DEV int moe_n_active(const MoeArgs& a) {
-    return a.n_active ? __builtin_amdgcn_readfirstlane(*a.n_active) : a.host_active;
+constexpr int kGuTiles = 2;  // 16-row tiles of gate and of up per workgroup
+
+FL_DEV int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+// Slot `slot` of the lists: expert, first entry and entry count (clamped to
+// the workspace); false when the slot is at or past n_active.  The four index
+// loads issue together.
+FL_DEV bool moe_slot(const MoeArgs& a, int slot, int& e, int& row0, int& M) {
+    const int na = __builtin_amdgcn_readfirstlane(*a.n_active);
+    const int ee = __builtin_amdgcn_readfirstlane(a.active[slot]);
+    const int r0 = __builtin_amdgcn_readfirstlane(a.offsets[slot]);
+    const int r1 = __builtin_amdgcn_readfirstlane(a.offsets[slot + 1]);
+    if (slot >= clampi(na, 0, a.max_slots)) return false;
+    e = clampi(ee, 0, a.E - 1);
+    row0 = clampi(r0, 0, a.max_entries);
+    const int end = clampi(r1, row0, a.max_entries);
+    M = end - row0 < a.T ? end - row0 : a.T;
+    return true;
 }
 
-FL_DEV float moe_coef(const MoeArgs& a, int slot, int e, int t) {
-    return a.coef_mode == 0 ? a.rw[(size_t)t * a.E + e] : a.coef[(size_t)slot * a.T + t];
+// 128-k block handled by wave `wave` at step i.  With an even NB a wave takes
+// adjacent block pairs; blocks [0, nwaves * NB) are covered once either way.
+template <int NB>
+FL_DEV int moe_kb(int wave, int i, int nwaves) {
+    return (NB % 2 == 0) ? 2 * (wave + (i >> 1) * nwaves) + (i & 1) : wave + i * nwaves;
 }
 
-// gate/up for one 16-row tile of one expert slot: h = silu(g) * u * coef,
-// stored fp16 in inter_buf.  Workgroup = 8 waves splitting hidden blocks.
-template <bool G128>
+FL_DEV uint16_t sz_scale(uint32_t v) { return (uint16_t)(v & 0xFFFFu); }
+FL_DEV uint16_t sz_zero(uint32_t v) { return (uint16_t)(v >> 16); }
+
+// gate/up for kGuTiles 16-row tiles of one slot's expert over only the tokens
+// routed to it: h = silu(x Wg^T) * (x Wu^T) * w, stored fp16 in inter_buf.
+// The waves split the hidden (K) blocks, NB each; every weight load of a wave
+// (one 1 KB block per load) is issued before the token rows are gathered
+// into LDS.  Workgroup 0 also zeroes y for the down kernel's accumulation.
+template <bool G128, int NB>
 __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    constexpr int NB = 2;  // hidden blocks per wave and matrix (hidden <= 8 waves * 2 * 128)
+    constexpr int TR = kGuTiles;
     const int nwaves = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -558,40 +700,58 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
     const int K = a.hidden;
     const int nfull = K >> 7;
     const int lda = K + 8;
-    const int M = a.T;
 
-    // which slot / tile
-    const int tiles_r = a.routed.inter / 16;
-    int slot, tile;
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < a.T * a.hidden / 4; i += blockDim.x)
+            reinterpret_cast<f32x4*>(a.y)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int groups_r = a.routed.inter / (16 * TR);
+    int slot, grp, e = 0, M = 0, row0 = 0;
     const MoeExperts* ex;
-    int e = 0;
     const int b = blockIdx.x;
-    if (b < a.max_active * tiles_r) {
-        slot = b / tiles_r;
-        tile = b % tiles_r;
-        if (slot >= moe_n_active(a)) return;
-        e = a.active[slot];
+    if (b < a.max_slots * groups_r) {
+        slot = b / groups_r;
+        grp = b - slot * groups_r;
+        if (!moe_slot(a, slot, e, row0, M)) return;
         ex = &a.routed;
     } else {
         if (!a.has_shared) return;
-        slot = a.max_active;
-        tile = b - a.max_active * tiles_r;
+        slot = -1;
+        grp = b - a.max_slots * groups_r;
+        row0 = a.max_entries;
+        M = a.T;
         ex = &a.shared;
     }
-    const int inter = ex->inter;
+    if (M <= 0) return;
     const int G = K / a.gs;
-    const size_t wbase = (size_t)e * inter * (K / 2);
-    const size_t sbase = (size_t)e * inter * G;
+    const size_t tb0 = (size_t)e * (ex->inter / 16) + (size_t)grp * TR;  // first row tile
 
+    u32x4 wg[NB][TR], wu[NB][TR];
+    uint32_t szg[NB][TR], szu[NB][TR];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        int kb = moe_kb<NB>(wave, i, nwaves);
+        kb = kb < nfull ? kb : nfull - 1;
+        const int g = (kb * 128 + 32 * kq) / a.gs;
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            const size_t off = ((tb0 + r) * nfull + kb) * 1024 + lane * 16;
+            wg[i][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ex->gq + off));
+            wu[i][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ex->uq + off));
+            const size_t so = ((tb0 + r) * G + g) * 16 + col;
+            szg[i][r] = ex->gsz[so];
+            szu[i][r] = ex->usz[so];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // gather this slot's token rows (fp32 -> fp16)
     f16* As = reinterpret_cast<f16*>(smem);
-    float* red = reinterpret_cast<float*>(smem + (((size_t)M * lda * 2 + 15) & ~(size_t)15));
-    // stage x as fp16
     {
         const int k8 = K >> 3;
-        const int nchunks = M * k8;
-        for (int c = threadIdx.x; c < nchunks; c += blockDim.x) {
-            const int m = c / k8, c8 = c - m * k8;
-            const float* src = a.x + (size_t)m * K + c8 * 8;
+        for (int c = threadIdx.x; c < M * k8; c += blockDim.x) {
+            const int j = c / k8, c8 = c - j * k8;
+            const int tkn = slot >= 0 ? clampi(a.tok[row0 + j], 0, a.T - 1) : j;
+            const float* src = a.x + (size_t)tkn * K + c8 * 8;
             const f32x4 lo = *reinterpret_cast<const f32x4*>(src);
             const f32x4 hi = *reinterpret_cast<const f32x4*>(src + 4);
             f16x8 v;
@@ -600,131 +760,137 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
                 v[q] = (f16)lo[q];
                 v[4 + q] = (f16)hi[q];
             }
-            *reinterpret_cast<f16x8*>(As + (size_t)m * lda + c8 * 8) = v;
+            *reinterpret_cast<f16x8*>(As + (size_t)j * lda + c8 * 8) = v;
         }
     }
-
-    const int row = tile * 16 + col;
-    const int nb = wave < nfull ? (nfull - wave + nwaves - 1) / nwaves : 0;
-    u32x4 wg[NB], wu[NB];
-    uint16_t sg[NB], zg[NB], su[NB], zu[NB];
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-        int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
-        kb = kb < nfull ? kb : nfull - 1;
-        const size_t off = wbase + (size_t)row * (K / 2) + kb * 64 + 16 * kq;
-        wg[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ex->gq + off));
-        wu[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ex->uq + off));
-        const size_t so = sbase + (size_t)row * G + (kb * 128 + 32 * kq) / a.gs;
-        sg[i] = ex->gs_[so];
-        zg[i] = ex->gz[so];
-        su[i] = ex->us[so];
-        zu[i] = ex->uz[so];
-    }
-    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
 
     const f16* arow = As + (size_t)(col < M ? col : M - 1) * lda + 32 * kq;
-    f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+    f32x4 acc[2 * TR];
+#pragma unroll
+    for (int r = 0; r < 2 * TR; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-        const bool live = i < nb;
-        int kb = wave + (live ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+        int kb = moe_kb<NB>(wave, i, nwaves);
+        const float live = kb < nfull ? 1.0f : 0.0f;
         kb = kb < nfull ? kb : nfull - 1;
         u32x4 av[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) av[j] = *reinterpret_cast<const u32x4*>(arow + kb * 128 + 8 * j);
-        rm_block_mma<G128>(acc[0], av, wg[i], sg[i], zg[i], live ? 1.0f : 0.0f);
-        rm_block_mma<G128>(acc[1], av, wu[i], su[i], zu[i], live ? 1.0f : 0.0f);
+#pragma unroll
+        for (int r = 0; r < TR; ++r) {
+            rm_block_mma<G128>(acc[2 * r], av, wg[i][r], sz_scale(szg[i][r]), sz_zero(szg[i][r]), live);
+            rm_block_mma<G128>(acc[2 * r + 1], av, wu[i][r], sz_scale(szu[i][r]), sz_zero(szu[i][r]), live);
+        }
         __builtin_amdgcn_sched_barrier(0);
     }
+    __syncthreads();  // the token rows are dead: the reduction reuses their LDS
 
-    reduce_and_store<2>(red, acc, M, wave, nwaves, lane, [&](int m, int t, int c, float v) {
-        // t == 0: gate, t == 1: up; combine through LDS slot of the gate value
-        if (t == 0) red[nwaves * 512 + m * 16 + c] = v;
-        else red[nwaves * 512 + 256 + m * 16 + c] = v;
-    });
+    // reduce the 2*TR tiles over the waves, then h = silu(g) * u * w
+    float* red = reinterpret_cast<float*>(smem);
+    const size_t red_bytes = (size_t)nwaves * 2 * TR * 1024;
+    const size_t as_bytes = ((size_t)a.T * lda * 2 + 15) & ~(size_t)15;
+    float* gu = reinterpret_cast<float*>(smem + (red_bytes > as_bytes ? red_bytes : as_bytes));
+    reduce_and_store<2 * TR>(red, acc, M, wave, nwaves, lane,
+                             [&](int m, int t, int c, float v) { gu[t * 256 + m * 16 + c] = v; });
     __syncthreads();
-    for (int idx = threadIdx.x; idx < M * 16; idx += blockDim.x) {
-        const int m = idx >> 4, c = idx & 15;
-        const float g = red[nwaves * 512 + idx];
-        const float u = red[nwaves * 512 + 256 + idx];
-        float cf;
-        if (slot < a.max_active)
-            cf = moe_coef(a, slot, e, m);
-        else
-            cf = a.scoef ? a.scoef[m] : 1.0f;
-        const float h = (g / (1.0f + expf(-g))) * u * cf;
-        a.inter_buf[((size_t)slot * a.T + m) * a.inter_pad + tile * 16 + c] = bitcast<uint16_t>((f16)h);
+    for (int idx = threadIdx.x; idx < TR * M * 16; idx += blockDim.x) {
+        const int r = idx / (16 * M), rem = idx - r * (16 * M);
+        const int m = rem >> 4, c = rem & 15;
+        const float g = gu[(2 * r) * 256 + m * 16 + c];
+        const float u = gu[(2 * r + 1) * 256 + m * 16 + c];
+        const float w = slot >= 0 ? a.tokw[row0 + m] : (a.scoef ? a.scoef[m] : 1.0f);
+        const float h = (g / (1.0f + expf(-g))) * u * w;
+        a.inter_buf[(size_t)(row0 + m) * a.inter_pad + (grp * TR + r) * 16 + c] =
+            bitcast<uint16_t>((f16)h);
     }
 }
 
-// down projection of every active slot (and the shared expert) for one
-// 16-row output tile, summed in the MFMA accumulator in a fixed order:
-// y[t, o] = sum_slots sum_i inter_buf[slot, t, i] * dequant(Wd)[o, i].
-template <bool G128>
-__global__ __launch_bounds__(1024) void moe_down_k(MoeArgs a) {
+// Down projection of one slot (blockIdx.y < max_slots) or one K piece of the
+// shared expert (blockIdx.y - max_slots) for TRD 16-row output tiles
+// (blockIdx.x), over that slot's entries; results are added to y[token] with
+// fp32 atomics (like the reference's moew_down), so the summation order of
+// a token's terms varies between calls.
+template <bool G128, int NB, int TRD>
+__global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    constexpr int CH = 4;  // items issued together per wave
+    __shared__ int toks[16];
+    constexpr int W = 16 * TRD;  // output columns per workgroup
     const int nwaves = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, kq = lane >> 4;
-    const int M = a.T;
-    const int o = blockIdx.x * 16 + col;  // output row of this lane's B column
-    const int na = moe_n_active(a);
-    const int nkb_r = a.routed.inter >> 7;
-    const int nkb_s = a.has_shared ? (a.shared.inter >> 7) : 0;
-    const int items = na * nkb_r + nkb_s;
-    const int mrow = col < M ? col : M - 1;
-    float* red = reinterpret_cast<float*>(smem);
+    const int y_slot = blockIdx.y;
+    const int o0 = blockIdx.x * W;
+    const bool is_shared = y_slot >= a.max_slots;
+    if (is_shared && (!a.has_shared || y_slot - a.max_slots >= a.pieces)) return;
 
-    f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
-    const int my = wave < items ? (items - wave + nwaves - 1) / nwaves : 0;
-    for (int base = 0; base < my; base += CH) {
-        u32x4 av[CH][4];
-        u32x4 wv[CH];
-        uint16_t sv[CH], zv[CH];
+    int e = 0, row0 = 0, M = 0, kb0, nfull;
+    const MoeExperts* ex;
+    if (!is_shared) {
+        if (!moe_slot(a, y_slot, e, row0, M)) return;
+        ex = &a.routed;
+        kb0 = 0;
+        nfull = ex->inter >> 7;
+    } else {
+        const int p = y_slot - a.max_slots;
+        row0 = a.max_entries;
+        M = a.T;
+        ex = &a.shared;
+        kb0 = p * nwaves * NB;
+        const int left = (ex->inter >> 7) - kb0;
+        nfull = left < nwaves * NB ? left : nwaves * NB;
+    }
+    if (M <= 0 || nfull <= 0) return;
+    const int inter = ex->inter;
+    const int nkb = inter >> 7;  // 128-k blocks per row of the expert
+    const int G = inter / a.gs;
+    const int mrow = col < M ? col : M - 1;
+    const uint16_t* arow = a.inter_buf + (size_t)(row0 + mrow) * a.inter_pad + 32 * kq;
+    const size_t tb0 = (size_t)e * (a.hidden / 16) + o0 / 16;  // first row tile
+    if (threadIdx.x < 16)
+        toks[threadIdx.x] = is_shared ? threadIdx.x
+                                      : clampi(a.tok[row0 + (threadIdx.x < M ? threadIdx.x : 0)], 0, a.T - 1);
+
+    u32x4 av[NB][4];
+    u32x4 wv[NB][TRD];
+    uint32_t sv[NB][TRD];
+    // activations first (L2 hits), then weights (HBM): loads retire in
+    // issue order, so each block then waits only for its own weights
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            int it = base + i;
-            it = it < my ? it : my - 1;
-            const int item = wave + it * nwaves;
-            int slot, kb;
-            const MoeExperts* ex;
-            int e = 0;
-            if (item < na * nkb_r) {
-                slot = item / nkb_r;
-                kb = item - slot * nkb_r;
-                e = a.active[slot];
-                ex = &a.routed;
-            } else {
-                slot = a.max_active;
-                kb = item - na * nkb_r;
-                ex = &a.shared;
-            }
-            const int inter = ex->inter;
-            const uint16_t* ar = a.inter_buf + ((size_t)slot * a.T + mrow) * a.inter_pad + kb * 128 + 32 * kq;
+    for (int i = 0; i < NB; ++i) {
+        int kb = moe_kb<NB>(wave, i, nwaves);
+        kb = kb0 + (kb < nfull ? kb : nfull - 1);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) av[i][j] = *reinterpret_cast<const u32x4*>(ar + 8 * j);
-            const int G = inter / a.gs;
-            const size_t woff = (size_t)e * a.hidden * (inter / 2) + (size_t)o * (inter / 2) + kb * 64 + 16 * kq;
-            wv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ex->dq + woff));
-            const size_t so = (size_t)e * a.hidden * G + (size_t)o * G + (kb * 128 + 32 * kq) / a.gs;
-            sv[i] = ex->ds[so];
-            zv[i] = ex->dz[so];
-        }
-        __builtin_amdgcn_sched_barrier(0);
+        for (int j = 0; j < 4; ++j) av[i][j] = *reinterpret_cast<const u32x4*>(arow + kb * 128 + 8 * j);
+    }
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            const float live = (base + i < my) ? 1.0f : 0.0f;
-            rm_block_mma<G128>(acc[0], av[i], wv[i], sv[i], zv[i], live);
-            __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < NB; ++i) {
+        int kb = moe_kb<NB>(wave, i, nwaves);
+        kb = kb0 + (kb < nfull ? kb : nfull - 1);
+        const int g = (kb * 128 + 32 * kq) / a.gs;
+#pragma unroll
+        for (int r = 0; r < TRD; ++r) {
+            wv[i][r] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(ex->dq + ((tb0 + r) * nkb + kb) * 1024 + lane * 16));
+            sv[i][r] = ex->dsz[((tb0 + r) * G + g) * 16 + col];
         }
     }
-
-    reduce_and_store<1>(red, acc, M, wave, nwaves, lane, [&](int m, int, int c, float v) {
-        a.y[(size_t)m * a.hidden + blockIdx.x * 16 + c] = v;
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 acc[TRD];
+#pragma unroll
+    for (int r = 0; r < TRD; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const float live = moe_kb<NB>(wave, i, nwaves) < nfull ? 1.0f : 0.0f;
+#pragma unroll
+        for (int r = 0; r < TRD; ++r)
+            rm_block_mma<G128>(acc[r], av[i], wv[i][r], sz_scale(sv[i][r]), sz_zero(sv[i][r]), live);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    float* red = reinterpret_cast<float*>(smem);
+    reduce_and_store<TRD>(red, acc, M, wave, nwaves, lane, [&](int m, int t, int c, float v) {
+        unsafeAtomicAdd(&a.y[(size_t)toks[m] * a.hidden + o0 + 16 * t + c], v);
     });
 }
 
@@ -756,6 +922,74 @@ void rm_dispatch(int nb, const void* X, const uint8_t* W, const uint16_t* S, con
         case 5: launch_rm<5, G128, XF32, YF32>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
         case 6: launch_rm<6, G128, XF32, YF32>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
         default: launch_rm<8, G128, XF32, YF32>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
+    }
+}
+
+// Launch plan of the fused MoE for one problem shape (host side).
+struct MoePlan {
+    int nb_gu, waves_gu, nb_d, trd, waves_d, pieces, inter_pad;
+    size_t lds_gu, lds_d, bytes;
+};
+
+// 16-row output tiles per down-projection workgroup for NB blocks per wave.
+constexpr int down_tiles(int nb) { return nb <= 2 ? 4 : (nb <= 4 ? 2 : 1); }
+
+// false when the shape is outside what the kernels support.
+bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, MoePlan& p) {
+    if (T <= 0 || T > 16 || hidden <= 0 || hidden % 128 || inter <= 0 || inter % 128) return false;
+    if (shared_inter < 0 || shared_inter % 128 || max_entries <= 0) return false;
+    const int nfh = hidden / 128;
+    p.nb_gu = (nfh + 7) / 8;
+    if (p.nb_gu > 4) return false;  // hidden <= 4096
+    p.waves_gu = (nfh + p.nb_gu - 1) / p.nb_gu;
+    const size_t as_bytes = (((size_t)T * (hidden + 8) * 2) + 15) & ~(size_t)15;
+    const size_t red_bytes = (size_t)p.waves_gu * 2 * kGuTiles * 1024;
+    p.lds_gu = (as_bytes > red_bytes ? as_bytes : red_bytes) + (size_t)2 * kGuTiles * 1024;
+    if (p.lds_gu > 160 * 1024) return false;
+    const int nfr = inter / 128;
+    const int nb = (nfr + 7) / 8;
+    if (nb > 8) return false;  // inter <= 8192
+    p.nb_d = nb == 5 ? 6 : (nb == 7 ? 8 : nb);
+    p.trd = down_tiles(p.nb_d);
+    if (hidden % (16 * p.trd)) return false;
+    p.waves_d = (nfr + p.nb_d - 1) / p.nb_d;
+    const int span = p.waves_d * p.nb_d;
+    p.pieces = shared_inter > 0 ? (shared_inter / 128 + span - 1) / span : 0;
+    p.lds_d = (size_t)p.waves_d * p.trd * 1024;
+    p.inter_pad = inter > shared_inter ? inter : shared_inter;
+    p.bytes = (size_t)(max_entries + T) * p.inter_pad * 2;
+    return true;
+}
+
+template <bool G128, int NB>
+void launch_gate_up(const MoeArgs& a, int grid, const MoePlan& p, hipStream_t st) {
+    hipLaunchKernelGGL((moe_gate_up_k<G128, NB>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu, st, a);
+}
+
+template <bool G128, int NB>
+void launch_down(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
+    const dim3 grid(a.hidden / (16 * down_tiles(NB)), a.max_slots + p.pieces);
+    hipLaunchKernelGGL((moe_down_k<G128, NB, down_tiles(NB)>), grid, dim3(64 * p.waves_d), p.lds_d,
+                       st, a);
+}
+
+template <bool G128>
+void moe_launch(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
+    const int grid_gu = a.max_slots * (a.routed.inter / (16 * kGuTiles)) +
+                        (a.has_shared ? a.shared.inter / (16 * kGuTiles) : 0);
+    switch (p.nb_gu) {
+        case 1: launch_gate_up<G128, 1>(a, grid_gu, p, st); break;
+        case 2: launch_gate_up<G128, 2>(a, grid_gu, p, st); break;
+        case 3: launch_gate_up<G128, 3>(a, grid_gu, p, st); break;
+        default: launch_gate_up<G128, 4>(a, grid_gu, p, st); break;
+    }
+    switch (p.nb_d) {
+        case 1: launch_down<G128, 1>(a, p, st); break;
+        case 2: launch_down<G128, 2>(a, p, st); break;
+        case 3: launch_down<G128, 3>(a, p, st); break;
+        case 4: launch_down<G128, 4>(a, p, st); break;
+        case 6: launch_down<G128, 6>(a, p, st); break;
+        default: launch_down<G128, 8>(a, p, st); break;
     }
 }
 
@@ -830,9 +1064,9 @@ int fastllm_route_topk(const float* logits, int T, int E, int top_k, int scoring
     if (n_group > 1 && (E % n_group || n_group > 64)) return 1;
     if (n_active && (!active || !offsets || !tok || !tokw)) return 1;
     if (!fl_current_device_supported()) return 2;
+    const MoeLists lists{n_active, active, offsets, tok, tokw};
     RouteArgs a{logits, e_score_bias, shared_logit, T, E, top_k, scoring, norm, n_group,
-                topk_group, routed_scaling, topk_ids, topk_w, rw, shared_coef,
-                n_active, active, offsets, tok, tokw};
+                topk_group, routed_scaling, topk_ids, topk_w, rw, shared_coef, lists};
     hipStream_t st = (hipStream_t)stream;
     const int wpb = T < 16 ? T : 16;
     const int grid = (T + 15) / 16;
@@ -841,80 +1075,112 @@ int fastllm_route_topk(const float* logits, int T, int E, int top_k, int scoring
     if (rc) return rc;
     if (grid > 1 && n_active) {
         hipLaunchKernelGGL(route_lists_k, dim3(1), dim3(1024), 0, st, topk_ids, topk_w, T, top_k,
-                           E, n_active, active, offsets, tok, tokw);
+                           E, lists);
         rc = finish("fastllm_route_topk");
     }
     return rc;
 }
 
-// Fused selective INT4 MoE FFN for up to 16 tokens (see MoeArgs).
-int fastllm_moe_int4_fused(const float* x, int T, int hidden, int group_size, int E,
-                           int inter, const uint8_t* gq, const void* gsc, const void* gz,
-                           const uint8_t* uq, const void* usc, const void* uz,
-                           const uint8_t* dq, const void* dsc, const void* dz,
-                           int shared_inter, const uint8_t* sgq, const void* sgs, const void* sgz,
-                           const uint8_t* suq, const void* sus, const void* suz,
-                           const uint8_t* sdq, const void* sds, const void* sdz,
-                           const float* shared_coef, const int* n_active, int host_active,
-                           const int* active, int max_active, const float* rw,
-                           const float* slot_coef, void* inter_buf, int inter_pad, float* y,
-                           void* stream) {
-    if (!x || T <= 0 || T > 16 || hidden <= 0 || hidden % 128 || hidden > 2048) return 1;
-    if (E <= 0 || inter <= 0 || inter % 128 || !gq || !uq || !dq || !active || !inter_buf || !y)
+int fastllm_moe_build_lists(const float* rw, const float* slot_coef, const int* cand, int T,
+                            int E, int S, int* n_active, int* active, int* offsets, int* tok,
+                            float* tokw, void* stream) {
+    if (T <= 0 || T > 16 || E <= 0 || S <= 0 || S > 256 || (!rw && !slot_coef)) return 1;
+    if (rw && !cand && S > E) return 1;
+    if (!n_active || !active || !offsets || !tok || !tokw) return 1;
+    if (!fl_current_device_supported()) return 2;
+    const MoeLists lists{n_active, active, offsets, tok, tokw};
+    hipLaunchKernelGGL(slot_lists_k, dim3(1), dim3(256), 0, (hipStream_t)stream,
+                       slot_coef ? nullptr : rw, slot_coef, cand, T, E, S, lists);
+    return finish("fastllm_moe_build_lists");
+}
+
+int fastllm_moe_int4_tile_repack(const uint8_t* qweight, const void* scales, const void* zeros,
+                                 uint8_t* qtile, uint32_t* sz, long rows, int in_f,
+                                 int group_size, void* stream) {
+    if (!qweight || !scales || !zeros || !qtile || !sz || rows <= 0 || rows % 16) return 1;
+    if (in_f <= 0 || in_f % 128 || (group_size != 32 && group_size != 64 && group_size != 128))
         return 1;
+    if (!fl_aligned(qweight, 16) || !fl_aligned(qtile, 16)) return 1;
+    if (!fl_current_device_supported()) return 2;
+    const long work = rows * (in_f / 32);
+    const int grid = (int)((work + 255) / 256 < 8192 ? (work + 255) / 256 : 8192);
+    hipLaunchKernelGGL(moe_tile_repack_k, dim3(grid), dim3(256), 0, (hipStream_t)stream, qweight,
+                       (const uint16_t*)scales, (const uint16_t*)zeros, qtile, sz, rows, in_f,
+                       in_f / group_size);
+    return finish("fastllm_moe_int4_tile_repack");
+}
+
+int fastllm_moe_int4_tile_unpack(const uint8_t* qtile, const uint32_t* sz, uint8_t* qweight,
+                                 void* scales, void* zeros, long rows, int in_f, int group_size,
+                                 void* stream) {
+    if (!qweight || !scales || !zeros || !qtile || !sz || rows <= 0 || rows % 16) return 1;
+    if (in_f <= 0 || in_f % 128 || (group_size != 32 && group_size != 64 && group_size != 128))
+        return 1;
+    if (!fl_aligned(qweight, 16) || !fl_aligned(qtile, 16)) return 1;
+    if (!fl_current_device_supported()) return 2;
+    const long work = rows * (in_f / 32);
+    const int grid = (int)((work + 255) / 256 < 8192 ? (work + 255) / 256 : 8192);
+    hipLaunchKernelGGL(moe_tile_unpack_k, dim3(grid), dim3(256), 0, (hipStream_t)stream, qtile, sz,
+                       qweight, (uint16_t*)scales, (uint16_t*)zeros, rows, in_f, in_f / group_size);
+    return finish("fastllm_moe_int4_tile_unpack");
+}
+
+size_t fastllm_moe_int4_workspace_bytes(int T, int hidden, int inter, int shared_inter,
+                                        int max_entries) {
+    MoePlan p;
+    return moe_plan(T, hidden, inter, shared_inter, max_entries, p) ? p.bytes : 0;
+}
+
+int fastllm_moe_int4_fused(const float* x, int T, int hidden, int group_size, int E, int inter,
+                           const uint8_t* gq, const uint32_t* gsz, const uint8_t* uq,
+                           const uint32_t* usz, const uint8_t* dq, const uint32_t* dsz,
+                           int shared_inter, const uint8_t* sgq, const uint32_t* sgsz,
+                           const uint8_t* suq, const uint32_t* susz, const uint8_t* sdq,
+                           const uint32_t* sdsz, const float* shared_coef, const int* n_active,
+                           const int* active, const int* offsets, const int* tok,
+                           const float* tokw, int max_slots, int max_entries, void* workspace,
+                           size_t workspace_bytes, float* y, void* stream) {
+    if (!x || !y || E <= 0 || !gq || !gsz || !uq || !usz || !dq || !dsz) return 1;
     if (group_size != 32 && group_size != 64 && group_size != 128) return 1;
-    if (max_active < 0 || (!rw && !slot_coef)) return 1;
+    if (!n_active || !active || !offsets || !tok || !tokw) return 1;
+    if (max_slots <= 0 || max_entries <= 0) return 1;
     const bool has_shared = shared_inter > 0;
-    if (has_shared && (shared_inter % 128 || !sgq || !suq || !sdq)) return 1;
-    const int need_pad = inter > shared_inter ? inter : shared_inter;
-    if (inter_pad < need_pad) return 1;
-    if (!fl_aligned(x, 16) || !fl_aligned(inter_buf, 16)) return 1;
+    if (has_shared && (!sgq || !sgsz || !suq || !susz || !sdq || !sdsz)) return 1;
+    MoePlan p;
+    if (!moe_plan(T, hidden, inter, has_shared ? shared_inter : 0, max_entries, p)) return 1;
+    if (!workspace || workspace_bytes < p.bytes || !fl_aligned(workspace, 16)) return 1;
+    if (!fl_aligned(x, 16) || !fl_aligned(y, 16)) return 1;
+    const bool al = fl_aligned(gq, 16) && fl_aligned(uq, 16) && fl_aligned(dq, 16) &&
+                    (!has_shared || (fl_aligned(sgq, 16) && fl_aligned(suq, 16) && fl_aligned(sdq, 16)));
+    if (!al) return 1;
     if (!fl_current_device_supported()) return 2;
     MoeArgs a;
     a.x = x;
     a.T = T;
     a.hidden = hidden;
     a.gs = group_size;
-    a.routed = MoeExperts{gq, (const uint16_t*)gsc, (const uint16_t*)gz, uq, (const uint16_t*)usc,
-                          (const uint16_t*)uz, dq, (const uint16_t*)dsc, (const uint16_t*)dz, inter};
-    a.shared = MoeExperts{sgq, (const uint16_t*)sgs, (const uint16_t*)sgz, suq, (const uint16_t*)sus,
-                          (const uint16_t*)suz, sdq, (const uint16_t*)sds, (const uint16_t*)sdz,
-                          has_shared ? shared_inter : 0};
-    a.has_shared = has_shared ? 1 : 0;
     a.E = E;
-    a.n_active = n_active;
-    a.host_active = host_active;
-    a.active = active;
-    a.rw = rw;
-    a.coef = slot_coef;
-    a.coef_mode = rw ? 0 : 1;
+    a.routed = MoeExperts{gq, gsz, uq, usz, dq, dsz, inter};
+    a.shared = MoeExperts{sgq, sgsz, suq, susz, sdq, sdsz, has_shared ? shared_inter : 0};
+    a.has_shared = has_shared ? 1 : 0;
+    a.pieces = p.pieces;
     a.scoef = shared_coef;
-    a.max_active = max_active;
-    a.inter_pad = inter_pad;
-    a.inter_buf = (uint16_t*)inter_buf;
+    a.n_active = n_active;
+    a.active = active;
+    a.offsets = offsets;
+    a.tok = tok;
+    a.tokw = tokw;
+    a.max_slots = max_slots;
+    a.max_entries = max_entries;
+    a.inter_pad = p.inter_pad;
+    a.inter_buf = static_cast<uint16_t*>(workspace);
     a.y = y;
     hipStream_t st = (hipStream_t)stream;
-    const bool g128 = group_size == 128;
-    // gate/up: one workgroup per (slot, 16-row tile)
-    const int tiles = max_active * (inter / 16) + (has_shared ? shared_inter / 16 : 0);
-    const int waves_gu = 8;
-    const size_t lds_gu = (((size_t)T * (hidden + 8) * 2 + 15) & ~(size_t)15) +
-                          (size_t)waves_gu * 2 * 1024 + 2 * 1024;
-    if (tiles > 0) {
-        if (g128)
-            hipLaunchKernelGGL(moe_gate_up_k<true>, dim3(tiles), dim3(64 * waves_gu), lds_gu, st, a);
-        else
-            hipLaunchKernelGGL(moe_gate_up_k<false>, dim3(tiles), dim3(64 * waves_gu), lds_gu, st, a);
-        const int rc = finish("fastllm_moe_int4_fused(gate_up)");
-        if (rc) return rc;
-    }
-    const int waves_d = 16;
-    const size_t lds_d = (size_t)waves_d * 1024;
-    if (g128)
-        hipLaunchKernelGGL(moe_down_k<true>, dim3(hidden / 16), dim3(64 * waves_d), lds_d, st, a);
+    if (group_size == 128)
+        moe_launch<true>(a, p, st);
     else
-        hipLaunchKernelGGL(moe_down_k<false>, dim3(hidden / 16), dim3(64 * waves_d), lds_d, st, a);
-    return finish("fastllm_moe_int4_fused(down)");
+        moe_launch<false>(a, p, st);
+    return finish("fastllm_moe_int4_fused");
 }
 
 }  // extern "C"

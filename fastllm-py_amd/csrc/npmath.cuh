@@ -58,3 +58,48 @@ __host__ __device__ inline float np_sum_rec(const float* a, int n) {
 }
 
 __host__ __device__ inline float np_sum_f32(const float* a, int n) { return np_sum_rec<3>(a, n); }
+
+// np_sum_f32 for n <= 256 evaluated by one wave, same result bit for bit.
+// The recursion's leaves (at most three for n <= 256: [0, n2) and the right
+// part, split once more when longer than 128) go to lane groups of 8; lane j
+// of a group forms accumulator r[j] over its leaf in numpy's order, the
+// groups fold ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) with xor-shuffles (the
+// same sums: float addition is commutative), add the leaf's tail, and lane 0
+// joins the leaves as the recursion does.  `a` may be LDS.  All lanes return
+// the sum.
+__device__ inline float np_sum_wave(const float* a, int n, int lane) {
+    int s1 = 0, l0 = n, l1 = 0, s2 = 0, l2 = 0, nl = 1;
+    if (n > 128) {
+        const int h = n / 2, n2 = h - h % 8, m = n - n2;
+        l0 = n2;
+        s1 = n2;
+        nl = 2;
+        l1 = m;
+        if (m > 128) {
+            const int hm = m / 2, m2 = hm - hm % 8;
+            l1 = m2;
+            s2 = n2 + m2;
+            l2 = m - m2;
+            nl = 3;
+        }
+    }
+    const int leaf = lane >> 3, j = lane & 7;
+    const int ls = leaf == 0 ? 0 : (leaf == 1 ? s1 : s2);
+    const int ll = leaf == 0 ? l0 : (leaf == 1 ? l1 : (leaf == 2 ? l2 : 0));
+    const bool blk = leaf < nl && ll >= 8;
+    float r = 0.0f;
+    if (blk) {
+        r = a[ls + j];
+        for (int i = 8; i < ll - ll % 8; i += 8) r += a[ls + i + j];
+    }
+    r = r + __shfl_xor(r, 1, 64);
+    r = r + __shfl_xor(r, 2, 64);
+    r = r + __shfl_xor(r, 4, 64);
+    float res = 0.0f;
+    if (j == 0 && leaf < nl) {
+        res = blk ? r : 0.0f;
+        for (int i = blk ? ll - ll % 8 : 0; i < ll; ++i) res += a[ls + i];
+    }
+    const float f0 = __shfl(res, 0, 64), f1 = __shfl(res, 8, 64), f2 = __shfl(res, 16, 64);
+    return nl == 1 ? f0 : (nl == 2 ? f0 + f1 : f0 + (f1 + f2));
+}

@@ -17,6 +17,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
 _B = ctypes.c_bool
+_SZ = ctypes.c_size_t
 
 # name -> (restype, argtypes).  Mirrors include/fastllm_kernels.h.
 SIGNATURES: dict[str, tuple] = {
@@ -51,8 +52,12 @@ SIGNATURES: dict[str, tuple] = {
     "fastllm_gate_matvec": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "fastllm_route_topk": (_I, [_P, _I, _I, _I, _I, _I, _F, _P, _I, _I, _P, _P, _P, _P, _P,
                                 _P, _P, _P, _P, _P, _P]),
-    "fastllm_moe_int4_fused": (_I, [_P, _I, _I, _I, _I, _I] + [_P] * 9 + [_I] + [_P] * 9 +
-                               [_P, _P, _I, _P, _I, _P, _P, _P, _I, _P, _P]),
+    "fastllm_moe_build_lists": (_I, [_P, _P, _P, _I, _I, _I] + [_P] * 6),
+    "fastllm_moe_int4_tile_repack": (_I, [_P, _P, _P, _P, _P, ctypes.c_long, _I, _I, _P]),
+    "fastllm_moe_int4_tile_unpack": (_I, [_P, _P, _P, _P, _P, ctypes.c_long, _I, _I, _P]),
+    "fastllm_moe_int4_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
+    "fastllm_moe_int4_fused": (_I, [_P, _I, _I, _I, _I, _I] + [_P] * 6 + [_I] + [_P] * 6 +
+                               [_P] * 6 + [_I, _I, _P, _SZ, _P, _P]),
 }
 
 

@@ -11,9 +11,10 @@ Format for a weight W of shape (out, in), group size gs along ``in``:
   scales  : (out, in//gs) fp16
   zeros   : (out, in//gs) fp16   -- dequant(W[o,i]) = (q - zero) * scale
 
-Differences from the reference kernels, all in the direction of the numpy
-reference: the fused MoE combines experts in a fixed order (no atomics), so a
-call is deterministic; activations feed the matrix cores as fp16.
+The fused MoE keeps its stacked experts in a tile layout of its own
+(``build_stacked_experts`` / ``tile_pack``; ``unpack_stacked`` inverts it)
+so every wave load reads one contiguous 1 KB block.  Activations feed the
+matrix cores as fp16.
 """
 from __future__ import annotations
 
@@ -75,11 +76,49 @@ def _quantize_int4_rowmajor_batched(W, group_size: int, xp=np):
     return qw, sc, ze, (qw.shape[-2], qw.shape[-1] * 2)
 
 
-def build_stacked_experts(expert_ws, group_size: int = 128, xp=np) -> dict:
-    """Stack E experts' {gate, up, down} into (E, out, in/2) INT4 device tensors
-    indexable by expert id (moe_int4.py:116-133)."""
+def tile_pack(qweight, scales, zeros, group_size: int):
+    """Row-major INT4 (rows, in/2) u8 + (rows, in/gs) fp16 scales/zeros (any
+    leading dims, rows % 16 == 0) -> the fused MoE's tile layout:
+    qtile (rows/16, in/128, 1024) u8 and sz (rows/16, in/gs, 16) int32 holding
+    scale bits | zero bits << 16 (csrc/moe_int4.hip describes the layout)."""
     t = nat.torch()
-    out = {"group": group_size}
+    q = nat.to_device(qweight, t.uint8).contiguous()
+    sc = nat.to_device(scales, t.float16).contiguous()
+    ze = nat.to_device(zeros, t.float16).contiguous()
+    in_f = q.shape[-1] * 2
+    rows = q.numel() // (in_f // 2)
+    qt = t.empty((rows // 16, in_f // 128, 1024), dtype=t.uint8, device=q.device)
+    sz = t.empty((rows // 16, in_f // group_size, 16), dtype=t.int32, device=q.device)
+    rc = nat.lib().fastllm_moe_int4_tile_repack(nat.ptr(q), nat.ptr(sc), nat.ptr(ze), nat.ptr(qt),
+                                                nat.ptr(sz), rows, in_f, group_size,
+                                                nat.current_stream_handle())
+    nat.check_rc(rc, "fastllm_moe_int4_tile_repack")
+    return qt, sz
+
+
+def tile_unpack(qtile, sz, rows: int, in_f: int, group_size: int):
+    """Inverse of ``tile_pack`` -> (qweight (rows, in/2) u8, scales, zeros
+    (rows, in/gs) fp16) device tensors, bit-exact."""
+    t = nat.torch()
+    q = t.empty((rows, in_f // 2), dtype=t.uint8, device=qtile.device)
+    sc = t.empty((rows, in_f // group_size), dtype=t.float16, device=qtile.device)
+    ze = t.empty_like(sc)
+    rc = nat.lib().fastllm_moe_int4_tile_unpack(nat.ptr(qtile), nat.ptr(sz), nat.ptr(q),
+                                                nat.ptr(sc), nat.ptr(ze), rows, in_f, group_size,
+                                                nat.current_stream_handle())
+    nat.check_rc(rc, "fastllm_moe_int4_tile_unpack")
+    return q, sc, ze
+
+
+def build_stacked_experts(expert_ws, group_size: int = 128, xp=np) -> dict:
+    """Stack E experts' {gate, up, down}, quantize them (row-major RTN group
+    INT4, moe_int4.py:116-133) and store them in the fused MoE's tile layout,
+    indexable by expert id: ``{proj}.qtile`` (E, out/16, in/128, 1024) u8,
+    ``{proj}.sz`` (E, out/16, in/gs, 16) int32, ``{proj}.shape`` (out, in).
+    The reference's callers only hand this dict to the fused MoE kernels;
+    ``unpack_stacked`` recovers the row-major payload."""
+    t = nat.torch()
+    out = {"group": group_size, "layout": "tile16x128"}
     for proj in ("gate", "up", "down"):
         ws = [w[proj] for w in expert_ws]
         if nat.is_tensor(ws[0]):
@@ -87,10 +126,34 @@ def build_stacked_experts(expert_ws, group_size: int = 128, xp=np) -> dict:
         else:
             stack = np.stack([np.asarray(w) for w in ws])
         qw, sc, ze, shp = _quantize_int4_rowmajor_batched(stack, group_size)
-        out[f"{proj}.qweight"] = qw
-        out[f"{proj}.scales"] = sc
-        out[f"{proj}.zeros"] = ze
-        out[f"{proj}.shape"] = shp
+        out.update(stack_tiles(proj, qw, sc, ze, group_size))
+    return out
+
+
+def stack_tiles(proj: str, qw, sc, ze, group_size: int) -> dict:
+    """Row-major stacked (E, out, in/2) / (E, out, in/gs) -> the tile-layout
+    entries of one projection of a stacked-experts dict."""
+    E, out_f, half = qw.shape
+    qt, sz = tile_pack(qw, sc, ze, group_size)
+    return {f"{proj}.qtile": qt.reshape(E, out_f // 16, half * 2 // 128, 1024),
+            f"{proj}.sz": sz.reshape(E, out_f // 16, half * 2 // group_size, 16),
+            f"{proj}.shape": (out_f, half * 2)}
+
+
+def unpack_stacked(stacked) -> dict:
+    """Tile-layout stacked experts -> row-major {proj}.qweight (E, out, in/2)
+    u8, {proj}.scales / {proj}.zeros (E, out, in/gs) fp16 device tensors."""
+    gs = stacked["group"]
+    out = {"group": gs}
+    for proj in ("gate", "up", "down"):
+        qt = stacked[f"{proj}.qtile"]
+        out_f, in_f = stacked[f"{proj}.shape"]
+        E = qt.shape[0]
+        q, sc, ze = tile_unpack(qt, stacked[f"{proj}.sz"], E * out_f, in_f, gs)
+        out[f"{proj}.qweight"] = q.reshape(E, out_f, in_f // 2)
+        out[f"{proj}.scales"] = sc.reshape(E, out_f, in_f // gs)
+        out[f"{proj}.zeros"] = ze.reshape(E, out_f, in_f // gs)
+        out[f"{proj}.shape"] = (out_f, in_f)
     return out
 
 
@@ -148,52 +211,101 @@ def gate_matvec(x, gate_w, E, hidden, out=None, threads=128):
 
 # -------------------------------------------------------------- fused MoE
 def _stacked_ptrs(st):
-    return [nat.ptr(st[f"{p}.{k}"]) for p in ("gate", "up", "down")
-            for k in ("qweight", "scales", "zeros")]
+    return [nat.ptr(st[f"{p}.{k}"]) for p in ("gate", "up", "down") for k in ("qtile", "sz")]
 
 
-def moe_forward(x, stacked, E, hidden, inter, *, rw=None, active=None, n_active=None,
-                host_active=None, slot_coef=None, shared=None, shared_inter=0,
-                shared_coef=None, out=None, inter_buf=None, max_active=None, stream=None):
+def moe_workspace_bytes(T: int, hidden: int, inter: int, shared_inter: int,
+                        max_entries: int) -> int:
+    """Device workspace (bytes) of one fused MoE call of this shape."""
+    n = nat.lib().fastllm_moe_int4_workspace_bytes(T, hidden, inter, shared_inter or 0,
+                                                   max_entries)
+    if n == 0:
+        raise ValueError(f"unsupported fused MoE shape T={T} hidden={hidden} inter={inter} "
+                         f"shared_inter={shared_inter}")
+    return int(n)
+
+
+def build_lists(T: int, E: int, *, rw=None, slot_coef=None, cand=None, out=None,
+                stream=None) -> dict:
+    """Expert-major MoE lists for the fused MoE from dense weights ``rw``
+    (T, E) (slots = ``cand`` experts, or all E in order) or per-slot weights
+    ``slot_coef`` (S, T) for the experts ``cand`` (S,).  Entries with weight 0
+    are dropped.  Same layout as the router's lists."""
+    t = nat.torch()
+    if slot_coef is not None:
+        coef = nat.to_device(slot_coef, t.float32).contiguous()
+        S = coef.shape[0]
+        dev = coef.device
+        rwd = None
+    else:
+        rwd = nat.to_device(rw, t.float32).reshape(T, E).contiguous()
+        coef = None
+        dev = rwd.device
+    cd = None
+    if cand is not None:
+        cd = nat.to_device(cand, t.int32).reshape(-1).contiguous()
+        S = cd.numel()
+    elif slot_coef is None:
+        S = E
+    o = out if out is not None else {}
+
+    def buf(name, shape, dtype):
+        if name not in o:
+            o[name] = t.empty(shape, dtype=dtype, device=dev)
+        return o[name]
+
+    na = buf("n_active", (1,), t.int32)
+    act = buf("active", (S,), t.int32)
+    offs = buf("offsets", (S + 1,), t.int32)
+    tok = buf("tok", (S * T,), t.int32)
+    tokw = buf("tokw", (S * T,), t.float32)
+    h = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
+    rc = nat.lib().fastllm_moe_build_lists(
+        nat.ptr(rwd) if rwd is not None else None, nat.ptr(coef) if coef is not None else None,
+        nat.ptr(cd) if cd is not None else None, T, E, S, nat.ptr(na), nat.ptr(act),
+        nat.ptr(offs), nat.ptr(tok), nat.ptr(tokw), h)
+    nat.check_rc(rc, "fastllm_moe_build_lists")
+    return o
+
+
+def moe_forward(x, stacked, E, hidden, inter, lists, *, max_slots=None, max_entries=None,
+                shared=None, shared_inter=0, shared_coef=None, out=None, workspace=None,
+                stream=None):
     """Fused selective INT4 MoE FFN for T <= 16 tokens (x (T, hidden) fp32):
 
-    y[t] = sum_{slots s} coef(s, t) * down_e(silu(gate_e x_t) * up_e x_t)
+    y[t] = sum_{entries p of t} tokw[p] * down_e(silu(gate_e x_t) * up_e x_t)
            + shared_coef[t] * shared(x_t)
 
-    Routing comes either as dense weights ``rw`` (T, E) with the active expert
-    list ``active`` (device int32) and its length ``n_active`` (device (1,)
-    int32) or ``host_active`` (int), or as per-slot weights ``slot_coef``
-    (S, T) for the experts listed in ``active``.  Experts are combined in slot
-    order inside the matrix cores: no atomics, deterministic."""
+    ``lists`` are expert-major MoE lists (``route_topk_device`` or
+    ``build_lists``).  Gate/up run only over the tokens routed to each
+    expert; the down projection adds each expert's term into y with fp32
+    atomics, as the reference's moew_down does, so the last bits depend on
+    arrival order.  ``workspace`` (uint8 device tensor) is reused when large
+    enough, else allocated."""
     t = nat.torch()
     xd = nat.to_device(x, t.float32)
     x2 = xd.reshape(-1, hidden).contiguous()
     T = x2.shape[0]
     if T > 16:
         raise ValueError("moe_forward handles up to 16 tokens per call")
-    act = nat.to_device(active, t.int32)
-    S = int(act.numel()) if max_active is None else int(max_active)
-    gs = stacked["group"]
-    pad = max(inter, shared_inter or 0)
-    nslots = S + (1 if shared is not None else 0)
-    need = nslots * T * pad
-    if inter_buf is not None and inter_buf.numel() * inter_buf.element_size() >= need * 2 \
-            and inter_buf.is_contiguous():
-        ib = inter_buf
-    else:
-        ib = t.empty((nslots, T, pad), dtype=t.float16, device=xd.device)
+    if max_entries is None:
+        max_entries = lists["tok"].numel()
+    if max_slots is None:
+        max_slots = min(lists["active"].numel(), max_entries)
+    sint = int(shared_inter or 0) if shared is not None else 0
+    need = moe_workspace_bytes(T, hidden, inter, sint, max_entries)
+    ws = workspace
+    if ws is None or ws.numel() * ws.element_size() < need or not ws.is_contiguous():
+        ws = t.empty((need,), dtype=t.uint8, device=xd.device)
     y = out if out is not None else t.empty((T, hidden), dtype=t.float32, device=xd.device)
-    sp = _stacked_ptrs(shared) if shared is not None else [None] * 9
+    sp = _stacked_ptrs(shared) if shared is not None else [None] * 6
     h = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
     rc = nat.lib().fastllm_moe_int4_fused(
-        nat.ptr(x2), T, hidden, gs, E, inter, *_stacked_ptrs(stacked),
-        int(shared_inter or 0) if shared is not None else 0, *sp,
+        nat.ptr(x2), T, hidden, stacked["group"], E, inter, *_stacked_ptrs(stacked), sint, *sp,
         nat.ptr(shared_coef) if shared_coef is not None else None,
-        nat.ptr(n_active) if n_active is not None else None,
-        int(host_active if host_active is not None else S), nat.ptr(act), S,
-        nat.ptr(rw) if rw is not None else None,
-        nat.ptr(slot_coef) if slot_coef is not None else None,
-        nat.ptr(ib), pad, nat.ptr(y), h)
+        nat.ptr(lists["n_active"]), nat.ptr(lists["active"]), nat.ptr(lists["offsets"]),
+        nat.ptr(lists["tok"]), nat.ptr(lists["tokw"]), int(max_slots), int(max_entries), nat.ptr(ws),
+        ws.numel() * ws.element_size(), nat.ptr(y), h)
     nat.check_rc(rc, "fastllm_moe_int4_fused")
     return y
 
@@ -202,17 +314,14 @@ def fused_moe_weighted(x, stacked, rw, E, hidden, inter, out=None, inter_buf=Non
                        threads=256, rpb=8, aidx=None):
     """(E,)-routing-weight-driven selective MoE FFN (moe_int4.py:263-294):
     y (hidden,) = sum_{e: rw[e] > 0} rw[e] * FFN_e(x).  ``aidx`` (K,) lists the
-    active experts; without it every expert is visited and zero weights skip
-    nothing but contribute 0."""
+    active experts; without it every expert is scanned and those with zero
+    weight are skipped.  ``inter_buf`` may be a reusable uint8 workspace."""
     t = nat.torch()
     rwd = nat.to_device(rw, t.float32).reshape(1, -1)
-    if aidx is None:
-        act = t.arange(E, dtype=t.int32, device=rwd.device)
-    else:
-        act = nat.to_device(aidx, t.int32).reshape(-1)
+    cand = None if aidx is None else nat.to_device(aidx, t.int32).reshape(-1)
+    L = build_lists(1, E, rw=rwd, cand=cand)
     y = out.reshape(1, hidden) if out is not None else None
-    r = moe_forward(x, stacked, E, hidden, inter, rw=rwd, active=act, out=y,
-                    inter_buf=inter_buf)
+    r = moe_forward(x, stacked, E, hidden, inter, L, out=y, workspace=inter_buf)
     return r.reshape(hidden)
 
 
@@ -220,12 +329,12 @@ def fused_moe_ffn2(x, stacked, eidx, rw, hidden, inter, out=None, inter_buf=None
     """Index-driven selective MoE FFN (moe_int4.py:372-396):
     y = sum_k rw[k] * FFN_{eidx[k]}(x)."""
     t = nat.torch()
-    act = nat.to_device(eidx, t.int32).reshape(-1)
+    cand = nat.to_device(eidx, t.int32).reshape(-1)
     coef = nat.to_device(rw, t.float32).reshape(-1, 1).contiguous()
-    E = stacked["gate.qweight"].shape[0]
+    E = stacked["gate.qtile"].shape[0]
+    L = build_lists(1, E, slot_coef=coef, cand=cand)
     y = out.reshape(1, hidden) if out is not None else None
-    r = moe_forward(x, stacked, E, hidden, inter, slot_coef=coef, active=act, out=y,
-                    inter_buf=inter_buf)
+    r = moe_forward(x, stacked, E, hidden, inter, L, out=y, workspace=inter_buf)
     return r.reshape(hidden)
 
 
@@ -256,8 +365,8 @@ def moe_branch(x, gate_w, stacked, top_k, *, E, hidden, inter, norm=False, scale
     sync (graph_decode._moe_branch, graph_decode.py:669-700):
     gate matvec (+ shared gate) -> router -> fused routed + shared FFN.
     Returns (T, hidden) fp32.  ``bufs`` may carry persistent buffers for
-    graph capture (keys of route_topk_device plus logits, slogit, inter_buf,
-    out)."""
+    graph capture (keys of route_topk_device plus logits, slogit, workspace,
+    out); missing ones are allocated and stored there."""
     from ..expert_router import route_topk_device
 
     t = nat.torch()
@@ -282,9 +391,12 @@ def moe_branch(x, gate_w, stacked, top_k, *, E, hidden, inter, norm=False, scale
     nat.check_rc(rc, "fastllm_gate_matvec")
     r = route_topk_device(logits, top_k, norm_topk_prob=norm, routed_scaling=scale,
                           shared_logit=sl, out=b, stream=stream)
-    max_active = min(E, T * top_k)
-    return moe_forward(xd, stacked, E, hidden, inter, rw=r["rw"], active=r["active"],
-                       n_active=r["n_active"], max_active=max_active, shared=shared,
-                       shared_inter=shared_inter,
+    if "workspace" not in b:
+        b["workspace"] = t.empty((moe_workspace_bytes(T, hidden, inter,
+                                                      shared_inter if shared is not None else 0,
+                                                      T * top_k),),
+                                 dtype=t.uint8, device=xd.device)
+    return moe_forward(xd, stacked, E, hidden, inter, r, max_slots=min(E, T * top_k),
+                       max_entries=T * top_k, shared=shared, shared_inter=shared_inter,
                        shared_coef=r.get("shared_coef") if shared_gate_w is not None else None,
-                       out=b.get("out"), inter_buf=b.get("inter_buf"), stream=stream)
+                       out=b.get("out"), workspace=b["workspace"], stream=stream)

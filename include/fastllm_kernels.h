@@ -14,6 +14,7 @@
 #define FASTLLM_KERNELS_H
 
 #include <stdbool.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -257,7 +258,7 @@ int fastllm_gate_matvec(const float *x, const void *gate_w,
  * times routed_scaling.  Ties at the k-th value go to the lower expert index.
  * Outputs: topk_ids/topk_w [T, top_k] (descending selection), optional dense
  * rw [T, E]; optional shared_coef[T] = sigmoid(shared_logit); optional
- * expert-major lists (all or none): n_active[1], active[E] ascending,
+ * expert-major MoE lists (all or none): n_active[1], active[E] ascending,
  * offsets[E+1], tok[T*top_k] ascending within an expert, tokw[T*top_k].
  * Replaces: route_topk (fastllm_py/expert_router.py:22-71) and
  * _route_topk_kernel (fastllm_py/graph_decode.py:242-285). */
@@ -269,36 +270,74 @@ int fastllm_route_topk(const float *logits, int T, int E, int top_k,
                        int *n_active, int *active, int *offsets, int *tok,
                        float *tokw, void *stream);
 
+/* MoE lists (layout of fastllm_route_topk's) for S caller-chosen slots,
+ * T <= 16, S <= 256: slot s is expert cand[s] (or s when cand is null) and
+ * token t joins it with weight rw[t, expert] (dense rw [T, E], slot_coef
+ * null) or slot_coef[s, t] when that weight is nonzero.  Slots keep their
+ * order; empty slots and experts outside [0, E) are dropped.  Capacities:
+ * active[S], offsets[S+1], tok/tokw[S*T].
+ * Replaces: the active-expert scan of fused_moe_weighted
+ * (fastllm_py/kernels/moe_int4.py:263-294) and the (eidx, rw) inputs of
+ * fused_moe_ffn2 (:372-396). */
+int fastllm_moe_build_lists(const float *rw, const float *slot_coef,
+                            const int *cand, int T, int E, int S,
+                            int *n_active, int *active, int *offsets,
+                            int *tok, float *tokw, void *stream);
+
+/* Row-major INT4 (qweight u8 [rows, in_f/2], scales/zeros fp16
+ * [rows, in_f/group]) -> the fused MoE's tile layout: qtile u8
+ * [rows/16, in_f/128, 1024] (block (R/16, kb) holds at byte 16*(c + 16*q)
+ * the row-major bytes [64*kb + 16*q, +16) of row 16*(R/16) + c) and sz u32
+ * [rows/16, in_f/group, 16] (scale bits | zero bits << 16).  rows % 16 == 0,
+ * in_f % 128 == 0.  fastllm_moe_int4_tile_unpack is the exact inverse.
+ * Replaces: the layout step of build_stacked_experts
+ * (fastllm_py/kernels/moe_int4.py:116-133); the reference's kernels read
+ * the row-major arrays directly. */
+int fastllm_moe_int4_tile_repack(const uint8_t *qweight, const void *scales,
+                                 const void *zeros, uint8_t *qtile,
+                                 uint32_t *sz, long rows, int in_f,
+                                 int group_size, void *stream);
+int fastllm_moe_int4_tile_unpack(const uint8_t *qtile, const uint32_t *sz,
+                                 uint8_t *qweight, void *scales, void *zeros,
+                                 long rows, int in_f, int group_size,
+                                 void *stream);
+
+/* Bytes of device workspace fastllm_moe_int4_fused needs for this shape
+ * (0 when the shape is unsupported). */
+size_t fastllm_moe_int4_workspace_bytes(int T, int hidden, int inter,
+                                        int shared_inter, int max_entries);
+
 /* Fused selective INT4 MoE FFN for T <= 16 tokens (x fp32 [T, hidden],
- * hidden % 128 == 0, hidden <= 2048):
- *   y[t] = sum_s coef(s, t) * down_e(silu(gate_e x_t) * up_e x_t)
+ * hidden % 128 == 0, hidden <= 4096, inter <= 8192):
+ *   y[t] = sum_{entries p of t} tokw[p] * down_e(silu(gate_e x_t) * up_e x_t)
  *          + shared_coef[t] * shared(x_t)          (y fp32 [T, hidden])
- * over the slots s < n_active (device count) or host_active (when n_active
- * is null) with expert ids active[s]; coef(s, t) = rw[t, active[s]] (dense
- * rw [T, E]) or slot_coef[s, t].  Experts in the row-major INT4 stacked
- * format: gq/gs/gz, uq/us/uz (E, inter, hidden/2 | hidden/group), dq/ds/dz
- * (E, hidden, inter/2 | inter/group); shared expert the same with E = 1 and
- * shared_inter (0 = none; shared_coef null = 1).  inter_buf: fp16 scratch of
- * (max_active + 1) * T * inter_pad elements, inter_pad >= max(inter,
- * shared_inter).  Two launches (gate/up+SwiGLU, down+combine), fixed
- * combine order, no atomics.
+ * driven by MoE lists (fastllm_route_topk / fastllm_moe_build_lists) with at
+ * most max_slots slots and max_entries entries.  Experts in the tile layout
+ * (fastllm_moe_int4_tile_repack of the stacked row-major arrays): gq/gsz,
+ * uq/usz over rows E*inter, in_f hidden; dq/dsz over rows E*hidden, in_f
+ * inter; the shared expert the same with E = 1 and shared_inter (0 = none;
+ * shared_coef null = 1).  workspace: fastllm_moe_int4_workspace_bytes(T,
+ * hidden, inter, shared_inter, max_entries) bytes, 16-byte aligned; calls
+ * sharing one workspace must not overlap.  Two launches: gate/up + SwiGLU
+ * over the routed tokens only (also zeroes y); down projection adding each
+ * term into y with fp32 atomics, as the reference's moew_down does (the
+ * last bits of y depend on the order of arrival).
  * Replaces: fused_moe_weighted (fastllm_py/kernels/moe_int4.py:175-294),
  * fused_moe_ffn2 (:300-396), fused_moe_ffn (:402-487) and the routed+shared
  * part of _moe_branch (fastllm_py/graph_decode.py:688-699). */
 int fastllm_moe_int4_fused(const float *x, int T, int hidden, int group_size,
-                           int E, int inter, const uint8_t *gq, const void *gsc,
-                           const void *gz, const uint8_t *uq, const void *usc,
-                           const void *uz, const uint8_t *dq, const void *dsc,
-                           const void *dz, int shared_inter, const uint8_t *sgq,
-                           const void *sgs, const void *sgz,
-                           const uint8_t *suq, const void *sus,
-                           const void *suz, const uint8_t *sdq,
-                           const void *sds, const void *sdz,
+                           int E, int inter, const uint8_t *gq,
+                           const uint32_t *gsz, const uint8_t *uq,
+                           const uint32_t *usz, const uint8_t *dq,
+                           const uint32_t *dsz, int shared_inter,
+                           const uint8_t *sgq, const uint32_t *sgsz,
+                           const uint8_t *suq, const uint32_t *susz,
+                           const uint8_t *sdq, const uint32_t *sdsz,
                            const float *shared_coef, const int *n_active,
-                           int host_active, const int *active, int max_active,
-                           const float *rw, const float *slot_coef,
-                           void *inter_buf, int inter_pad, float *y,
-                           void *stream);
+                           const int *active, const int *offsets,
+                           const int *tok, const float *tokw, int max_slots,
+                           int max_entries, void *workspace,
+                           size_t workspace_bytes, float *y, void *stream);
 
 #ifdef __cplusplus
 }

@@ -262,6 +262,23 @@ def dequantize_int4_rowmajor(packed, scales, zeros, gs: int = 128):
 
 
 # ------------------------------------------------------------------ matmuls
+def moe_tile_pack(packed, scales, zeros):
+    """Row-major INT4 (rows, in/2) u8 + (rows, G) fp16 scales/zeros -> the
+    fused MoE tile layout of this library (no reference counterpart: the
+    reference's kernels read the row-major arrays): qtile (rows/16, in/128,
+    1024) u8 with qtile[t, kb, 16 * (c + 16 q) + b] = packed[16 t + c,
+    64 kb + 16 q + b]; sz (rows/16, G, 16) u32 = scale bits | zero bits << 16
+    of row 16 t + c."""
+    rows, half = packed.shape
+    q = np.asarray(packed, np.uint8).reshape(rows // 16, 16, half // 64, 4, 16)
+    qt = q.transpose(0, 2, 3, 1, 4).reshape(rows // 16, half // 64, 1024)
+    sb = np.asarray(scales, np.float16).view(np.uint16).astype(np.uint32)
+    zb = np.asarray(zeros, np.float16).view(np.uint16).astype(np.uint32)
+    G = sb.shape[1]
+    sz = (sb | (zb << 16)).reshape(rows // 16, 16, G).transpose(0, 2, 1)
+    return np.ascontiguousarray(qt), np.ascontiguousarray(sz)
+
+
 def matmul_ref(x, w_hat):
     """fp32 x @ w_hat.T (the reference tests' dequantize-then-matmul)."""
     return np.asarray(x, dtype=F32) @ np.asarray(w_hat, dtype=F32).T

@@ -17,7 +17,7 @@ def declared_symbols():
     for h in glob.glob(os.path.join(ROOT, "include", "*.h")):
         text = open(h).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-        for m in re.finditer(r"^\s*(?:bool|int|void|float)\s+\**\s*(\w+)\s*\(", text, flags=re.M):
+        for m in re.finditer(r"^\s*(?:bool|int|void|float|size_t)\s+\**\s*(\w+)\s*\(", text, flags=re.M):
             names.append(m.group(1))
     return names
 
@@ -38,3 +38,31 @@ def test_library_exports_every_declared_symbol():
 
 def test_python_binding_table_matches_header():
     assert set(_native.SIGNATURES) == set(declared_symbols())
+
+
+def test_moe_entry_argument_checks():
+    """Shape/argument validation of the fused-MoE entry points runs before any
+    device call: valid arguments reach the device check (rc 2 without a GPU,
+    or launch on one), invalid ones return 1.  Fake aligned pointers only."""
+    lib = _native.lib()
+    p = 1 << 20  # never dereferenced: validation fails or stops at the device check
+    ws = lib.fastllm_moe_int4_workspace_bytes(1, 2048, 1408, 5632, 4)
+    assert ws == (4 + 1) * 5632 * 2
+    assert lib.fastllm_moe_int4_workspace_bytes(17, 2048, 1408, 0, 4) == 0
+    assert lib.fastllm_moe_int4_workspace_bytes(1, 2000, 1408, 0, 4) == 0
+
+    def fused(T=1, hidden=2048, gs=128, inter=1408, sinter=5632, ws_bytes=ws, slots=4, entries=4):
+        sh = [p] * 6 if sinter else [None] * 6
+        return lib.fastllm_moe_int4_fused(p, T, hidden, gs, 60, inter, *([p] * 6), sinter, *sh,
+                                          None, p, p, p, p, p, slots, entries, p, ws_bytes, p, None)
+
+    import torch
+    if not torch.cuda.is_available():
+        assert fused() == 2
+    assert fused(gs=96) == 1
+    assert fused(hidden=2000) == 1
+    assert fused(ws_bytes=ws - 1) == 1
+    assert fused(slots=0) == 1
+    assert fused(T=17) == 1
+    assert lib.fastllm_moe_int4_tile_repack(p, p, p, p, p, 24, 256, 128, None) == 1  # rows % 16
+    assert lib.fastllm_moe_int4_tile_repack(p, p, p, p, p, 32, 200, 128, None) == 1  # in % 128

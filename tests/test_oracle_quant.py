@@ -221,3 +221,23 @@ def test_marlin_permutation_brute_force():
     want = (q.reshape(N, G, gs).astype(np.float32) - zero[:, :, None]) * \
         scale.astype(np.float16).astype(np.float32)[:, :, None]
     np.testing.assert_array_equal(deq, want.reshape(N, G * gs))
+
+
+def test_moe_tile_pack_brute_force():
+    """The MoE tile layout's reshape/transpose against its per-byte definition
+    (lane c + 16 q of block (t, kb) holds row 16 t + c, bytes 64 kb + 16 q ..)."""
+    rng = np.random.default_rng(11)
+    rows, in_f, gs = 32, 256, 64
+    packed = rng.integers(0, 256, size=(rows, in_f // 2)).astype(np.uint8)
+    sc = (rng.random((rows, in_f // gs)) + 0.5).astype(np.float16)
+    ze = rng.integers(0, 16, size=(rows, in_f // gs)).astype(np.float16)
+    qt, sz = Q.moe_tile_pack(packed, sc, ze)
+    assert qt.shape == (rows // 16, in_f // 128, 1024) and sz.shape == (rows // 16, in_f // gs, 16)
+    for R in range(rows):
+        for j in range(in_f // 2):
+            kb, q, b = j // 64, (j % 64) // 16, j % 16
+            assert qt[R // 16, kb, 16 * (R % 16 + 16 * q) + b] == packed[R, j]
+        for g in range(in_f // gs):
+            v = int(sz[R // 16, g, R % 16])
+            assert v & 0xFFFF == int(sc[R, g].view(np.uint16))
+            assert v >> 16 == int(ze[R, g].view(np.uint16))
