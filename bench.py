@@ -34,6 +34,10 @@ for _p in (ROOT, os.path.join(ROOT, "fastllm-py_amd")):
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the roofline kernel measured with rocprofv3 --pmc
+# FETCH_SIZE / WRITE_SIZE (x2.000 / x1.000 copy-kernel calibration); see
+# profiles/int4_gemv_gate_up_qwen3_8b_m1_traffic.md.  Keyed by (kernel, M).
+MEASURED_TRAFFIC = {("int4_gemv_nb<2,4,false,true>", 1): 56_860_672}
 QWEN3_8B = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096),
             ("down", 4096, 12288)]
 FP8_SHAPES = [("2048x2048", 2048, 2048), ("10944x2048", 10944, 2048), ("2048x10944", 2048, 10944)]
@@ -283,6 +287,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ms", default="1,4,8,16")
     ap.add_argument("--only", default="int4,fp8,moe")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first copy a 64 MiB buffer 5 times (a known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
@@ -296,6 +303,14 @@ def main():
     lib = nat.load()
     torch.cuda.init()
     stream = torch.cuda.Stream()
+    if args.calib_copy:
+        src = torch.ones(16 * 2 ** 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration copy: 5 x 64 MiB (67108864 B read + written per launch)")
+        del src, dst
     only = set(args.only.split(","))
     breakdown = {}
 
@@ -337,9 +352,11 @@ def main():
     bpl = marlin_bytes(M0, 24576, 4096)
     dur_us = head["us_per_call"]["gate_up"]
     achieved = bpl / (dur_us * 1e-6) / 1e9
+    kname = "int4_gemv_nb<2,4,false,true>"
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": f"int4_gemv_nb<2,4,false,true> (gate_up 24576x4096, M={M0})",
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": MEASURED_TRAFFIC.get((kname, M0)),
+                "kernel": f"{kname} (gate_up 24576x4096, M={M0})",
                 "bytes_per_launch": int(bpl), "us_per_launch": round(dur_us, 3)}
 
     cpu = None
