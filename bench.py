@@ -240,6 +240,46 @@ def run_moe(torch, lib, stream, T_list=(1, 16)):
     return res
 
 
+# ----------------------------------------------------------- prefill GEMM
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def run_gemm_prefill(torch, lib, stream, M=512, N=8192, K=2048):
+    """Config 5's dense INT4 GEMM on the matrix cores: M=512 fp16 rows against an
+    8192x2048 INT4 g128 Marlin-format weight (rotated through HBM)."""
+    from fastllm_py.moe import quantize_marlin_matrix_device
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5000)
+    W = torch.randn((N, K), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+    base = quantize_marlin_matrix_device(W, GS)
+    del W
+    n = copies_for(marlin_bytes(0, N, K))
+    cps = [base] + [{f: v.clone() for f, v in base.items()} for _ in range(n - 1)]
+    x = torch.randn((M, K), generator=gen, device="cuda").to(torch.float16)
+    y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    fn = lib.FastllmCudaMarlinHalfInt4GemmStream
+
+    def mk(p):
+        args = (x.data_ptr(), p["qweight"].data_ptr(), p["scales"].data_ptr(),
+                p["zeros"].data_ptr(), y.data_ptr(), M, N, K, GS, None)
+
+        def go(h):
+            if not fn(*args, h):
+                raise RuntimeError("INT4 GEMM rejected")
+        return go
+    rounds = max(1, -(-64 // n))
+    seq = [mk(p) for _ in range(rounds) for p in cps]
+    us = graph_time(torch, stream, seq, 4) / len(seq) * 1e3
+    flops = 2.0 * M * N * K
+    tflops = flops / (us * 1e-6) / 1e12
+    del cps
+    torch.cuda.empty_cache()
+    return {"shape": f"M{M} N{N} K{K}", "us_per_call": round(us, 3), "TFLOP/s": round(tflops, 1),
+            "mfma_util_fp16_dense": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "weight_GB/s": round(marlin_bytes(M, N, K) / us / 1e3, 1)}
+
+
 # ------------------------------------------------------------- CPU baseline
 def cpu_baseline_int4(budget_s=15.0):
     """The reference's CPU semantics through the numpy oracle: per call,
@@ -286,7 +326,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--only", default="int4,fp8,moe")
+    ap.add_argument("--only", default="int4,fp8,moe,gemm")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy a 64 MiB buffer 5 times (a known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -338,6 +378,9 @@ def main():
     del layers
     torch.cuda.empty_cache()
 
+    if "gemm" in only:
+        breakdown["int4_gemm_prefill"] = run_gemm_prefill(torch, lib, stream)
+        log(f"GEMM: {breakdown['int4_gemm_prefill']}")
     if "fp8" in only:
         breakdown["fp8_b128x128_bf16"] = run_fp8(torch, lib, stream)
         log(f"FP8: {breakdown['fp8_b128x128_bf16']}")

@@ -467,6 +467,190 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
     }
 }
 
+// Prefill-shaped GEMM (M > 64, K % 128 == 0) on the matrix cores.
+//
+// Workgroup tile 128 x 128, four waves in a 2 x 2 arrangement, wave tile
+// 64 x 64 (4 m-tiles x 4 n-tiles of 16 x 16 fp32 accumulators).  Per 128-k
+// block:
+//   * the 128 x 128 fp16 activation tile is staged in LDS (row stride 136
+//     halves: the 16 rows a ds_read_b128 gathers then start 4 banks apart),
+//     double-buffered, with the global loads of block kb+1 issued before the
+//     MFMAs of block kb;
+//   * each wave reads its 4 n-tiles' weights straight from the tile layout
+//     into MFMA B-operand registers (one 16-byte load per lane per n-tile,
+//     also issued a block ahead) and dequantizes them in registers:
+//     (q - z) exactly in fp16, times the fp16 group scale (the B operand is
+//     s * (q - z) rounded to fp16, as a Marlin kernel feeds its tensor cores);
+//   * 64 v_mfma_f32_16x16x32_f16 per wave accumulate in fp32.
+// Rows >= M read row M-1 and are not stored; n-tiles >= N read the last
+// n-tile and are not stored.
+// Workgroup-to-tile order: the hardware deals workgroup b to XCD b % 8, so
+// when the tile count is a multiple of 8 the tiles of one XCD are a
+// contiguous run in (n-block major, m-block minor) order, and the m-blocks
+// that share a weight strip share one L2.
+constexpr int kGemmBM = 128, kGemmBN = 128, kGemmLda = 136;
+constexpr int kGemmMfmaMinM = 64;  // M above this takes the MFMA GEMM
+
+FL_DEV f16x8 dequant_word_scaled(uint32_t w, uint32_t zlo, uint32_t zhi, f16x2 s2) {
+    const uint32_t w8 = w >> 8;
+    const f16x2 p0 = (bitcast<f16x2>(and_or(w, 0x000F000Fu, 0x64006400u)) + bitcast<f16x2>(zlo)) * s2;
+    const f16x2 p1 = (bitcast<f16x2>(and_or(w, 0x00F000F0u, 0x54005400u)) + bitcast<f16x2>(zhi)) * s2;
+    const f16x2 p2 = (bitcast<f16x2>(and_or(w8, 0x000F000Fu, 0x64006400u)) + bitcast<f16x2>(zlo)) * s2;
+    const f16x2 p3 = (bitcast<f16x2>(and_or(w8, 0x00F000F0u, 0x54005400u)) + bitcast<f16x2>(zhi)) * s2;
+    const u32x4 r{bitcast<uint32_t>(p0), bitcast<uint32_t>(p1), bitcast<uint32_t>(p2),
+                  bitcast<uint32_t>(p3)};
+    return bitcast<f16x8>(r);
+}
+
+template <bool G32>
+__global__ __launch_bounds__(256) void int4_gemm_mfma(
+    const f16* __restrict__ A, const uint32_t* __restrict__ Wq, const uint16_t* __restrict__ S,
+    const uint32_t* __restrict__ Z, f16* __restrict__ C, int M, int N, int K) {
+    constexpr int SPB = G32 ? 4 : 1;
+    __shared__ __align__(16) f16 As[2][kGemmBM * kGemmLda];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int col = lane & 15, kq = lane >> 4;
+    const int nkb = K >> 7;
+    const int zwords = N >> 3;
+    const int ntiles = N >> 4;
+
+    // tile of this workgroup (XCD-grouped order when it divides evenly)
+    const int nblk = (N + kGemmBN - 1) / kGemmBN, mblk = (M + kGemmBM - 1) / kGemmBM;
+    const int total = nblk * mblk;
+    int lin = blockIdx.x;
+    if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+    const int nb_i = lin / mblk, mb_i = lin - nb_i * mblk;
+    const int m0 = mb_i * kGemmBM;
+    const int nt0 = nb_i * (kGemmBN / 16) + wn * 4;  // first n-tile of this wave
+
+    // weight tile bases and scale/zero positions of the wave's 4 n-tiles
+    const uint32_t* tb[4];
+    int spos[4], zw[4], zsh[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        int nt = nt0 + t;
+        nt = nt < ntiles ? nt : ntiles - 1;
+        tb[t] = Wq + (size_t)nt * (2 * (size_t)K) + lane * 4;
+        const int n = nt * 16 + col;
+        spos[t] = marlin_scale_pos(n);
+        const int cl = n & 63;
+        zw[t] = ((n >> 6) << 3) + (cl & 7);
+        zsh[t] = 4 * slot_of(cl >> 3);
+    }
+
+    // activation staging: thread moves 8 chunks of 8 halves per block
+    const f16* arow_g[8];
+    int lds_off[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int c = threadIdx.x + 256 * i;
+        const int r = c >> 4, c16 = c & 15;
+        int m = m0 + r;
+        m = m < M ? m : M - 1;
+        arow_g[i] = A + (size_t)m * K + c16 * 8;
+        lds_off[i] = r * kGemmLda + c16 * 8;
+    }
+
+    f16x8 ra[8];
+    u32x4 wv[4];
+    uint32_t sv[4][SPB], zv[4][SPB];
+    auto load_block = [&](int kb) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ra[i] = *reinterpret_cast<const f16x8*>(arow_g[i] + kb * 128);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            wv[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tb[t] + kb * 256));
+#pragma unroll
+            for (int g = 0; g < SPB; ++g) {
+                const size_t grp = (size_t)kb * SPB + g;
+                sv[t][g] = S[grp * N + spos[t]];
+                zv[t][g] = Z[grp * zwords + zw[t]];
+            }
+        }
+    };
+
+    f32x4 acc[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    load_block(0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) *reinterpret_cast<f16x8*>(&As[0][lds_off[i]]) = ra[i];
+    __syncthreads();
+
+    const int arow_l = (wm * 64 + col) * kGemmLda + 8 * kq;
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int cur = kb & 1;
+        // this block's weights and scales leave the prefetch registers
+        u32x4 wc[4];
+        uint32_t sc[4][SPB], zc[4][SPB];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            wc[t] = wv[t];
+#pragma unroll
+            for (int g = 0; g < SPB; ++g) {
+                sc[t][g] = sv[t][g];
+                zc[t][g] = zv[t][g];
+            }
+        }
+        if (kb + 1 < nkb) load_block(kb + 1);
+
+        const f16* as = &As[cur][arow_l];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f16x8 a[4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+                a[mt] = *reinterpret_cast<const f16x8*>(as + mt * 16 * kGemmLda + 32 * j);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int g = G32 ? j : 0;
+                uint32_t zlo, zhi;
+                zero_bits((zc[t][g] >> zsh[t]) & 0xFu, zlo, zhi);
+                const f16 s = bitcast<f16>((uint16_t)sc[t][g]);
+                const f16x8 b = dequant_word_scaled(wc[t][j], zlo, zhi, f16x2{s, s});
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) acc[mt][t] = mfma_f16(a[mt], b, acc[mt][t]);
+            }
+        }
+        if (kb + 1 < nkb) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) *reinterpret_cast<f16x8*>(&As[cur ^ 1][lds_off[i]]) = ra[i];
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const int nt = nt0 + t;
+        if (nt >= ntiles) continue;
+        const int n = nt * 16 + col;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = m0 + wm * 64 + mt * 16 + 4 * kq + e;
+                if (m < M) C[(size_t)m * N + n] = (f16)acc[mt][t][e];
+            }
+    }
+}
+
+hipError_t launch_gemm_mfma(const f16* A, const uint32_t* Wq, const uint16_t* S, const uint32_t* Z,
+                            f16* C, int M, int N, int K, bool g32, hipStream_t stream) {
+    const int tiles = ((N + kGemmBN - 1) / kGemmBN) * ((M + kGemmBM - 1) / kGemmBM);
+    if (g32)
+        hipLaunchKernelGGL((int4_gemm_mfma<true>), dim3(tiles), dim3(256), 0, stream, A, Wq, S, Z,
+                           C, M, N, K);
+    else
+        hipLaunchKernelGGL((int4_gemm_mfma<false>), dim3(tiles), dim3(256), 0, stream, A, Wq, S, Z,
+                           C, M, N, K);
+    return hipGetLastError();
+}
+
 struct GemvCfg {
     int tiles;  // n-tiles (16 columns) per workgroup: 1 or 2
     int waves;  // waves per workgroup, 1..16
@@ -631,6 +815,10 @@ bool int4_marlin_abi_gemm(const void* a, const uint32_t* q, const void* scales,
     const bool g32 = group_size == 32;
     const f16* A = static_cast<const f16*>(a);
     f16* Cp = static_cast<f16*>(c);
+    if (M > kGemmMfmaMinM && K % 128 == 0)
+        return report(launch_gemm_mfma(A, q, static_cast<const uint16_t*>(scales), zeros, Cp, M, N,
+                                       K, g32, stream),
+                      "FastllmCudaMarlinHalfInt4Gemm");
     if (M > 16)
         return int4_gemm_large_m(A, q, static_cast<const f16*>(scales), zeros, Cp, M, N, K, g32,
                                  stream);

@@ -110,7 +110,27 @@ def test_gemm_parity_larger_m(torch_gpu, M):
     assert Q.max_abs_rel(out.float().cpu().numpy(), ref) < TOL
 
 
-@pytest.mark.parametrize("M", [1, 16])
+# prefill shapes on the MFMA GEMM (M > 64): config 5's dense 8192x2048 at
+# M=512, ragged M and N (N % 128 == 64), group 32
+@pytest.mark.parametrize("M,K,N,gs", [(512, 2048, 8192, 128), (65, 1024, 576, 128),
+                                      (200, 2048, 1408, 128), (129, 512, 192, 32),
+                                      (300, 768, 2048, 128), (256, 1024, 1024, 32)])
+def test_gemm_mfma_parity(torch_gpu, M, K, N, gs):
+    from fastllm_py.kernels import marlin
+
+    torch = torch_gpu
+    rng = np.random.default_rng(5000 + M + K + N + gs)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    pay, w_hat, _ = _prep(torch, W, gs)
+    out = marlin.marlin_gemm_int4(torch.from_numpy(a).cuda(), pay["qweight"], pay["scales"],
+                                  pay["zeros"])
+    ref = Q.matmul_ref(a.astype(np.float32), w_hat)
+    err = Q.max_abs_rel(out.float().cpu().numpy(), ref)
+    assert err < TOL, err
+
+
+@pytest.mark.parametrize("M", [1, 16, 256])
 def test_stream_entry_bit_identical(torch_gpu, M):
     # reference tests/test_native_kernels.py:132-154
     from fastllm_py.kernels import marlin
