@@ -469,27 +469,44 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
 
 // Prefill-shaped GEMM (M > 64, K % 128 == 0) on the matrix cores.
 //
-// Workgroup tile 128 x 128, four waves in a 2 x 2 arrangement, wave tile
-// 64 x 64 (4 m-tiles x 4 n-tiles of 16 x 16 fp32 accumulators).  Per 128-k
-// block:
-//   * the 128 x 128 fp16 activation tile is staged in LDS (row stride 136
-//     halves: the 16 rows a ds_read_b128 gathers then start 4 banks apart),
-//     double-buffered, with the global loads of block kb+1 issued before the
-//     MFMAs of block kb;
-//   * each wave reads its 4 n-tiles' weights straight from the tile layout
-//     into MFMA B-operand registers (one 16-byte load per lane per n-tile,
-//     also issued a block ahead) and dequantizes them in registers:
-//     (q - z) exactly in fp16, times the fp16 group scale (the B operand is
-//     s * (q - z) rounded to fp16, as a Marlin kernel feeds its tensor cores);
-//   * 64 v_mfma_f32_16x16x32_f16 per wave accumulate in fp32.
+// Workgroup tile 64 (m) x 256 (n): eight waves side by side along n, each
+// with a 64 x 32 wave tile (4 m-tiles x 2 n-tiles of 16 x 16 fp32
+// accumulators), two waves per SIMD so one wave's dequantization overlaps
+// the other's MFMAs.  The tile shape follows from traffic: a 128-k block
+// brings 256 B per activation row (fp16) but 64 B per weight column (int4),
+// so 64 x 256 moves 2 B of L2 traffic per output element and block where
+// 128 x 128 moves 2.5, and the workgroup reuses its A rows 256 times.
+// Every main-loop global load goes straight to LDS (buffer_load ... lds), so
+// nothing in the loop waits on a VGPR load: kGemmAhead blocks are in flight
+// into a ring of kGemmAhead + 1 LDS stages, and one vmcnt wait plus one
+// barrier per block hand a finished stage to all waves.  A stage holds, for
+// one 128-k block:
+//   * A  (16 KB): the 64 x 128 fp16 activation tile, fragment-major -- the
+//     1 KB of (m-tile, 32-k step j) holds lane l's MFMA A operand at 16 l,
+//     so every ds_read_b128 is linear and conflict-free;
+//   * B  (16 KB): the 16 n-tiles' 1 KB tile-layout blocks as they lie;
+//   * S  (2 KB): per group row of the block, the strip's 256 fp16 scales
+//     (Marlin positions 256 nb .. 256 nb + 255; the permutation stays inside
+//     64-column chunks);
+//   * Z  (1 KB): per group row, the strip's 32 packed zero words.
+// B is dequantized in registers: (q - z) exactly in fp16, times the fp16
+// group scale (the B operand is s * (q - z) rounded to fp16, as a Marlin
+// kernel feeds its tensor cores); 32 v_mfma_f32_16x16x32_f16 per wave and
+// block accumulate in fp32.
 // Rows >= M read row M-1 and are not stored; n-tiles >= N read the last
-// n-tile and are not stored.
+// n-tile and are not stored; blocks past the end re-read the last block
+// with a zero scale (uniform load counts and trip structure).
 // Workgroup-to-tile order: the hardware deals workgroup b to XCD b % 8, so
 // when the tile count is a multiple of 8 the tiles of one XCD are a
 // contiguous run in (n-block major, m-block minor) order, and the m-blocks
 // that share a weight strip share one L2.
-constexpr int kGemmBM = 128, kGemmBN = 128, kGemmLda = 136;
-constexpr int kGemmMfmaMinM = 64;  // M above this takes the MFMA GEMM
+constexpr int kGemmBM = 64, kGemmBN = 256;
+constexpr int kGemmMfmaMinM = 64;   // M above this takes the MFMA GEMM
+constexpr int kGemmAhead = 3;       // blocks in flight ahead of the one computed
+constexpr int kGemmStages = kGemmAhead + 1;
+constexpr int kStA = 0, kStB = 16384, kStS = kStB + 16384, kStZ = kStS + 2048;
+constexpr int kStageBytes = kStZ + 1024;
+constexpr size_t kGemmLds = (size_t)kGemmStages * kStageBytes;
 
 FL_DEV f16x8 dequant_word_scaled(uint32_t w, uint32_t zlo, uint32_t zhi, f16x2 s2) {
     const uint32_t w8 = w >> 8;
@@ -502,138 +519,194 @@ FL_DEV f16x8 dequant_word_scaled(uint32_t w, uint32_t zlo, uint32_t zhi, f16x2 s
     return bitcast<f16x8>(r);
 }
 
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] and
+// vmcnt[5:4] at bits 15:14; expcnt and lgkmcnt left at their maxima).
+template <int N>
+FL_DEV void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+typedef void __attribute__((address_space(3)))* lptr_t;
+
+// Raw buffer resource over [base, base + bytes) (gfx9 descriptor, dword 3 =
+// 0x00020000): loads take a 32-bit per-lane offset plus a wave-uniform SGPR
+// offset, so the per-block address step is one scalar add.
+FL_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
 template <bool G32>
-__global__ __launch_bounds__(256) void int4_gemm_mfma(
+__global__ __launch_bounds__(512) void int4_gemm_mfma(
     const f16* __restrict__ A, const uint32_t* __restrict__ Wq, const uint16_t* __restrict__ S,
     const uint32_t* __restrict__ Z, f16* __restrict__ C, int M, int N, int K) {
-    constexpr int SPB = G32 ? 4 : 1;
-    __shared__ __align__(16) f16 As[2][kGemmBM * kGemmLda];
+    constexpr int D = kGemmAhead, NS = kGemmStages;
+    constexpr int SPB = G32 ? 4 : 1;  // group rows per block
+    // DMA loads per block and wave: 2 A fragments, 2 B tiles, 2 scale/zero
+    // pieces (3 * SPB pieces are needed; waves past them repeat one)
+    constexpr int LPB = 2 + 2 + 2;
+    extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
     const int col = lane & 15, kq = lane >> 4;
     const int nkb = K >> 7;
     const int zwords = N >> 3;
     const int ntiles = N >> 4;
+    const int G = K / (G32 ? 32 : 128);
 
-    // tile of this workgroup (XCD-grouped order when it divides evenly)
     const int nblk = (N + kGemmBN - 1) / kGemmBN, mblk = (M + kGemmBM - 1) / kGemmBM;
     const int total = nblk * mblk;
     int lin = blockIdx.x;
     if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
     const int nb_i = lin / mblk, mb_i = lin - nb_i * mblk;
     const int m0 = mb_i * kGemmBM;
-    const int nt0 = nb_i * (kGemmBN / 16) + wn * 4;  // first n-tile of this wave
+    const int nt_base = nb_i * 16;
 
-    // weight tile bases and scale/zero positions of the wave's 4 n-tiles
-    const uint32_t* tb[4];
-    int spos[4], zw[4], zsh[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        int nt = nt0 + t;
-        nt = nt < ntiles ? nt : ntiles - 1;
-        tb[t] = Wq + (size_t)nt * (2 * (size_t)K) + lane * 4;
-        const int n = nt * 16 + col;
-        spos[t] = marlin_scale_pos(n);
-        const int cl = n & 63;
-        zw[t] = ((n >> 6) << 3) + (cl & 7);
-        zsh[t] = 4 * slot_of(cl >> 3);
-    }
+    const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)M * K * 2);
+    const __amdgpu_buffer_rsrc_t rW = buf_rsrc(Wq, (uint32_t)N * K / 2);
+    const __amdgpu_buffer_rsrc_t rS = buf_rsrc(S, (uint32_t)G * N * 2);
+    const __amdgpu_buffer_rsrc_t rZ = buf_rsrc(Z, (uint32_t)G * zwords * 4);
 
-    // activation staging: thread moves 8 chunks of 8 halves per block
-    const f16* arow_g[8];
-    int lds_off[8];
+    // DMA sources of this wave: A fragments f = 2 wave + i (f = 4 m-tile + j)
+    // and B n-tiles 2 wave + i of the strip
+    uint32_t ao[2], bo[2];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int c = threadIdx.x + 256 * i;
-        const int r = c >> 4, c16 = c & 15;
-        int m = m0 + r;
+    for (int i = 0; i < 2; ++i) {
+        const int f = wave * 2 + i;
+        int m = m0 + 16 * (f >> 2) + col;
         m = m < M ? m : M - 1;
-        arow_g[i] = A + (size_t)m * K + c16 * 8;
-        lds_off[i] = r * kGemmLda + c16 * 8;
+        ao[i] = 2u * ((uint32_t)m * K + 32 * (f & 3) + 8 * kq);
+        int nt = nt_base + wave * 2 + i;
+        nt = nt < ntiles ? nt : ntiles - 1;
+        bo[i] = (uint32_t)nt * (8u * K) + lane * 16;
+    }
+    // scale/zero pieces: piece p < 3 SPB is (row g = p / 3, part p % 3):
+    // parts 0, 1 = scale positions [128 part, +128) of the strip (64 lanes x
+    // 4 B), part 2 = the strip's 32 zero words (lanes 32..63 repeat them).
+    // Wave w moves pieces 2 w and 2 w + 1 (modulo 3 SPB).
+    uint32_t pvo[2], prow_bytes[2], pgrp[2];
+    int pdst[2];
+    bool pis_s[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int p = (wave * 2 + i) % (3 * SPB);
+        const int g = p / 3, part = p % 3;
+        pgrp[i] = g;
+        pis_s[i] = part < 2;
+        if (part < 2) {
+            int q = nb_i * 256 + part * 128 + 2 * lane;
+            q = q < N ? q : N - 2;
+            pvo[i] = 2u * q;
+            prow_bytes[i] = 2u * N;
+            pdst[i] = kStS + g * 512 + part * 256;
+        } else {
+            int w = nb_i * 32 + (lane & 31);
+            w = w < zwords ? w : zwords - 1;
+            pvo[i] = 4u * w;
+            prow_bytes[i] = 4u * zwords;
+            pdst[i] = kStZ + g * 256;
+        }
     }
 
-    f16x8 ra[8];
-    u32x4 wv[4];
-    uint32_t sv[4][SPB], zv[4][SPB];
-    auto load_block = [&](int kb) {
+    auto issue = [&](int kb, int slot) {
+        kb = kb < nkb ? kb : nkb - 1;
+        unsigned char* st = smem + (size_t)slot * kStageBytes;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) ra[i] = *reinterpret_cast<const f16x8*>(arow_g[i] + kb * 128);
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(st + kStA + (wave * 2 + i) * 1024),
+                                                     16, ao[i], kb * 256, 0, 0);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            wv[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tb[t] + kb * 256));
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, (lptr_t)(st + kStB + (wave * 2 + i) * 1024),
+                                                     16, bo[i], kb * 1024, 0, 0);
 #pragma unroll
-            for (int g = 0; g < SPB; ++g) {
-                const size_t grp = (size_t)kb * SPB + g;
-                sv[t][g] = S[grp * N + spos[t]];
-                zv[t][g] = Z[grp * zwords + zw[t]];
-            }
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t grp = (uint32_t)kb * SPB + pgrp[i];
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(pis_s[i] ? rS : rZ, (lptr_t)(st + pdst[i]), 4,
+                                                     pvo[i], grp * prow_bytes[i], 0, 0);
         }
     };
 
-    f32x4 acc[4][4];
+    // this wave's 2 n-tiles: scale/zero positions inside the stage's rows
+    int sp[2], zp[2], zsh[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int n = (nt_base + wave * 2 + t) * 16 + col;
+        sp[t] = marlin_scale_pos(n) - nb_i * 256;
+        const int cl = n & 63;
+        zp[t] = ((n >> 6) << 3) + (cl & 7) - nb_i * 32;
+        zsh[t] = 4 * slot_of(cl >> 3);
+    }
+
+    f32x4 acc[4][2];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 2; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    load_block(0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) *reinterpret_cast<f16x8*>(&As[0][lds_off[i]]) = ra[i];
-    __syncthreads();
+    for (int d = 0; d < D; ++d) issue(d, d);
 
-    const int arow_l = (wm * 64 + col) * kGemmLda + 8 * kq;
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int cur = kb & 1;
-        // this block's weights and scales leave the prefetch registers
-        u32x4 wc[4];
-        uint32_t sc[4][SPB], zc[4][SPB];
+    const int afrag = kStA + lane * 16;
+    for (int kb0 = 0; kb0 < nkb; kb0 += NS) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            wc[t] = wv[t];
+        for (int u = 0; u < NS; ++u) {
+            const int kb = kb0 + u;
+            const f16 live = kb < nkb ? (f16)1.0f : (f16)0.0f;
+            wait_vmcnt<(D - 1) * LPB>();
+            asm volatile("s_barrier" ::: "memory");
+            issue(kb + D, (u + D) % NS);
+            const unsigned char* st = smem + (size_t)u * kStageBytes;
+            u32x4 wv[2];
+            uint32_t zl[2][SPB], zh[2][SPB];
+            f16 sc[2][SPB];
 #pragma unroll
-            for (int g = 0; g < SPB; ++g) {
-                sc[t][g] = sv[t][g];
-                zc[t][g] = zv[t][g];
+            for (int t = 0; t < 2; ++t) {
+                wv[t] = *reinterpret_cast<const u32x4*>(st + kStB + (wave * 2 + t) * 1024 + lane * 16);
+#pragma unroll
+                for (int g = 0; g < SPB; ++g) {
+                    const uint16_t sb = *reinterpret_cast<const uint16_t*>(st + kStS + g * 512 + 2 * sp[t]);
+                    const uint32_t zw = *reinterpret_cast<const uint32_t*>(st + kStZ + g * 256 + 4 * zp[t]);
+                    sc[t][g] = bitcast<f16>(sb) * live;
+                    zero_bits((zw >> zsh[t]) & 0xFu, zl[t][g], zh[t][g]);
+                }
+            }
+            const unsigned char* as = st + afrag;
+            f16x8 a[2][4];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt) a[0][mt] = *reinterpret_cast<const f16x8*>(as + mt * 4 * 1024);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (j < 3) {
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt)
+                        a[(j + 1) & 1][mt] =
+                            *reinterpret_cast<const f16x8*>(as + (mt * 4 + j + 1) * 1024);
+                }
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int g = G32 ? j : 0;
+                    const f16x8 b = dequant_word_scaled(wv[t][j], zl[t][g], zh[t][g],
+                                                        f16x2{sc[t][g], sc[t][g]});
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) acc[mt][t] = mfma_f16(a[j & 1][mt], b, acc[mt][t]);
+                }
             }
         }
-        if (kb + 1 < nkb) load_block(kb + 1);
-
-        const f16* as = &As[cur][arow_l];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            f16x8 a[4];
-#pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
-                a[mt] = *reinterpret_cast<const f16x8*>(as + mt * 16 * kGemmLda + 32 * j);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int g = G32 ? j : 0;
-                uint32_t zlo, zhi;
-                zero_bits((zc[t][g] >> zsh[t]) & 0xFu, zlo, zhi);
-                const f16 s = bitcast<f16>((uint16_t)sc[t][g]);
-                const f16x8 b = dequant_word_scaled(wc[t][j], zlo, zhi, f16x2{s, s});
-#pragma unroll
-                for (int mt = 0; mt < 4; ++mt) acc[mt][t] = mfma_f16(a[mt], b, acc[mt][t]);
-            }
-        }
-        if (kb + 1 < nkb) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) *reinterpret_cast<f16x8*>(&As[cur ^ 1][lds_off[i]]) = ra[i];
-        }
-        __syncthreads();
     }
+    wait_vmcnt<0>();  // no LDS copy may still be in flight when the workgroup ends
 
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int nt = nt0 + t;
+    for (int t = 0; t < 2; ++t) {
+        const int nt = nt_base + wave * 2 + t;
         if (nt >= ntiles) continue;
         const int n = nt * 16 + col;
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int m = m0 + wm * 64 + mt * 16 + 4 * kq + e;
+                const int m = m0 + mt * 16 + 4 * kq + e;
                 if (m < M) C[(size_t)m * N + n] = (f16)acc[mt][t][e];
             }
     }
@@ -643,11 +716,11 @@ hipError_t launch_gemm_mfma(const f16* A, const uint32_t* Wq, const uint16_t* S,
                             f16* C, int M, int N, int K, bool g32, hipStream_t stream) {
     const int tiles = ((N + kGemmBN - 1) / kGemmBN) * ((M + kGemmBM - 1) / kGemmBM);
     if (g32)
-        hipLaunchKernelGGL((int4_gemm_mfma<true>), dim3(tiles), dim3(256), 0, stream, A, Wq, S, Z,
-                           C, M, N, K);
+        hipLaunchKernelGGL((int4_gemm_mfma<true>), dim3(tiles), dim3(512), kGemmLds, stream, A, Wq,
+                           S, Z, C, M, N, K);
     else
-        hipLaunchKernelGGL((int4_gemm_mfma<false>), dim3(tiles), dim3(256), 0, stream, A, Wq, S, Z,
-                           C, M, N, K);
+        hipLaunchKernelGGL((int4_gemm_mfma<false>), dim3(tiles), dim3(512), kGemmLds, stream, A, Wq,
+                           S, Z, C, M, N, K);
     return hipGetLastError();
 }
 
