@@ -280,6 +280,59 @@ def run_gemm_prefill(torch, lib, stream, M=512, N=8192, K=2048):
             "weight_GB/s": round(marlin_bytes(M, N, K) / us / 1e3, 1)}
 
 
+def run_moe_prefill(torch, lib, stream, T=512):
+    """Config 5's grouped MoE layer (Qwen3-30B-A3B): 128 experts, hidden 2048,
+    inter 768, top-8 softmax with renormalisation from fp16 logits ~ N(0,1),
+    M=512 tokens.  Timed unit = one layer: route + gate/up + down launches;
+    HBM-bound on the routed experts' packed weights."""
+    from fastllm_py.expert_router import route_topk_device
+    from fastllm_py.kernels import moe_int4
+
+    E, hidden, inter, K = 128, 2048, 768, 8
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5100)
+
+    def layer():
+        st = {"group": 128}
+        for proj, (o, i) in (("gate", (inter, hidden)), ("up", (inter, hidden)),
+                             ("down", (hidden, inter))):
+            w = (torch.randn((E, o, i), generator=gen, device="cuda") * 0.02).half()
+            qw, sc, ze, _ = moe_int4._quantize_int4_rowmajor_batched(w, 128)
+            del w
+            st.update(moe_int4.stack_tiles(proj, qw, sc, ze, 128))
+        return st
+    expert_bytes = 3 * inter * hidden // 2 + 3 * inter * hidden // 128 * 4
+    nl = copies_for(E * expert_bytes)
+    layers = [layer() for _ in range(nl)]
+    logits = torch.randn((T, E), generator=gen, device="cuda").half().float()
+    x = torch.randn((T, hidden), generator=gen, device="cuda").half().float()
+    bufs = {}
+    route_topk_device(logits, K, norm_topk_prob=True, out=bufs)
+    torch.cuda.synchronize()
+    distinct = len(np.unique(bufs["topk_ids"].cpu().numpy()))
+    y = torch.empty((T, hidden), device="cuda")
+    ws = torch.empty((moe_int4.moe_workspace_bytes(T, hidden, inter, 0, T * K),),
+                     dtype=torch.uint8, device="cuda")
+
+    def mk(st):
+        def go(h):
+            route_topk_device(logits, K, norm_topk_prob=True, out=bufs, stream=h)
+            moe_int4.moe_forward(x, st, E, hidden, inter, bufs, max_slots=E, max_entries=T * K,
+                                 out=y, workspace=ws, stream=h)
+        return go
+    rounds = max(1, -(-16 // nl))
+    seq = [mk(st) for _ in range(rounds) for st in layers]
+    us = graph_time(torch, stream, seq, 4) / len(seq) * 1e3
+    routed = distinct * expert_bytes
+    flops = 2.0 * T * K * 3 * inter * hidden
+    del layers
+    torch.cuda.empty_cache()
+    return {"T": T, "us_per_layer": round(us, 3), "distinct_experts": distinct,
+            "routed_weight_bytes": routed, "weight_GB/s": round(routed / us / 1e3, 1),
+            "pct_of_hbm_peak": round(routed / us / 1e3 / HBM_PEAK_GBS * 100, 2),
+            "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1)}
+
+
 # ------------------------------------------------------------- CPU baseline
 def cpu_baseline_int4(budget_s=15.0):
     """The reference's CPU semantics through the numpy oracle: per call,
@@ -381,6 +434,8 @@ def main():
     if "gemm" in only:
         breakdown["int4_gemm_prefill"] = run_gemm_prefill(torch, lib, stream)
         log(f"GEMM: {breakdown['int4_gemm_prefill']}")
+        breakdown["moe_prefill_qwen3_30b_a3b_int4"] = run_moe_prefill(torch, lib, stream)
+        log(f"MoE prefill: {breakdown['moe_prefill_qwen3_30b_a3b_int4']}")
     if "fp8" in only:
         breakdown["fp8_b128x128_bf16"] = run_fp8(torch, lib, stream)
         log(f"FP8: {breakdown['fp8_b128x128_bf16']}")

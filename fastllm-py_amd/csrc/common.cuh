@@ -47,6 +47,25 @@ FL_DEV f32x4 mfma_bf16(bf16x8 a, bf16x8 b, f32x4 c) {
 
 FL_DEV float half_bits_to_float(uint16_t h) { return (float)bitcast<f16>(h); }
 
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] and
+// vmcnt[5:4] at bits 15:14; expcnt and lgkmcnt left at their maxima).
+template <int N>
+FL_DEV void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+typedef void __attribute__((address_space(3)))* lptr_t;
+
+// Raw buffer resource over [base, base + bytes) (gfx9 descriptor, dword 3 =
+// 0x00020000): loads take a 32-bit per-lane offset plus a wave-uniform SGPR
+// offset, so the per-block address step is one scalar add; offsets at or
+// past `bytes` read 0.
+FL_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
 // Host-side launch error check: returns the HIP error of the last launch.
 static inline hipError_t fl_last_error() { return hipGetLastError(); }
 

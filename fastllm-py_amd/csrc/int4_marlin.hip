@@ -24,28 +24,9 @@
 //     exponent of 1024 (bits 0-3) or of 64 (bits 4-7).
 #include "common.cuh"
 #include "device.cuh"
+#include "int4_common.cuh"
 
 namespace {
-
-// nibble slot of k-offset r inside a tile-layout u32 (and, as it happens, the
-// inverse of Marlin's zero-point interleave {0,2,4,6,1,3,5,7}).
-__host__ __device__ constexpr int slot_of(int r) {
-    return (r & 1) ? 4 + (r >> 1) : (r >> 1);
-}
-
-FL_DEV uint32_t gptq_word_to_tile_word(uint32_t w) {
-    uint32_t o = 0;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) o |= ((w >> (4 * r)) & 0xFu) << (4 * slot_of(r));
-    return o;
-}
-
-FL_DEV uint32_t tile_word_to_gptq_word(uint32_t w) {
-    uint32_t o = 0;
-#pragma unroll
-    for (int r = 0; r < 8; ++r) o |= ((w >> (4 * slot_of(r))) & 0xFu) << (4 * r);
-    return o;
-}
 
 // Position of (tile-layout u32 index o) in GPTQ coordinates: returns the
 // source word index (k/8)*N + n.
@@ -242,35 +223,6 @@ __global__ __launch_bounds__(1024) void int4_tile_mm(
         const int n = (strip * T + t) * 16 + (l & 15);
         if (m < M) C[(size_t)m * N + n] = (f16)v;
     }
-}
-
-// (a & m) | c in one VALU op.
-FL_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
-    return r;
-}
-
-// Dequantize with the zero point folded into fp16 constants: zlo = -(1024+z),
-// zhi = -(64+z) as fp16 pairs (exact), magic_lo/hi = 0x64006400 / 0x54005400.
-FL_DEV f16x8 dequant_word_fast(uint32_t w, uint32_t zlo, uint32_t zhi, uint32_t mlo,
-                               uint32_t mhi) {
-    const uint32_t w8 = w >> 8;
-    const f16x2 p0 = bitcast<f16x2>(and_or(w, 0x000F000Fu, mlo)) + bitcast<f16x2>(zlo);
-    const f16x2 p1 = bitcast<f16x2>(and_or(w, 0x00F000F0u, mhi)) + bitcast<f16x2>(zhi);
-    const f16x2 p2 = bitcast<f16x2>(and_or(w8, 0x000F000Fu, mlo)) + bitcast<f16x2>(zlo);
-    const f16x2 p3 = bitcast<f16x2>(and_or(w8, 0x00F000F0u, mhi)) + bitcast<f16x2>(zhi);
-    const u32x4 r{bitcast<uint32_t>(p0), bitcast<uint32_t>(p1), bitcast<uint32_t>(p2),
-                  bitcast<uint32_t>(p3)};
-    return bitcast<f16x8>(r);
-}
-
-// fp16-pair bit patterns of -(1024+z) and -(64+z) for a zero point z in 0..15.
-FL_DEV void zero_bits(uint32_t z, uint32_t& zlo, uint32_t& zhi) {
-    const uint32_t lo = 0xE400u | z;         // -(1024 + z): exponent 10, mantissa z
-    const uint32_t hi = 0xD400u | (z << 4);  // -(64 + z): exponent 6, ulp 1/16
-    zlo = lo | (lo << 16);
-    zhi = hi | (hi << 16);
 }
 
 // Decode-shaped GEMV (M <= 16): one 16-row m-tile, W waves per workgroup on a
@@ -517,24 +469,6 @@ FL_DEV f16x8 dequant_word_scaled(uint32_t w, uint32_t zlo, uint32_t zhi, f16x2 s
     const u32x4 r{bitcast<uint32_t>(p0), bitcast<uint32_t>(p1), bitcast<uint32_t>(p2),
                   bitcast<uint32_t>(p3)};
     return bitcast<f16x8>(r);
-}
-
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] and
-// vmcnt[5:4] at bits 15:14; expcnt and lgkmcnt left at their maxima).
-template <int N>
-FL_DEV void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-typedef void __attribute__((address_space(3)))* lptr_t;
-
-// Raw buffer resource over [base, base + bytes) (gfx9 descriptor, dword 3 =
-// 0x00020000): loads take a 32-bit per-lane offset plus a wave-uniform SGPR
-// offset, so the per-block address step is one scalar add.
-FL_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                             0x00020000);
 }
 
 template <bool G32>

@@ -15,15 +15,10 @@
 #include "common.cuh"
 #include "device.cuh"
 #include "gemv_common.cuh"
+#include "int4_common.cuh"
 #include "npmath.cuh"
 
 namespace {
-
-FL_DEV uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
-    return r;
-}
 
 // 8 row-major nibbles (bytes b0..b3 of w; byte b = k 2b low, 2b+1 high) ->
 // fp16 (q - z) in k order.  magic = {1024 (lo), 64 (hi)} exponent pair,
@@ -74,6 +69,43 @@ FL_DEV void rm_block_mma(f32x4& acc, const u32x4 (&a)[4], u32x4 w, uint16_t s16,
         for (int j = 0; j < 4; ++j)
             part = mfma_f16(bitcast<f16x8>(a[j]),
                             bitcast<f16x8>(scale_f16x8(rm_dequant(w[j], zc, kRmMagic), s16)), part);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(live, part[e], acc[e]);
+    }
+}
+
+// Zero point of a stacked-expert group (fp16 holding an integer 0..15) as
+// the fp16 pairs -(1024+z) and -(64+z).
+FL_DEV void tile_zero_bits(uint16_t z16, uint32_t& zlo, uint32_t& zhi) {
+    zero_bits((uint32_t)(float)bitcast<f16>(z16), zlo, zhi);
+}
+
+// One 128-k block of one 16-row tile of the stacked-expert tile layout
+// (nibbles interleaved like the Marlin tile layout): B lanes dequantized,
+// 4 MFMAs, scale applied (group 128: on the fp32 partial; smaller groups: in
+// fp16 before).
+template <bool G128>
+FL_DEV void tile_block_mma(f32x4& acc, const u32x4 (&a)[4], u32x4 w, uint16_t s16, uint16_t z16,
+                           float live) {
+    uint32_t zlo, zhi;
+    tile_zero_bits(z16, zlo, zhi);
+    f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (G128) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            part = mfma_f16(bitcast<f16x8>(a[j]), dequant_word_fast(w[j], zlo, zhi, 0x64006400u, 0x54005400u),
+                            part);
+        const float s = (float)bitcast<f16>(s16) * live;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(s, part[e], acc[e]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            part = mfma_f16(bitcast<f16x8>(a[j]),
+                            bitcast<f16x8>(scale_f16x8(bitcast<u32x4>(dequant_word_fast(
+                                                           w[j], zlo, zhi, 0x64006400u, 0x54005400u)),
+                                                       s16)),
+                            part);
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(live, part[e], acc[e]);
     }
@@ -506,14 +538,108 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
 }
 
 // MoE lists for batches routed by several workgroups (entries read from the
-// router's topk_ids / topk_w).
+// router's topk_ids / topk_w), one workgroup of 1024 threads.  Entries of an
+// expert are its tokens in ascending order (a token's K experts are
+// distinct), so entry (t, k) of expert e sits at
+//   base[e] + #{t' < t : t' chose e},
+// and that count is a popcount over a token bitmap sel[e] of the expert:
+//   1. every thread loads its entries, counts experts (LDS atomics) and sets
+//      the token bits of sel;
+//   2. the first wave scans the expert counts (slot offsets, active list)
+//      while the others form pc[e][w], the bits of sel[e] below word w;
+//   3. every entry writes itself at base[e] + pc[e][t/32] + the popcount
+//      of sel[e][t/32] below bit t%32 -- no serial walk anywhere.
+// Limits: T * K <= kListIds, E * ceil(T / 32) <= kListSel.
+constexpr int kListIds = 4096;
+constexpr int kListSel = 4096;
 __global__ __launch_bounds__(1024) void route_lists_k(const int* __restrict__ ids,
                                                       const float* __restrict__ tw, int T, int K,
                                                       int E, MoeLists L) {
+    constexpr int R = kListIds / 1024;  // entries per thread
     __shared__ int cnt[256];
     __shared__ int base[256];
-    __shared__ int chunk[1024];
-    build_lists(ids, tw, T, K, E, L, cnt, base, chunk);
+    __shared__ uint32_t sel[kListSel];
+    __shared__ int pc[kListSel];
+    const int TK = T * K;
+    const int tw32 = (T + 31) >> 5;  // bitmap words per expert
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+    for (int i = tid; i < E * tw32; i += 1024) sel[i] = 0u;
+    int ev[R], tv[R];
+    float wv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = tid + 1024 * r;
+        const int ic = i < TK ? i : TK - 1;
+        ev[r] = ids[ic];
+        wv[r] = tw[ic];
+        tv[r] = ic / K;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (tid + 1024 * r < TK) {
+            atomicAdd(&cnt[ev[r]], 1);
+            atomicOr(&sel[ev[r] * tw32 + (tv[r] >> 5)], 1u << (tv[r] & 31));
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        int c[4], tot = 0, act = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * tid + q;
+            c[q] = e < E ? cnt[e] : 0;
+            tot += c[q];
+            act += c[q] > 0 ? 1 : 0;
+        }
+        int it = tot, ia = act;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int vt = __shfl_up(it, o, 64), va = __shfl_up(ia, o, 64);
+            if (tid >= o) {
+                it += vt;
+                ia += va;
+            }
+        }
+        int off = it - tot, na = ia - act;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * tid + q;
+            if (e < E) {
+                base[e] = off;
+                if (c[q] > 0) {
+                    L.active[na] = e;
+                    L.offsets[na] = off;
+                    ++na;
+                }
+                off += c[q];
+            }
+        }
+        if (tid == 63) {
+            L.offsets[ia] = it;
+            *L.n_active = ia;
+        }
+    } else {
+        // pc[e][w] = popcount of sel[e][0..w): one expert per thread
+        for (int e = tid - 64; e < E; e += 1024 - 64) {
+            int run = 0;
+            for (int w = 0; w < tw32; ++w) {
+                pc[e * tw32 + w] = run;
+                run += __popc(sel[e * tw32 + w]);
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (tid + 1024 * r < TK) {
+            const int e = ev[r], t = tv[r], w = e * tw32 + (t >> 5);
+            const int p = base[e] + pc[w] + __popc(sel[w] & ((1u << (t & 31)) - 1u));
+            L.tok[p] = t;
+            L.tokw[p] = wv[r];
+        }
+    }
 }
 
 // MoE lists from an explicit slot list: slot s is expert cand[s] (or s when
@@ -591,7 +717,10 @@ __global__ void moe_tile_repack_k(const uint8_t* __restrict__ q, const uint16_t*
         const long R = i / cpr;
         const int c = (int)(i - R * cpr), kb = c >> 2, kq = c & 3;
         const long dst = ((R >> 4) * (in_f / 128) + kb) * 1024 + ((R & 15) + 16 * kq) * 16;
-        *reinterpret_cast<u32x4*>(qt + dst) = *reinterpret_cast<const u32x4*>(q + R * (in_f / 2) + c * 16);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(q + R * (in_f / 2) + c * 16);
+        *reinterpret_cast<u32x4*>(qt + dst) =
+            u32x4{gptq_word_to_tile_word(v[0]), gptq_word_to_tile_word(v[1]),
+                  gptq_word_to_tile_word(v[2]), gptq_word_to_tile_word(v[3])};
     }
     const long nsz = rows * G;
     for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nsz; i += stride) {
@@ -611,7 +740,10 @@ __global__ void moe_tile_unpack_k(const uint8_t* __restrict__ qt, const uint32_t
         const long R = i / cpr;
         const int c = (int)(i - R * cpr), kb = c >> 2, kq = c & 3;
         const long src = ((R >> 4) * (in_f / 128) + kb) * 1024 + ((R & 15) + 16 * kq) * 16;
-        *reinterpret_cast<u32x4*>(q + R * (in_f / 2) + c * 16) = *reinterpret_cast<const u32x4*>(qt + src);
+        const u32x4 v = *reinterpret_cast<const u32x4*>(qt + src);
+        *reinterpret_cast<u32x4*>(q + R * (in_f / 2) + c * 16) =
+            u32x4{tile_word_to_gptq_word(v[0]), tile_word_to_gptq_word(v[1]),
+                  tile_word_to_gptq_word(v[2]), tile_word_to_gptq_word(v[3])};
     }
     const long nsz = rows * G;
     for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nsz; i += stride) {
@@ -651,6 +783,7 @@ struct MoeArgs {
     const float* tokw;
     int max_slots, max_entries, inter_pad;
     uint16_t* inter_buf;
+    const uint16_t* xh;  // (T, hidden) fp16 copy of x (grouped kernels only)
     float* y;  // (T, hidden) fp32
 };
 
@@ -779,8 +912,8 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
         for (int j = 0; j < 4; ++j) av[j] = *reinterpret_cast<const u32x4*>(arow + kb * 128 + 8 * j);
 #pragma unroll
         for (int r = 0; r < TR; ++r) {
-            rm_block_mma<G128>(acc[2 * r], av, wg[i][r], sz_scale(szg[i][r]), sz_zero(szg[i][r]), live);
-            rm_block_mma<G128>(acc[2 * r + 1], av, wu[i][r], sz_scale(szu[i][r]), sz_zero(szu[i][r]), live);
+            tile_block_mma<G128>(acc[2 * r], av, wg[i][r], sz_scale(szg[i][r]), sz_zero(szg[i][r]), live);
+            tile_block_mma<G128>(acc[2 * r + 1], av, wu[i][r], sz_scale(szu[i][r]), sz_zero(szu[i][r]), live);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -885,13 +1018,253 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
         const float live = moe_kb<NB>(wave, i, nwaves) < nfull ? 1.0f : 0.0f;
 #pragma unroll
         for (int r = 0; r < TRD; ++r)
-            rm_block_mma<G128>(acc[r], av[i], wv[i][r], sz_scale(sv[i][r]), sz_zero(sv[i][r]), live);
+            tile_block_mma<G128>(acc[r], av[i], wv[i][r], sz_scale(sv[i][r]), sz_zero(sv[i][r]), live);
         __builtin_amdgcn_sched_barrier(0);
     }
     float* red = reinterpret_cast<float*>(smem);
     reduce_and_store<TRD>(red, acc, M, wave, nwaves, lane, [&](int m, int t, int c, float v) {
         unsafeAtomicAdd(&a.y[(size_t)toks[m] * a.hidden + o0 + 16 * t + c], v);
     });
+}
+
+// ------------------------------------------- grouped MoE GEMM (prefill)
+// The two fused-MoE kernels for T > 16 tokens: per list slot a grouped GEMM
+// over the slot's entries, in chunks of 64 rows (4 m-tiles).
+//   PHASE 0 (gate/up): one workgroup per (slot, 128 intermediate columns);
+//     wave w computes gate tile 8 strip + w and up tile 8 strip + w over all
+//     of hidden, so h = silu(g) * u * w_entry is formed in registers and
+//     stored fp16 to inter_buf (no cross-wave reduction: waves split N).
+//     Its token rows come from xh, the fp16 copy of x made by x_to_f16_k.
+//   PHASE 1 (down): one workgroup per (slot, 256 hidden columns); wave w
+//     computes tiles 16 strip + 2 w, + 1 over the slot's inter_buf rows and
+//     adds them into y[token] with fp32 atomics, like the decode kernel.
+// Slot indices >= max_slots are the shared expert (rows max_entries + t,
+// tokens t = 0..T-1, coefficient scoef[t] or 1).
+// Every main-loop load goes global -> LDS (buffer_load ... lds), kMgAhead
+// blocks ahead, into a ring of kMgAhead + 1 stages; one vmcnt wait and one
+// barrier per 128-k block hand a stage to all waves.  A stage holds
+//   * A (16 KB): 64 rows x 128 k fp16, fragment-major for the row-major k
+//     order of the stacked tile layout -- lane (c, q) of MFMA step j reads
+//     row c, k 32 q + 8 j .. + 7 at 16 (64 (4 mt + j) + c + 16 q);
+//   * per wave (2.5 KB): its two 1 KB tile blocks and the tiles' 16 x
+//     (128 / gs) scale|zero words.
+// B is dequantized in registers to s * (q - z) in fp16 (lane (c, q)'s 32 k
+// lie in one group for every group size >= 32) and 32 MFMAs per wave and
+// block accumulate in fp32; m-tiles past the chunk's rows skip their MFMAs.
+constexpr int kMgAhead = 1, kMgStages = kMgAhead + 1;
+constexpr int kMgWaves = 4;                     // waves per workgroup
+constexpr int kMgWaveStage = 2 * 1024 + 2 * 256;  // B tiles + scale|zero rows
+constexpr int kMgABytes = 64 * 128 * 2;            // A tile of one stage
+constexpr int kMgStage = kMgABytes + kMgWaves * kMgWaveStage;
+constexpr size_t kMgLds = (size_t)kMgStages * kMgStage;
+
+// xh[t, :] = fp16(x[t, :]) for the grouped kernels' A copies
+__global__ void x_to_f16_k(const float* __restrict__ x, uint16_t* __restrict__ xh, int n8) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += gridDim.x * blockDim.x) {
+        const f32x4 lo = reinterpret_cast<const f32x4*>(x)[2 * i];
+        const f32x4 hi = reinterpret_cast<const f32x4*>(x)[2 * i + 1];
+        f16x8 h;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            h[q] = (f16)lo[q];
+            h[4 + q] = (f16)hi[q];
+        }
+        reinterpret_cast<f16x8*>(xh)[i] = h;
+    }
+}
+
+template <int PHASE, bool G128>
+__global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int D = kMgAhead, NS = kMgStages;
+    constexpr int NW = kMgWaves, FPW = 16 / NW;  // waves, A fragments copied per wave
+    constexpr int LPB = FPW + 2 + 2;  // per block and wave: A fragments, 2 B tiles, 2 sz rows
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, kq = lane >> 4;
+    const int slot = blockIdx.y, strip = blockIdx.x;
+    if (PHASE == 0) {
+        // every workgroup zeroes its share of y for the down phase's atomics
+        const int nwg = gridDim.x * gridDim.y;
+        const int wg = blockIdx.y * gridDim.x + blockIdx.x;
+        const int n4 = a.T * a.hidden / 4;
+        for (int i = wg * 64 * NW + threadIdx.x; i < n4; i += nwg * 64 * NW)
+            reinterpret_cast<f32x4*>(a.y)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const bool is_shared = slot >= a.max_slots;
+    if (is_shared && !a.has_shared) return;
+    int e = 0, row0, M;
+    const MoeExperts* ex;
+    if (!is_shared) {
+        if (!moe_slot(a, slot, e, row0, M)) return;
+        // moe_slot caps M at T for the decode kernels; a prefill slot holds
+        // every entry routed to its expert
+        const int r1 = clampi(__builtin_amdgcn_readfirstlane(a.offsets[slot + 1]), row0, a.max_entries);
+        M = r1 - row0;
+        ex = &a.routed;
+    } else {
+        row0 = a.max_entries;
+        M = a.T;
+        ex = &a.shared;
+    }
+    const int inter = ex->inter;
+    const int K = PHASE == 0 ? a.hidden : inter;
+    const int Nrows = PHASE == 0 ? inter : a.hidden;  // output rows of the weight
+    const int ncols = PHASE == 0 ? 16 * NW : 32 * NW;  // columns per workgroup
+    if (M <= 0 || strip * ncols >= Nrows) return;
+    const int nkb = K >> 7;
+    const int G = K / a.gs;
+    const int spb = 128 / a.gs;  // groups per 128-k block
+
+    // this wave's two weight tiles
+    __amdgpu_buffer_rsrc_t rq[2], rz[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        size_t tile;
+        const uint8_t* tq;
+        const uint32_t* tsz;
+        if (PHASE == 0) {
+            tile = (size_t)e * (inter / 16) + strip * NW + wave;
+            tq = t == 0 ? ex->gq : ex->uq;
+            tsz = t == 0 ? ex->gsz : ex->usz;
+        } else {
+            tile = (size_t)e * (a.hidden / 16) + strip * 2 * NW + wave * 2 + t;
+            tq = ex->dq;
+            tsz = ex->dsz;
+        }
+        rq[t] = buf_rsrc(tq + tile * nkb * 1024, nkb * 1024);
+        rz[t] = buf_rsrc(tsz + tile * G * 16, G * 64);
+    }
+    // A rows: PHASE 0 token rows of xh, PHASE 1 the slot's inter_buf rows
+    const uint16_t* abase = PHASE == 0 ? a.xh : a.inter_buf;
+    const int astride = PHASE == 0 ? a.hidden : a.inter_pad;  // halves
+    const int arows = PHASE == 0 ? a.T : a.max_entries + a.T;
+    const __amdgpu_buffer_rsrc_t rA = buf_rsrc(abase, (uint32_t)arows * astride * 2);
+    const uint32_t zlane = 4u * (lane < 16 * spb ? lane : 16 * spb - 1);
+    const int g_local = kq * 32 / a.gs;  // this lane's group within a block
+
+    for (int mc = 0; mc < M; mc += 64) {
+        const int mt_live = (M - mc + 15) >> 4;  // m-tiles holding rows of this chunk
+        // A fragments f = FPW wave + i (f = 4 m-tile + j) of this wave
+        uint32_t ao[4];
+#pragma unroll
+        for (int i = 0; i < FPW; ++i) {
+            const int f = wave * FPW + i;
+            int m = mc + 16 * (f >> 2) + col;
+            m = m < M ? m : M - 1;
+            const int row = PHASE == 0 ? (is_shared ? m : clampi(a.tok[row0 + m], 0, a.T - 1))
+                                       : row0 + m;
+            ao[i] = 2u * ((uint32_t)row * astride + 32 * kq + 8 * (f & 3));
+        }
+        auto issue = [&](int kb, int stg) {
+            kb = kb < nkb ? kb : nkb - 1;
+            unsigned char* st = smem + (size_t)stg * kMgStage;
+#pragma unroll
+            for (int i = 0; i < FPW; ++i)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(st + (wave * FPW + i) * 1024), 16,
+                                                         ao[i], kb * 256, 0, 0);
+            unsigned char* wst = st + kMgABytes + wave * kMgWaveStage;
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rq[t], (lptr_t)(wst + t * 1024), 16,
+                                                         lane * 16, kb * 1024, 0, 0);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rz[t], (lptr_t)(wst + 2048 + t * 256), 4,
+                                                         zlane, kb * spb * 64, 0, 0);
+        };
+
+        f32x4 acc[4][2];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+        for (int d = 0; d < D; ++d) issue(d, d);
+        for (int kb = 0; kb < nkb; ++kb) {
+            wait_vmcnt<(D - 1) * LPB>();
+            asm volatile("s_barrier" ::: "memory");
+            issue(kb + D, (kb + D) % NS);
+            const unsigned char* st = smem + (size_t)(kb % NS) * kMgStage;
+            const unsigned char* wst = st + kMgABytes + wave * kMgWaveStage;
+            u32x4 wv[2];
+            uint32_t zlo[2], zhi[2];
+            uint16_t sc[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                wv[t] = *reinterpret_cast<const u32x4*>(wst + t * 1024 + lane * 16);
+                const uint32_t szw =
+                    *reinterpret_cast<const uint32_t*>(wst + 2048 + t * 256 + 4 * (g_local * 16 + col));
+                tile_zero_bits(sz_zero(szw), zlo[t], zhi[t]);
+                sc[t] = sz_scale(szw);
+            }
+            const unsigned char* ab = st + lane * 16;
+            // group 128: q - z products accumulate in a per-block fp32 partial
+            // that takes the column scale once; smaller groups scale B in fp16
+            f32x4 part[4][2];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) part[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                f16x8 av[4];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+                    av[mt] = *reinterpret_cast<const f16x8*>(ab + (mt * 4 + j) * 1024);
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    f16x8 b = dequant_word_fast(wv[t][j], zlo[t], zhi[t], 0x64006400u, 0x54005400u);
+                    if (!G128) b = bitcast<f16x8>(scale_f16x8(bitcast<u32x4>(b), sc[t]));
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt)
+                        if (mt < mt_live) {
+                            if (G128)
+                                part[mt][t] = mfma_f16(av[mt], b, part[mt][t]);
+                            else
+                                acc[mt][t] = mfma_f16(av[mt], b, acc[mt][t]);
+                        }
+                }
+            }
+            if (G128) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const float sv = (float)bitcast<f16>(sc[t]);
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt)
+                        if (mt < mt_live)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                acc[mt][t][i] = __builtin_fmaf(sv, part[mt][t][i], acc[mt][t][i]);
+                }
+            }
+        }
+        wait_vmcnt<0>();
+
+        // epilogue: rows mc + 16 mt + 4 kq + i of the chunk
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = mc + 16 * mt + 4 * kq + i;
+                if (m >= M) continue;
+                if (PHASE == 0) {
+                    const float g = acc[mt][0][i], u = acc[mt][1][i];
+                    const float w = !is_shared ? a.tokw[row0 + m] : (a.scoef ? a.scoef[m] : 1.0f);
+                    const float h = (g / (1.0f + expf(-g))) * u * w;
+                    a.inter_buf[(size_t)(row0 + m) * a.inter_pad + strip * 16 * NW + wave * 16 + col] =
+                        bitcast<uint16_t>((f16)h);
+                } else {
+                    const int tkn = is_shared ? m : clampi(a.tok[row0 + m], 0, a.T - 1);
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+                        unsafeAtomicAdd(&a.y[(size_t)tkn * a.hidden + strip * 32 * NW + wave * 32 + t * 16 + col],
+                                        acc[mt][t][i]);
+                }
+            }
+        asm volatile("s_barrier" ::: "memory");  // the chunk's LDS is reused by the next chunk
+    }
 }
 
 int finish(const char* what) {
@@ -927,6 +1300,8 @@ void rm_dispatch(int nb, const void* X, const uint8_t* W, const uint16_t* S, con
 
 // Launch plan of the fused MoE for one problem shape (host side).
 struct MoePlan {
+    bool grouped;   // T > 16: the grouped-GEMM kernels
+    size_t xh_off;  // grouped: workspace offset of the fp16 copy of x
     int nb_gu, waves_gu, nb_d, trd, waves_d, pieces, inter_pad;
     size_t lds_gu, lds_d, bytes;
 };
@@ -936,8 +1311,17 @@ constexpr int down_tiles(int nb) { return nb <= 2 ? 4 : (nb <= 4 ? 2 : 1); }
 
 // false when the shape is outside what the kernels support.
 bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, MoePlan& p) {
-    if (T <= 0 || T > 16 || hidden <= 0 || hidden % 128 || inter <= 0 || inter % 128) return false;
+    if (T <= 0 || hidden <= 0 || hidden % 128 || inter <= 0 || inter % 128) return false;
     if (shared_inter < 0 || shared_inter % 128 || max_entries <= 0) return false;
+    p.grouped = T > 16;
+    p.inter_pad = inter > shared_inter ? inter : shared_inter;
+    p.bytes = (size_t)(max_entries + T) * p.inter_pad * 2;
+    if (p.grouped) {
+        // + the fp16 copy of x, 256-byte aligned after inter_buf
+        p.xh_off = (p.bytes + 255) & ~(size_t)255;
+        p.bytes = p.xh_off + (size_t)T * hidden * 2;
+        return hidden % 256 == 0;  // grouped GEMM: 256-column down strips
+    }
     const int nfh = hidden / 128;
     p.nb_gu = (nfh + 7) / 8;
     if (p.nb_gu > 4) return false;  // hidden <= 4096
@@ -971,6 +1355,22 @@ void launch_down(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
     const dim3 grid(a.hidden / (16 * down_tiles(NB)), a.max_slots + p.pieces);
     hipLaunchKernelGGL((moe_down_k<G128, NB, down_tiles(NB)>), grid, dim3(64 * p.waves_d), p.lds_d,
                        st, a);
+}
+
+void moe_launch_grouped(const MoeArgs& a, hipStream_t st) {
+    const int n8 = a.T * a.hidden / 8;
+    hipLaunchKernelGGL(x_to_f16_k, dim3((n8 + 255) / 256 < 1024 ? (n8 + 255) / 256 : 1024), dim3(256), 0,
+                       st, a.x, const_cast<uint16_t*>(a.xh), n8);
+    const int slots = a.max_slots + (a.has_shared ? 1 : 0);
+    const int inter_max = a.routed.inter > a.shared.inter ? a.routed.inter : a.shared.inter;
+    const dim3 gu(inter_max / (16 * kMgWaves), slots), dn(a.hidden / (32 * kMgWaves), slots);
+    if (a.gs == 128) {
+        hipLaunchKernelGGL((moe_gemm_k<0, true>), gu, dim3(64 * kMgWaves), kMgLds, st, a);
+        hipLaunchKernelGGL((moe_gemm_k<1, true>), dn, dim3(64 * kMgWaves), kMgLds, st, a);
+    } else {
+        hipLaunchKernelGGL((moe_gemm_k<0, false>), gu, dim3(64 * kMgWaves), kMgLds, st, a);
+        hipLaunchKernelGGL((moe_gemm_k<1, false>), dn, dim3(64 * kMgWaves), kMgLds, st, a);
+    }
 }
 
 template <bool G128>
@@ -1063,6 +1463,9 @@ int fastllm_route_topk(const float* logits, int T, int E, int top_k, int scoring
     if (scoring != 0 && scoring != 1) return 1;
     if (n_group > 1 && (E % n_group || n_group > 64)) return 1;
     if (n_active && (!active || !offsets || !tok || !tokw)) return 1;
+    // the multi-workgroup list builder stages ids, weights and a token bitmap in LDS
+    if (n_active && T > 16 && ((long)T * top_k > kListIds || (long)E * ((T + 31) / 32) > kListSel))
+        return 1;
     if (!fl_current_device_supported()) return 2;
     const MoeLists lists{n_active, active, offsets, tok, tokw};
     RouteArgs a{logits, e_score_bias, shared_logit, T, E, top_k, scoring, norm, n_group,
@@ -1174,9 +1577,13 @@ int fastllm_moe_int4_fused(const float* x, int T, int hidden, int group_size, in
     a.max_entries = max_entries;
     a.inter_pad = p.inter_pad;
     a.inter_buf = static_cast<uint16_t*>(workspace);
+    a.xh = p.grouped ? reinterpret_cast<const uint16_t*>(static_cast<char*>(workspace) + p.xh_off)
+                     : nullptr;
     a.y = y;
     hipStream_t st = (hipStream_t)stream;
-    if (group_size == 128)
+    if (p.grouped)
+        moe_launch_grouped(a, st);
+    else if (group_size == 128)
         moe_launch<true>(a, p, st);
     else
         moe_launch<false>(a, p, st);

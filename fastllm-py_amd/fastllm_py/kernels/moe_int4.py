@@ -271,7 +271,7 @@ def build_lists(T: int, E: int, *, rw=None, slot_coef=None, cand=None, out=None,
 def moe_forward(x, stacked, E, hidden, inter, lists, *, max_slots=None, max_entries=None,
                 shared=None, shared_inter=0, shared_coef=None, out=None, workspace=None,
                 stream=None):
-    """Fused selective INT4 MoE FFN for T <= 16 tokens (x (T, hidden) fp32):
+    """Fused selective INT4 MoE FFN (x (T, hidden) fp32):
 
     y[t] = sum_{entries p of t} tokw[p] * down_e(silu(gate_e x_t) * up_e x_t)
            + shared_coef[t] * shared(x_t)
@@ -280,14 +280,15 @@ def moe_forward(x, stacked, E, hidden, inter, lists, *, max_slots=None, max_entr
     ``build_lists``).  Gate/up run only over the tokens routed to each
     expert; the down projection adds each expert's term into y with fp32
     atomics, as the reference's moew_down does, so the last bits depend on
-    arrival order.  ``workspace`` (uint8 device tensor) is reused when large
-    enough, else allocated."""
+    arrival order.  Up to 16 tokens take the decode kernels (weights split
+    over the waves along k); more tokens take the grouped GEMM kernels (each
+    slot's entries in 64-row chunks on the matrix cores), the prefill form of
+    MoELayer._run_gpu_experts (fastllm_py/moe.py:135-159).  ``workspace``
+    (uint8 device tensor) is reused when large enough, else allocated."""
     t = nat.torch()
     xd = nat.to_device(x, t.float32)
     x2 = xd.reshape(-1, hidden).contiguous()
     T = x2.shape[0]
-    if T > 16:
-        raise ValueError("moe_forward handles up to 16 tokens per call")
     if max_entries is None:
         max_entries = lists["tok"].numel()
     if max_slots is None:

@@ -39,3 +39,23 @@ def moe_ref(x, deq, topk_idx, topk_w, shared_deq=None, shared_coef=None):
         c = np.ones(T, np.float32) if shared_coef is None else np.asarray(shared_coef, np.float32)
         y += c[:, None] * s
     return y
+
+
+def moe_ref_grouped(x, deq, topk_idx, topk_w, shared_deq=None, shared_coef=None):
+    """moe_ref evaluated expert by expert (each expert's tokens in one batch),
+    the way MoELayer._run_gpu_experts groups its tasks (fastllm_py/moe.py:
+    135-159); same arithmetic as moe_ref up to fp32 summation order."""
+    x = np.asarray(x, np.float32)
+    idx = np.asarray(topk_idx)
+    w = np.asarray(topk_w, np.float32)
+    T = x.shape[0]
+    y = np.zeros((T, deq["down"].shape[1]), np.float32)
+    for e in np.unique(idx):
+        tt, kk = np.nonzero(idx == e)
+        f = expert_ffn(x[tt], deq["gate"][e], deq["up"][e], deq["down"][e])
+        np.add.at(y, tt, w[tt, kk][:, None] * f)
+    if shared_deq is not None:
+        s = expert_ffn(x, shared_deq["gate"][0], shared_deq["up"][0], shared_deq["down"][0])
+        c = np.ones(T, np.float32) if shared_coef is None else np.asarray(shared_coef, np.float32)
+        y += c[:, None] * s
+    return y

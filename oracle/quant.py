@@ -262,16 +262,29 @@ def dequantize_int4_rowmajor(packed, scales, zeros, gs: int = 128):
 
 
 # ------------------------------------------------------------------ matmuls
+def nibble_interleave_u32(words):
+    """u32 holding k-offsets r = 0..7 at bits 4r -> the same nibbles with
+    r in slot {0,4,1,5,2,6,3,7}[r] (bits 4 slot)."""
+    w = np.asarray(words, np.uint32)
+    out = np.zeros_like(w)
+    for r in range(8):
+        slot = (r >> 1) + (4 if r & 1 else 0)
+        out |= ((w >> np.uint32(4 * r)) & np.uint32(0xF)) << np.uint32(4 * slot)
+    return out
+
+
 def moe_tile_pack(packed, scales, zeros):
     """Row-major INT4 (rows, in/2) u8 + (rows, G) fp16 scales/zeros -> the
     fused MoE tile layout of this library (no reference counterpart: the
     reference's kernels read the row-major arrays): qtile (rows/16, in/128,
-    1024) u8 with qtile[t, kb, 16 * (c + 16 q) + b] = packed[16 t + c,
-    64 kb + 16 q + b]; sz (rows/16, G, 16) u32 = scale bits | zero bits << 16
-    of row 16 t + c."""
+    1024) u8 whose bytes [16 (c + 16 q), + 16) hold the row-major bytes
+    [64 kb + 16 q, + 16) of row 16 t + c as four little-endian u32, each with
+    its 8 nibbles interleaved by nibble_interleave_u32; sz (rows/16, G, 16)
+    u32 = scale bits | zero bits << 16 of row 16 t + c."""
     rows, half = packed.shape
     q = np.asarray(packed, np.uint8).reshape(rows // 16, 16, half // 64, 4, 16)
     qt = q.transpose(0, 2, 3, 1, 4).reshape(rows // 16, half // 64, 1024)
+    qt = nibble_interleave_u32(np.ascontiguousarray(qt).view("<u4")).view(np.uint8)
     sb = np.asarray(scales, np.float16).view(np.uint16).astype(np.uint32)
     zb = np.asarray(zeros, np.float16).view(np.uint16).astype(np.uint32)
     G = sb.shape[1]

@@ -455,3 +455,64 @@ def test_fused_moe_edge_lists(torch_gpu):
     assert Q.max_abs_rel(y, ref) < 5e-3
     z = moe_int4.fused_moe_weighted(xd, st, torch.zeros(E, device="cuda"), E, hidden, inter)
     assert torch.count_nonzero(z).item() == 0
+
+
+@pytest.mark.parametrize("T,E,K,hidden,inter,sinter,gs,norm", [
+    (17, 8, 2, 256, 256, 0, 128, True),     # just past the decode kernels
+    (64, 16, 4, 512, 384, 1024, 64, False),  # shared expert, group 64
+    (100, 32, 8, 512, 768, 0, 32, True),     # ragged 64-row chunks, group 32
+    (300, 4, 4, 256, 128, 256, 128, False),  # every expert holds all 300 tokens
+])
+def test_fused_moe_prefill(torch_gpu, T, E, K, hidden, inter, sinter, gs, norm):
+    """T > 16: router lists + the grouped-GEMM MoE kernels vs the fp32 oracle
+    (expert-grouped evaluation, pinned to the per-token oracle on the CPU);
+    a second call agrees up to the atomic summation order."""
+    from fastllm_py.expert_router import route_topk_device
+    from fastllm_py.kernels import moe_int4
+
+    torch = torch_gpu
+    rng = np.random.default_rng(T * 13 + hidden + E)
+    st = moe_int4.build_stacked_experts(_experts(rng, E, hidden, inter, 0.05), gs)
+    sh = moe_int4.build_stacked_experts(_experts(rng, 1, hidden, sinter, 0.05), gs) if sinter else None
+    x = (rng.standard_normal((T, hidden)) * 0.5).astype(np.float32)
+    logits = rng.standard_normal((T, E)).astype(np.float16).astype(np.float32)
+    sl = rng.standard_normal(T).astype(np.float32)
+    r = route_topk_device(logits, K, norm_topk_prob=norm, shared_logit=sl if sinter else None)
+    xd = torch.from_numpy(x).cuda()
+    kw = dict(max_slots=min(E, T * K), max_entries=T * K, shared=sh, shared_inter=sinter,
+              shared_coef=r.get("shared_coef"))
+    y = moe_int4.moe_forward(xd, st, E, hidden, inter, r, **kw)
+    y2 = moe_int4.moe_forward(xd, st, E, hidden, inter, r, **kw)
+    assert Q.max_abs_rel(y2.cpu().numpy(), y.cpu().numpy()) < 1e-6
+    ids, w = r["topk_ids"].cpu().numpy(), r["topk_w"].cpu().numpy()
+    coef = 1.0 / (1.0 + np.exp(-sl)) if sinter else None
+    ref = OM.moe_ref_grouped(x, OM.dequant_stacked(_np_stacked(st), gs), ids, w,
+                             OM.dequant_stacked(_np_stacked(sh), gs) if sh else None, coef)
+    assert Q.max_abs_rel(y.cpu().numpy(), ref) < 5e-3
+
+
+def test_moe_prefill_config5(torch_gpu):
+    """BASELINE config 5 (Qwen3-30B-A3B MoE layer at M=512): 128 experts,
+    hidden 2048, inter 768, top-8 softmax with renormalisation from fp16
+    logits ~ N(0,1); routing bit-exact vs the golden fixture, output vs the
+    fp32 oracle."""
+    from fastllm_py.expert_router import route_topk_device
+    from fastllm_py.kernels import moe_int4
+
+    torch = torch_gpu
+    g = np.load(os.path.join(GOLDEN, "route_qwen3moe_t512.npz"))
+    T, E, K, hidden, inter = 512, 128, 8, 2048, 768
+    rng = np.random.default_rng(5512)
+    experts = _experts(rng, E, hidden, inter, 0.02)
+    st = moe_int4.build_stacked_experts(experts, 128)
+    del experts
+    x = rng.standard_normal((T, hidden)).astype(np.float16).astype(np.float32)
+    r = route_topk_device(g["logits"], K, norm_topk_prob=True)
+    ids = r["topk_ids"].cpu().numpy()
+    w = r["topk_w"].cpu().numpy()
+    np.testing.assert_array_equal(ids, g["idx_canonical"])
+    np.testing.assert_array_equal(w.view(np.uint32), g["w_canonical"].view(np.uint32))
+    y = moe_int4.moe_forward(torch.from_numpy(x).cuda(), st, E, hidden, inter, r,
+                             max_slots=E, max_entries=T * K)
+    ref = OM.moe_ref_grouped(x, OM.dequant_stacked(_np_stacked(st), 128), ids, w)
+    assert Q.max_abs_rel(y.cpu().numpy(), ref) < 5e-3

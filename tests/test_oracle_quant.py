@@ -224,8 +224,10 @@ def test_marlin_permutation_brute_force():
 
 
 def test_moe_tile_pack_brute_force():
-    """The MoE tile layout's reshape/transpose against its per-byte definition
-    (lane c + 16 q of block (t, kb) holds row 16 t + c, bytes 64 kb + 16 q ..)."""
+    """The MoE tile layout against its per-nibble definition: weight (R, k)
+    sits in block (R // 16, k // 128), lane c + 16 q (c = R % 16,
+    q = k % 128 // 32), u32 j = k % 32 // 8, nibble slot
+    {0,4,1,5,2,6,3,7}[k % 8]."""
     rng = np.random.default_rng(11)
     rows, in_f, gs = 32, 256, 64
     packed = rng.integers(0, 256, size=(rows, in_f // 2)).astype(np.uint8)
@@ -233,10 +235,14 @@ def test_moe_tile_pack_brute_force():
     ze = rng.integers(0, 16, size=(rows, in_f // gs)).astype(np.float16)
     qt, sz = Q.moe_tile_pack(packed, sc, ze)
     assert qt.shape == (rows // 16, in_f // 128, 1024) and sz.shape == (rows // 16, in_f // gs, 16)
+    slot_of = [0, 4, 1, 5, 2, 6, 3, 7]
     for R in range(rows):
-        for j in range(in_f // 2):
-            kb, q, b = j // 64, (j % 64) // 16, j % 16
-            assert qt[R // 16, kb, 16 * (R % 16 + 16 * q) + b] == packed[R, j]
+        for k in range(in_f):
+            want = (int(packed[R, k // 2]) >> (4 * (k % 2))) & 0xF
+            kb, q, j, r = k // 128, (k % 128) // 32, (k % 32) // 8, k % 8
+            byte = 16 * (R % 16 + 16 * q) + 4 * j + slot_of[r] // 2
+            got = (int(qt[R // 16, kb, byte]) >> (4 * (slot_of[r] % 2))) & 0xF
+            assert got == want
         for g in range(in_f // gs):
             v = int(sz[R // 16, g, R % 16])
             assert v & 0xFFFF == int(sc[R, g].view(np.uint16))
