@@ -1052,7 +1052,7 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
 // lie in one group for every group size >= 32) and 32 MFMAs per wave and
 // block accumulate in fp32; m-tiles past the chunk's rows skip their MFMAs.
 constexpr int kMgAhead = 1, kMgStages = kMgAhead + 1;
-constexpr int kMgWaves = 4;                     // waves per workgroup
+constexpr int kMgWaves = 8;                     // waves per workgroup
 constexpr int kMgWaveStage = 2 * 1024 + 2 * 256;  // B tiles + scale|zero rows
 constexpr int kMgABytes = 64 * 128 * 2;            // A tile of one stage
 constexpr int kMgStage = kMgABytes + kMgWaves * kMgWaveStage;
@@ -1161,8 +1161,9 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
             unsigned char* st = smem + (size_t)stg * kMgStage;
 #pragma unroll
             for (int i = 0; i < FPW; ++i)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(st + (wave * FPW + i) * 1024), 16,
-                                                         ao[i], kb * 256, 0, 0);
+                if (kMgAhead > 1 || wave * FPW + i < 4 * mt_live)  // dead m-tiles: no copy
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(st + (wave * FPW + i) * 1024),
+                                                             16, ao[i], kb * 256, 0, 0);
             unsigned char* wst = st + kMgABytes + wave * kMgWaveStage;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
