@@ -57,6 +57,15 @@ FL_DEV void wait_vmcnt() {
 
 typedef void __attribute__((address_space(3)))* lptr_t;
 
+// Workgroup barrier that hands LDS data to the other waves without draining
+// this wave's outstanding global loads: it waits for the wave's LDS accesses
+// (lgkmcnt(0)) and then s_barrier.  __syncthreads() would also wait for
+// vmcnt(0) (its release fence), i.e. for every weight load issued before it.
+FL_DEV void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (0 << 8));
+    asm volatile("s_barrier" ::: "memory");
+}
+
 // Raw buffer resource over [base, base + bytes) (gfx9 descriptor, dword 3 =
 // 0x00020000): loads take a 32-bit per-lane offset plus a wave-uniform SGPR
 // offset, so the per-block address step is one scalar add; offsets at or

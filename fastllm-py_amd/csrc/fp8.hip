@@ -83,7 +83,9 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
     const int nb = wave < nfull ? (nfull - wave + nwaves - 1) / nwaves : 0;
     const int sw = ALDS ? stage_waves(M, K) : 0;
     const bool early = sw <= nwaves;
-    if (ALDS && early && wave < sw) stage_rows_early(A, As, M, K, lda, wave, lane);
+    RowStager stg;
+    const bool stager = ALDS && early && wave < sw;
+    if (stager) stg.load(A, M, K, lda, wave, lane);
 
     const uint8_t* rbase[T];
     int nrow[T];
@@ -113,8 +115,9 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
     }
     __builtin_amdgcn_sched_barrier(0);
     if (ALDS) {
+        if (stager) stg.store(As);
         if (!early) stage_rows_loop(A, As, M, K, lda);
-        __syncthreads();
+        lds_barrier();  // the weight loads stay in flight
     }
 
     const int arow_m = col < M ? col : M - 1;

@@ -7,34 +7,40 @@
 
 #include "common.cuh"
 
-// Stage the M x K activations (16-bit elements) into LDS rows of stride
-// `lda` halves.  Called by the first `sw = ceil(M*K/8 / 256)` waves only,
-// before they issue their weight loads: vector loads retire in issue order,
-// so staging after the weight loads would make the LDS barrier wait for all
-// of them.  Each lane moves 4 chunks of 8 halves; indices are clamped so
-// every lane loads and stores (duplicates rewrite the same value).
-template <typename E>
-FL_DEV void stage_rows_early(const E* __restrict__ A, E* __restrict__ As, int M, int K, int lda,
-                             int wave, int lane) {
-    const int k8 = K >> 3;
-    const int nchunks = M * k8;
-    const float inv_k8 = 1.0f / (float)k8;
+// Staging of the M x K activations (16-bit elements) into LDS rows of stride
+// `lda` halves by the first `sw = ceil(M*K/8 / 256)` waves, split in two so
+// the weight loads go out in between: load() issues this lane's 4 chunk
+// loads (8 halves each) before the wave's weight loads, store() writes them
+// to LDS after.  Vector loads retire in issue order, so the store waits only
+// for the activation loads while the weight loads stay in flight.  Indices
+// are clamped so every lane loads and stores (duplicates rewrite the same
+// value).
+struct RowStager {
     u32x4 v[4];
     int dst[4];
+    template <typename E>
+    FL_DEV void load(const E* __restrict__ A, int M, int K, int lda, int wave, int lane) {
+        const int k8 = K >> 3;
+        const int nchunks = M * k8;
+        const float inv_k8 = 1.0f / (float)k8;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        int c = (wave * 64 + lane) * 4 + r;
-        c = c < nchunks ? c : nchunks - 1;
-        int m = (int)((float)c * inv_k8);
-        m -= (m * k8 > c) ? 1 : 0;
-        m += ((m + 1) * k8 <= c) ? 1 : 0;
-        const int c8 = c - m * k8;
-        v[r] = *reinterpret_cast<const u32x4*>(A + (size_t)m * K + c8 * 8);
-        dst[r] = m * lda + c8 * 8;
+        for (int r = 0; r < 4; ++r) {
+            int c = (wave * 64 + lane) * 4 + r;
+            c = c < nchunks ? c : nchunks - 1;
+            int m = (int)((float)c * inv_k8);
+            m -= (m * k8 > c) ? 1 : 0;
+            m += ((m + 1) * k8 <= c) ? 1 : 0;
+            const int c8 = c - m * k8;
+            v[r] = *reinterpret_cast<const u32x4*>(A + (size_t)m * K + c8 * 8);
+            dst[r] = m * lda + c8 * 8;
+        }
     }
+    template <typename E>
+    FL_DEV void store(E* __restrict__ As) const {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) *reinterpret_cast<u32x4*>(As + dst[r]) = v[r];
-}
+        for (int r = 0; r < 4; ++r) *reinterpret_cast<u32x4*>(As + dst[r]) = v[r];
+    }
+};
 
 template <typename E>
 FL_DEV void stage_rows_loop(const E* __restrict__ A, E* __restrict__ As, int M, int K, int lda) {

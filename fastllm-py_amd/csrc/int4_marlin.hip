@@ -24,6 +24,7 @@
 //     exponent of 1024 (bits 0-3) or of 64 (bits 4-7).
 #include "common.cuh"
 #include "device.cuh"
+#include "gemv_common.cuh"
 #include "int4_common.cuh"
 
 namespace {
@@ -231,12 +232,22 @@ __global__ __launch_bounds__(1024) void int4_tile_mm(
 //   * Each wave issues ALL of its weight, scale and zero loads before doing
 //     anything else (indices clamped so the issue is unconditional), so HBM
 //     latency is paid once per wave and a workgroup keeps W*NB KB in flight.
-//   * The M x K activations are staged once per workgroup in LDS (row stride
-//     K+8 halves).  MFMA rows >= M read row M-1: C rows are independent and
-//     rows >= M are never stored, so no masking is needed.
+//   * Activations (AM = activation mode):
+//       AM 0 (M <= 4): each wave copies the rows of ITS OWN blocks into its
+//         own LDS slot -- one global->LDS copy (buffer_load ... lds, no
+//         VGPRs) of 1 KB = 4 rows x 128 k per block, issued before its weight
+//         loads -- so no workgroup barrier separates the load issue from the
+//         first MFMA.  A barrier there makes every wave wait until the
+//         slowest wave has issued all of its loads into a saturated memory
+//         system, which serialises the compute tail behind the stream;
+//       AM 1: the M x K rows are staged once per workgroup in LDS (row stride
+//         K+8 halves) behind an LDS-only barrier;
+//       AM 2: MFMA A operands are read from global memory at use.
+//     MFMA rows >= M read row M-1: C rows are independent and rows >= M are
+//     never stored, so no masking is needed.
 //   * A trailing 64-k block (group 32 only) is done by wave 0 at the end.
 //   * Cross-wave reduction through LDS in fixed wave order.
-template <int T, int NB, bool G32, bool ALDS>
+template <int T, int NB, bool G32, int AM>
 __global__ __launch_bounds__(1024) void int4_gemv_nb(
     const f16* __restrict__ A, const uint32_t* __restrict__ Wq, const uint16_t* __restrict__ S,
     const uint32_t* __restrict__ Z, f16* __restrict__ C, int M, int N, int K) {
@@ -250,9 +261,13 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
     const int col = lane & 15;
     const int kq = lane >> 4;
     const int zwords = N >> 3;
+    constexpr bool ALDS = AM == 1;
     const int lda = K + 8;
     f16* As = reinterpret_cast<f16*>(smem);
-    float* red = reinterpret_cast<float*>(smem + (ALDS ? (((size_t)M * lda * 2 + 15) & ~(size_t)15) : 0));
+    // AM 0: wave w's slot of NB blocks x 1 KB (4 rows x 128 k) at w * NB KB
+    const size_t abytes = AM == 0 ? (size_t)nwaves * NB * 1024
+                                  : (ALDS ? (((size_t)M * lda * 2 + 15) & ~(size_t)15) : 0);
+    float* red = reinterpret_cast<float*>(smem + abytes);
 
     const int nb = wave < nfull ? (nfull - wave + nwaves - 1) / nwaves : 0;
 
@@ -268,33 +283,31 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
         tbase[t] = Wq + (size_t)(strip * T + t) * (2 * (size_t)K);
     }
 
-    // Activations are staged by the first `sw` waves (4 chunks of 8 halves
-    // per lane, indices clamped so every lane loads and stores) before those
-    // waves issue their weight loads; the other waves issue weight loads at
-    // once.  Loads retire in issue order, so had the staging loads followed
-    // the weight loads, the LDS barrier would have waited for every weight
-    // block.  M*K too large for that goes through a plain staging loop.
+    // Activations are staged by the first `sw` waves (RowStager: their
+    // activation loads go out before their weight loads, the LDS stores
+    // after them, so the stores wait only for the activations and the LDS
+    // barrier does not drain the weight loads).  M*K too large for that goes
+    // through a plain staging loop.
     const int k8 = K >> 3;
     const int nchunks = ALDS ? M * k8 : 0;
     const int sw = (nchunks + 255) >> 8;
     const bool early = sw <= nwaves;
-    if (ALDS && early && wave < sw) {
-        const float inv_k8 = 1.0f / (float)k8;
-        f16x8 ast[4];
-        int dst[4];
+    RowStager stg;
+    const bool stager = ALDS && early && wave < sw;
+    if (stager) stg.load(A, M, K, lda, wave, lane);
+    // AM 0: lane l of block slot i copies row min(l / 16, M - 1), 16-byte
+    // piece l % 16 of the block into this wave's LDS slot
+    unsigned char* aslot = smem + (size_t)wave * NB * 1024;
+    if (AM == 0) {
+        const int own_m = (lane >> 4) < M ? (lane >> 4) : M - 1;
+        const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)M * K * 2);
+        const uint32_t ao = 2u * ((uint32_t)own_m * K + 8 * (lane & 15));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            int c = (wave * 64 + lane) * 4 + r;
-            c = c < nchunks ? c : nchunks - 1;
-            int m = (int)((float)c * inv_k8);
-            m -= (m * k8 > c) ? 1 : 0;
-            m += ((m + 1) * k8 <= c) ? 1 : 0;
-            const int c8 = c - m * k8;
-            ast[r] = *reinterpret_cast<const f16x8*>(A + (size_t)m * K + c8 * 8);
-            dst[r] = m * lda + c8 * 8;
+        for (int i = 0; i < NB; ++i) {
+            int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+            kb = kb < nfull ? kb : nfull - 1;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(aslot + i * 1024), 16, ao, kb * 256, 0, 0);
         }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) *reinterpret_cast<f16x8*>(As + dst[r]) = ast[r];
     }
 
     // One straight-line issue of every load this wave will need (block
@@ -320,7 +333,15 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
     }
     __builtin_amdgcn_sched_barrier(0);
 
+    if (AM == 0) {
+        // this wave's activation copies, issued before its weight loads, are
+        // done once at most the weight loads are outstanding (no barrier:
+        // only this wave reads its slot)
+        constexpr int WL = NB * T * (1 + 2 * SPB);
+        wait_vmcnt<(WL < 63 ? WL : 63)>();
+    }
     if (ALDS) {
+        if (stager) stg.store(As);
         if (!early) {
             for (int idx = threadIdx.x; idx < nchunks; idx += blockDim.x) {
                 const int m = idx / k8, c8 = idx - m * k8;
@@ -328,12 +349,13 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
                     *reinterpret_cast<const f16x8*>(A + (size_t)m * K + c8 * 8);
             }
         }
-        __syncthreads();
+        lds_barrier();  // the weight loads stay in flight
     }
 
     const uint32_t mlo = 0x64006400u, mhi = 0x54005400u;
     const int arow_m = col < M ? col : M - 1;
     const f16* arow = ALDS ? As + (size_t)arow_m * lda + 8 * kq : A + (size_t)arow_m * K + 8 * kq;
+    (void)aslot;
     f32x4 acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -349,8 +371,13 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
         kb = kb < nfull ? kb : nfull - 1;
         f16x8 a[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            a[j] = *reinterpret_cast<const f16x8*>(arow + kb * 128 + 32 * j);
+        for (int j = 0; j < 4; ++j) {
+            if (AM == 0)
+                a[j] = *reinterpret_cast<const f16x8*>(aslot + (size_t)i * 1024 + arow_m * 256 +
+                                                       2 * (32 * j + 8 * kq));
+            else
+                a[j] = *reinterpret_cast<const f16x8*>(arow + kb * 128 + 32 * j);
+        }
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             if (!G32) {
@@ -384,9 +411,10 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
     if (G32 && (K & 127) && wave == 0) {
         // trailing 64-k block: two 32-k groups
         f16x8 a[2];
+        const f16* arow_t = AM == 0 ? A + (size_t)arow_m * K + 8 * kq : arow;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-            a[j] = *reinterpret_cast<const f16x8*>(arow + nfull * 128 + 32 * j);
+            a[j] = *reinterpret_cast<const f16x8*>(arow_t + nfull * 128 + 32 * j);
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             const u32x2 w2 = *reinterpret_cast<const u32x2*>(tbase[t] + nfull * 256 + lane * 2);
@@ -669,15 +697,19 @@ constexpr size_t kGemvLdsCap = 96 * 1024;  // activations staged in LDS up to th
 template <int T, int NB, bool G32>
 hipError_t launch_gemv_nb(const f16* A, const uint32_t* Wq, const uint16_t* S, const uint32_t* Z,
                           f16* C, int M, int N, int K, int waves, hipStream_t stream) {
-    const size_t abytes = (((size_t)M * (K + 8) * 2 + 15) & ~(size_t)15);
-    const bool alds = abytes <= kGemvLdsCap;
-    const size_t lds = (alds ? abytes : 0) + (size_t)waves * T * 256 * sizeof(float);
-    if (alds)
-        hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, true>), dim3(N / (16 * T)), dim3(64 * waves),
-                           lds, stream, A, Wq, S, Z, C, M, N, K);
+    const size_t red = (size_t)waves * T * 256 * sizeof(float);
+    const dim3 grid(N / (16 * T)), block(64 * waves);
+    const size_t own = (size_t)waves * NB * 1024;
+    const size_t shared = (((size_t)M * (K + 8) * 2 + 15) & ~(size_t)15);
+    if (M <= 4 && own + red <= 160 * 1024)
+        hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 0>), grid, block, own + red, stream, A, Wq, S, Z,
+                           C, M, N, K);
+    else if (shared <= kGemvLdsCap)
+        hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 1>), grid, block, shared + red, stream, A, Wq, S,
+                           Z, C, M, N, K);
     else
-        hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, false>), dim3(N / (16 * T)), dim3(64 * waves),
-                           lds, stream, A, Wq, S, Z, C, M, N, K);
+        hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 2>), grid, block, red, stream, A, Wq, S, Z, C, M,
+                           N, K);
     return hipGetLastError();
 }
 

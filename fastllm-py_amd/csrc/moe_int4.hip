@@ -172,7 +172,7 @@ __global__ __launch_bounds__(1024) void rm_gemv_nb(const void* __restrict__ Xv,
         zv[i] = Z[(size_t)nc * G + g];
     }
     __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
+    lds_barrier();  // the weight loads stay in flight
 
     const f16* arow = As + (size_t)(col < M ? col : M - 1) * lda + 32 * kq;
     f32x4 acc[1] = {f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -896,7 +896,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
             *reinterpret_cast<f16x8*>(As + (size_t)j * lda + c8 * 8) = v;
         }
     }
-    __syncthreads();
+    lds_barrier();  // the weight loads stay in flight
 
     const f16* arow = As + (size_t)(col < M ? col : M - 1) * lda + 32 * kq;
     f32x4 acc[2 * TR];
