@@ -176,6 +176,180 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
     });
 }
 
+// Decode GEMV for M <= 4 on 4-row tiles ("quartered" MFMA).
+//
+// A 16 x 16 MFMA tile normally needs 16 weight rows, so N = 2048 gives only
+// 128 workgroups -- half of the GPU's CUs.  Here the 16 B-operand columns are
+// (row r, k-quarter h) = column 4 h + r of a 4-row tile, and the 16 A-operand
+// rows are (k-quarter h', activation row m) = row 4 h' + m: lane column
+// 4 h + r reads the weights of row r in quarter h of K, lane row 4 h' + m the
+// activations of row m in quarter h'.  The diagonal blocks h' == h of the
+// product are the quarter partial sums; summing them over h gives the
+// output.  The off-diagonal blocks are discarded.  So one 128-k MFMA step
+// covers 4 rows x 4 quarters, and a workgroup needs only 4 weight rows.
+//   * Quarter h holds blocks [h QB, (h + 1) QB) of the nfull full 128-k
+//     blocks (QB = ceil(nfull / 4)); waves take block slots b of a quarter
+//     round-robin, NB at most.  Blocks past nfull repeat the last one with a
+//     zero scale.
+//   * Each wave copies the activations of its own slots global -> LDS
+//     (buffer_load ... lds, 1 KB = 4 quarters x 128 k per activation row)
+//     before issuing its weight loads; no workgroup barrier precedes the
+//     MFMAs.
+//   * A trailing 64-wide block (128 x 128 format) is added by wave 0 through
+//     quarter 0.
+//   * Lane l holds the diagonal element of column l % 16 when
+//     l / 16 == (l % 16) / 4; waves and quarters are summed through LDS in a
+//     fixed order.
+template <int NB, bool INLINE, bool BF16>
+__global__ __launch_bounds__(1024) void fp8_gemv_q4(
+    const uint16_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ Sc,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int rs,
+    int nks) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int BSTRIDE = INLINE ? 132 : 128;
+    const int nwaves = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row0 = blockIdx.x * 4;
+    const int nfull = K >> 7;
+    const int QB = (nfull + 3) >> 2;
+    const int col = lane & 15, kq = lane >> 4;
+    const int r = col & 3, h = col >> 2;  // B column (row, quarter)
+    const int am = col & 3, ah = col >> 2;  // A row (quarter ah, activation row am)
+
+    // this wave's slots b = wave + i * nwaves (< QB), block of quarter q: q QB + b
+    const int nb = wave < QB ? (QB - wave + nwaves - 1) / nwaves : 0;
+    auto slot_b = [&](int i) { return wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves; };
+
+    // activation copies: slot i, row m -> 1 KB at aslot + (i * 4 + m) KB,
+    // lane l = 16 quarter + piece: k = (quarter QB + b) 128 + 8 piece
+    unsigned char* aslot = smem + (size_t)wave * NB * 4096;
+    {
+        const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)M * K * 2);
+        const int q = lane >> 4, piece = lane & 15;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const int b = slot_b(i);
+            int kb = q * QB + b;
+            kb = kb < nfull ? kb : nfull - 1;
+            for (int m = 0; m < M; ++m)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rA, (lptr_t)(aslot + (i * 4 + m) * 1024), 16,
+                    2u * ((uint32_t)m * K + kb * 128 + 8 * piece), 0, 0, 0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // every copy is issued before any weight load
+
+    const int wrow = row0 + r < N ? row0 + r : N - 1;
+    const uint8_t* rbase = W + (size_t)wrow * rs;
+    u32x4 lo[NB], hi[NB];
+    float sv[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const int b = slot_b(i);
+        const int kbr = h * QB + b;
+        const int kb = kbr < nfull ? kbr : nfull - 1;
+        const uint8_t* bp = rbase + (size_t)kb * BSTRIDE;
+        lo[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(bp + 16 * kq));
+        hi[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(bp + 64 + 16 * kq));
+        float sc = INLINE ? *reinterpret_cast<const float*>(bp + 128)
+                          : Sc[(size_t)(wrow >> 7) * nks + kb];
+        sv[i] = (i < nb && kbr < nfull) ? sc : 0.0f;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the activation copies went out first: done once at most the weight
+    // loads (2 or 3 per slot) are outstanding
+    {
+        constexpr int WL = NB * 3;  // lo, hi, scale
+        wait_vmcnt<(WL < 63 ? WL : 63)>();
+    }
+
+    const int arow = am < M ? am : M - 1;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const unsigned char* ab = aslot + (i * 4 + arow) * 1024 + ah * 256 + 32 * kq;
+        const u32x4 a0 = *reinterpret_cast<const u32x4*>(ab);
+        const u32x4 a1 = *reinterpret_cast<const u32x4*>(ab + 16);
+        const u32x4 a2 = *reinterpret_cast<const u32x4*>(ab + 128);
+        const u32x4 a3 = *reinterpret_cast<const u32x4*>(ab + 144);
+        f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+        part = mfma16<BF16>(a0, fp8x8_to_16<BF16>(lo[i][0], lo[i][1]), part);
+        part = mfma16<BF16>(a1, fp8x8_to_16<BF16>(lo[i][2], lo[i][3]), part);
+        part = mfma16<BF16>(a2, fp8x8_to_16<BF16>(hi[i][0], hi[i][1]), part);
+        part = mfma16<BF16>(a3, fp8x8_to_16<BF16>(hi[i][2], hi[i][3]), part);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(sv[i], part[e], acc[e]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    if (!INLINE && (K & 127) && wave == 0) {
+        // trailing 64-wide block, through quarter 0 only (columns and A rows
+        // of other quarters carry zeros)
+        const int kt = nfull * 128;
+        u32x4 a0 = u32x4{0u, 0u, 0u, 0u}, a1 = a0, w = a0;
+        if (ah == 0) {
+            const uint16_t* ar = A + (size_t)arow * K + kt + 16 * kq;
+            a0 = *reinterpret_cast<const u32x4*>(ar);
+            a1 = *reinterpret_cast<const u32x4*>(ar + 8);
+        }
+        if (h == 0) w = *reinterpret_cast<const u32x4_a4*>(rbase + (size_t)nfull * BSTRIDE + 16 * kq);
+        f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+        part = mfma16<BF16>(a0, fp8x8_to_16<BF16>(w[0], w[1]), part);
+        part = mfma16<BF16>(a1, fp8x8_to_16<BF16>(w[2], w[3]), part);
+        const float st = Sc[(size_t)(wrow >> 7) * nks + nfull];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(st, part[e], acc[e]);
+    }
+
+    // diagonal lanes (kq == h) hold rows m = 0..3 of column (r, h)
+    float* red = reinterpret_cast<float*>(smem + (size_t)nwaves * NB * 4096);
+    if (kq == h) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[(wave * 16 + col) * 4 + e] = acc[e];
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        const int rr = threadIdx.x >> 2, m = threadIdx.x & 3;
+        const int n = row0 + rr;
+        if (m < M && n < N) {
+            float v = 0.f;
+            for (int w = 0; w < nwaves; ++w)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v += red[(w * 16 + 4 * q + rr) * 4 + m];
+            if (bias) v += act_to_f32<BF16>(bias[n]);
+            C[(size_t)m * N + n] = f32_to_act<BF16>(v);
+        }
+    }
+}
+
+template <int NB, bool INLINE, bool BF16>
+hipError_t launch_fp8_q4(const uint16_t* A, const uint8_t* W, const float* Sc, const uint16_t* bias,
+                         uint16_t* C, int M, int N, int K, int rs, int nks, int waves,
+                         hipStream_t st) {
+    const size_t lds = (size_t)waves * NB * 4096 + (size_t)waves * 16 * 4 * sizeof(float);
+    hipLaunchKernelGGL((fp8_gemv_q4<NB, INLINE, BF16>), dim3((N + 3) / 4), dim3(64 * waves), lds, st,
+                       A, W, Sc, bias, C, M, N, K, rs, nks);
+    return hipGetLastError();
+}
+
+// M <= 4 and few 16-row strips: the quartered kernel, as many waves as a
+// quarter has blocks (up to 16), the fewest slots per wave that cover it
+template <bool INLINE, bool BF16>
+hipError_t fp8_q4(const uint16_t* A, const uint8_t* W, const float* Sc, const uint16_t* bias,
+                  uint16_t* C, int M, int N, int K, int rs, int nks, hipStream_t st) {
+    const int QB = ((K >> 7) + 3) >> 2;
+    const int nb = (QB + 15) / 16;
+    const int waves = (QB + nb - 1) / nb;
+    if (nb > 4) return hipErrorInvalidValue;
+    switch (nb) {
+        case 1: return launch_fp8_q4<1, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        case 2: return launch_fp8_q4<2, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        case 3: return launch_fp8_q4<3, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        default: return launch_fp8_q4<4, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+    }
+}
+
 struct Fp8Cfg {
     int tiles, waves, nb;
 };
@@ -231,6 +405,9 @@ hipError_t fp8_dispatch_nb(int nb, const uint16_t* A, const uint8_t* W, const fl
 template <bool INLINE, bool BF16>
 hipError_t fp8_gemm(const uint16_t* A, const uint8_t* W, const float* Sc, const uint16_t* bias,
                     uint16_t* C, int M, int N, int K, int rs, int nks, hipStream_t st) {
+    // few 16-row strips and M <= 4: the quartered 4-row kernel
+    if (M <= 4 && K >= 512 && K <= 32768 && N < 8192 && N % 4 == 0)
+        return fp8_q4<INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, st);
     // decode-shaped kernel, 16 activation rows per launch
     for (int m0 = 0; m0 < M; m0 += 16) {
         const int Mc = (M - m0) < 16 ? (M - m0) : 16;
