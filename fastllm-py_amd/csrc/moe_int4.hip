@@ -352,19 +352,30 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
     const int E = a.E, K = a.K;
     float sel[4], p[4];
     const float* s = a.logits + (size_t)t * E;
+    // every logit (and bias) load goes out at once, indices clamped: a
+    // guarded load per use would be one serialized memory round trip each
+    float lv[4], bv4[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int e = lane + 64 * c;
+        const int ec = e < E ? e : E - 1;
+        lv[c] = s[ec];
+        bv4[c] = a.bias ? a.bias[ec] : 0.0f;
+    }
+    const float slog = (a.scoef && a.slogit) ? a.slogit[t] : 0.0f;
     if (a.scoring == 0) {
         float m = -__builtin_inff();
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int e = lane + 64 * c;
-            if (e < E) m = fmaxf(m, s[e]);
+            if (e < E) m = fmaxf(m, lv[c]);
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int e = lane + 64 * c;
-            if (e < E) exw[e] = np_expf(s[e] - m);
+            if (e < E) exw[e] = np_expf(lv[c] - m);
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
@@ -380,9 +391,9 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
         for (int c = 0; c < 4; ++c) {
             const int e = lane + 64 * c;
             if (e < E) {
-                const float d = 1.0f + np_expf(-s[e]);
+                const float d = 1.0f + np_expf(-lv[c]);
                 p[c] = 1.0f / d;
-                sel[c] = a.bias ? p[c] + a.bias[e] : p[c] + 0.0f;
+                sel[c] = a.bias ? p[c] + bv4[c] : p[c] + 0.0f;
             } else {
                 p[c] = 0.f;
                 sel[c] = -__builtin_inff();
@@ -429,42 +440,53 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
             if (e < E && !kg) sel[c] = -__builtin_inff();
         }
     }
-    // top-k by (value desc, index asc); lane i keeps the i-th pick
-    int my_id = 0;
-    float my_w = 0.f;
-    for (int i = 0; i < K; ++i) {
-        float bv = -__builtin_inff();
-        int bi = 0x7fffffff;
+    // top-k by (value desc, index asc) through ranks: with the selection
+    // values in LDS, every expert counts the experts ahead of it; the K
+    // experts of rank < K are the picks and the rank is the selection order.
+    // (One pass of broadcast LDS reads instead of K dependent wave-wide
+    // arg-max shuffle trees.)
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const int E4 = (E + 3) & ~3;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int e = lane + 64 * c;
+        if (e < E4) exw[e] = e < E ? sel[c] : -__builtin_inff();
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    const int nc = (E + 63) >> 6;
+    int rk[4] = {0, 0, 0, 0};
+    for (int j = 0; j < E4; j += 4) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(exw + j);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
+            if (c >= nc) break;
             const int e = lane + 64 * c;
-            if (e < E && (sel[c] > bv || (sel[c] == bv && e < bi))) {
-                bv = sel[c];
-                bi = e;
-            }
-        }
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
+            for (int q = 0; q < 4; ++q)
+                rk[c] += (v[q] > sel[c] || (v[q] == sel[c] && j + q < e)) ? 1 : 0;
         }
-        bi = __builtin_amdgcn_readfirstlane(bi);
-        const int bc = bi >> 6;
-        const float pc = bc == 0 ? p[0] : (bc == 1 ? p[1] : (bc == 2 ? p[2] : p[3]));
-        const float pw = __shfl(pc, bi & 63, 64);
-        if (lane == (bi & 63)) {
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    int* pid = reinterpret_cast<int*>(exw);        // exw is dead: picks in rank order
+    float* pwv = exw + kMaxTopK;
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                if (c == bc) sel[c] = -__builtin_inff();
+    for (int c = 0; c < 4; ++c) {
+        const int e = lane + 64 * c;
+        if (e < E && rk[c] < K) {
+            pid[rk[c]] = e;
+            pwv[rk[c]] = p[c];
         }
-        if (lane == i) {
-            my_id = bi;
-            my_w = pw;
-        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    int my_id = 0;
+    float my_w = 0.f;
+    if (lane < K) {
+        my_id = pid[lane];
+        my_w = pwv[lane];
     }
     if (a.norm) {
         // numpy row sum of the k weights (selection order), + 1e-20: below 8
@@ -496,7 +518,7 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
         sids[tl * K + lane] = my_id;
         sws[tl * K + lane] = my_w;
     }
-    if (lane == 0 && a.scoef && a.slogit) a.scoef[t] = 1.0f / (1.0f + expf(-a.slogit[t]));
+    if (lane == 0 && a.scoef && a.slogit) a.scoef[t] = 1.0f / (1.0f + expf(-slog));
     if (a.rw) {
         float w[4] = {0.f, 0.f, 0.f, 0.f};
         for (int i = 0; i < K; ++i) {
@@ -532,6 +554,25 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
         route_token(a, t, tl, lane, ex[wv], sids, sws);
     }
     if (gridDim.x == 1 && a.lists.n_active) {
+        if (a.T == 1) {
+            // one token: its K picks are the K slots, ordered by expert id
+            // (the experts are distinct, so the ranks are too)
+            const int K = a.K;
+            if (lane < K) {
+                const int id = sids[lane];
+                int rank = 0;
+                for (int j = 0; j < K; ++j) rank += sids[j] < id ? 1 : 0;
+                a.lists.active[rank] = id;
+                a.lists.offsets[rank] = rank;
+                a.lists.tok[rank] = 0;
+                a.lists.tokw[rank] = sws[lane];
+                if (lane == 0) {
+                    a.lists.offsets[K] = K;
+                    *a.lists.n_active = K;
+                }
+            }
+            return;
+        }
         __syncthreads();
         build_lists(sids, sws, a.T, a.K, a.E, a.lists, cnt, base, chunk);
     }
@@ -788,6 +829,7 @@ struct MoeArgs {
 };
 
 constexpr int kGuTiles = 2;  // 16-row tiles of gate and of up per workgroup
+constexpr int kGuOwnT = 4;    // up to this many tokens each wave stages its own activations
 
 FL_DEV int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
 
@@ -833,6 +875,23 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
     const int K = a.hidden;
     const int nfull = K >> 7;
     const int lda = K + 8;
+    // T <= 4: each wave converts every token's rows of its own blocks into
+    // its own LDS slot (NB blocks x T rows x 128 halves), loading them first
+    // of all -- they depend on nothing -- and reading them back without a
+    // workgroup barrier.  Larger T gathers the slot's rows per workgroup.
+    const bool own = a.T <= kGuOwnT;
+    f32x4 xs[NB][2];
+    if (own) {
+        const int m = (lane >> 4) < a.T ? (lane >> 4) : a.T - 1;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            int kb = moe_kb<NB>(wave, i, nwaves);
+            kb = kb < nfull ? kb : nfull - 1;
+            const float* src = a.x + (size_t)m * K + kb * 128 + 8 * (lane & 15);
+            xs[i][0] = *reinterpret_cast<const f32x4*>(src);
+            xs[i][1] = *reinterpret_cast<const f32x4*>(src + 4);
+        }
+    }
 
     if (blockIdx.x == 0)
         for (int i = threadIdx.x; i < a.T * a.hidden / 4; i += blockDim.x)
@@ -858,6 +917,12 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
     if (M <= 0) return;
     const int G = K / a.gs;
     const size_t tb0 = (size_t)e * (ex->inter / 16) + (size_t)grp * TR;  // first row tile
+    // the token of this lane's MFMA row and the entry weights, loaded now so
+    // neither waits at the end
+    const int jr = col < M ? col : M - 1;
+    const int tok_r = slot >= 0 ? clampi(a.tok[row0 + jr], 0, a.T - 1) : jr;
+    const int jw = (int)threadIdx.x < M ? (int)threadIdx.x : 0;
+    const float wpre = slot >= 0 ? a.tokw[row0 + jw] : (a.scoef ? a.scoef[jw] : 1.0f);
 
     u32x4 wg[NB][TR], wu[NB][TR];
     uint32_t szg[NB][TR], szu[NB][TR];
@@ -877,9 +942,23 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    // gather this slot's token rows (fp32 -> fp16)
     f16* As = reinterpret_cast<f16*>(smem);
-    {
+    unsigned char* oslot = smem + (size_t)wave * NB * a.T * 256;
+    if (own) {
+        if ((lane >> 4) < a.T) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                f16x8 v;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    v[q] = (f16)xs[i][0][q];
+                    v[4 + q] = (f16)xs[i][1][q];
+                }
+                *reinterpret_cast<f16x8*>(oslot + ((size_t)i * a.T + (lane >> 4)) * 256 + 16 * (lane & 15)) = v;
+            }
+        }
+    } else {
+        // gather this slot's token rows (fp32 -> fp16)
         const int k8 = K >> 3;
         for (int c = threadIdx.x; c < M * k8; c += blockDim.x) {
             const int j = c / k8, c8 = c - j * k8;
@@ -895,10 +974,10 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
             }
             *reinterpret_cast<f16x8*>(As + (size_t)j * lda + c8 * 8) = v;
         }
+        lds_barrier();  // the weight loads stay in flight
     }
-    lds_barrier();  // the weight loads stay in flight
 
-    const f16* arow = As + (size_t)(col < M ? col : M - 1) * lda + 32 * kq;
+    const f16* arow = As + (size_t)jr * lda + 32 * kq;
     f32x4 acc[2 * TR];
 #pragma unroll
     for (int r = 0; r < 2 * TR; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -909,7 +988,10 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
         kb = kb < nfull ? kb : nfull - 1;
         u32x4 av[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) av[j] = *reinterpret_cast<const u32x4*>(arow + kb * 128 + 8 * j);
+        for (int j = 0; j < 4; ++j)
+            av[j] = own ? *reinterpret_cast<const u32x4*>(oslot + ((size_t)i * a.T + tok_r) * 256 +
+                                                          2 * (32 * kq + 8 * j))
+                        : *reinterpret_cast<const u32x4*>(arow + kb * 128 + 8 * j);
 #pragma unroll
         for (int r = 0; r < TR; ++r) {
             tile_block_mma<G128>(acc[2 * r], av, wg[i][r], sz_scale(szg[i][r]), sz_zero(szg[i][r]), live);
@@ -922,8 +1004,10 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
     // reduce the 2*TR tiles over the waves, then h = silu(g) * u * w
     float* red = reinterpret_cast<float*>(smem);
     const size_t red_bytes = (size_t)nwaves * 2 * TR * 1024;
-    const size_t as_bytes = ((size_t)a.T * lda * 2 + 15) & ~(size_t)15;
+    const size_t as_bytes = own ? (size_t)nwaves * NB * a.T * 256 : (((size_t)a.T * lda * 2 + 15) & ~(size_t)15);
     float* gu = reinterpret_cast<float*>(smem + (red_bytes > as_bytes ? red_bytes : as_bytes));
+    float* wsm = gu + 2 * TR * 256;
+    if ((int)threadIdx.x < M) wsm[threadIdx.x] = wpre;
     reduce_and_store<2 * TR>(red, acc, M, wave, nwaves, lane,
                              [&](int m, int t, int c, float v) { gu[t * 256 + m * 16 + c] = v; });
     __syncthreads();
@@ -932,8 +1016,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
         const int m = rem >> 4, c = rem & 15;
         const float g = gu[(2 * r) * 256 + m * 16 + c];
         const float u = gu[(2 * r + 1) * 256 + m * 16 + c];
-        const float w = slot >= 0 ? a.tokw[row0 + m] : (a.scoef ? a.scoef[m] : 1.0f);
-        const float h = (g / (1.0f + expf(-g))) * u * w;
+        const float h = (g / (1.0f + expf(-g))) * u * wsm[m];
         a.inter_buf[(size_t)(row0 + m) * a.inter_pad + (grp * TR + r) * 16 + c] =
             bitcast<uint16_t>((f16)h);
     }
@@ -1327,9 +1410,10 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
     p.nb_gu = (nfh + 7) / 8;
     if (p.nb_gu > 4) return false;  // hidden <= 4096
     p.waves_gu = (nfh + p.nb_gu - 1) / p.nb_gu;
-    const size_t as_bytes = (((size_t)T * (hidden + 8) * 2) + 15) & ~(size_t)15;
+    const size_t as_bytes = T <= kGuOwnT ? (size_t)p.waves_gu * p.nb_gu * T * 256
+                                         : (((size_t)T * (hidden + 8) * 2) + 15) & ~(size_t)15;
     const size_t red_bytes = (size_t)p.waves_gu * 2 * kGuTiles * 1024;
-    p.lds_gu = (as_bytes > red_bytes ? as_bytes : red_bytes) + (size_t)2 * kGuTiles * 1024;
+    p.lds_gu = (as_bytes > red_bytes ? as_bytes : red_bytes) + (size_t)2 * kGuTiles * 1024 + 16 * 4;
     if (p.lds_gu > 160 * 1024) return false;
     const int nfr = inter / 128;
     const int nb = (nfr + 7) / 8;
