@@ -344,59 +344,133 @@ FL_DEV void build_lists(const int* ids, const float* ws, int T, int K, int E, Mo
     }
 }
 
-// Route token t with one wave.  `exw` is the wave's 256-float LDS row;
-// lane i < K ends with the i-th selection (expert `my_id`, final weight
+// Order-preserving map of a float to an unsigned key (larger float, larger
+// key; -inf above 0, so 0 marks "removed").
+FL_DEV uint32_t order_key(float v) {
+    const uint32_t u = bitcast<uint32_t>(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+FL_DEV float key_float(uint32_t k) {
+    return bitcast<float>((k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k);
+}
+
+FL_DEV uint32_t umax4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    const uint32_t x = a > b ? a : b, y = c > d ? c : d;
+    return x > y ? x : y;
+}
+
+// Wave-wide unsigned maximum, uniform: DPP butterflies inside each 16-lane
+// row (xor 1, xor 2, half-row mirror, row mirror), then the four row results
+// read into scalar registers.
+FL_DEV uint32_t wave_umax(uint32_t k) {
+    uint32_t o;
+    o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+    k = k > o ? k : o;
+    o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+    k = k > o ? k : o;
+    o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    k = k > o ? k : o;
+    o = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)k, 0x140, 0xF, 0xF, false);  // row_mirror
+    k = k > o ? k : o;
+    const uint32_t r0 = (uint32_t)__builtin_amdgcn_readlane((int)k, 0);
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_readlane((int)k, 16);
+    const uint32_t r2 = (uint32_t)__builtin_amdgcn_readlane((int)k, 32);
+    const uint32_t r3 = (uint32_t)__builtin_amdgcn_readlane((int)k, 48);
+    return umax4(r0, r1, r2, r3);
+}
+
+// numpy's float32 row sum (np_sum_f32) of n <= 128 values held one per lane
+// in v[0] (e < 64) and v[1] (e >= 64), also stored at a[e] (LDS): lanes
+// j < 8 read their accumulator's values a[j + 8 i] at once and add them in
+// order, three DPP butterflies form ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) (the
+// same sums: float addition is commutative), the tail comes from lane reads.
+// Every lane returns the sum.
+FL_DEV float np_sum_wave128(const float* a, int n, int lane, float v0, float v1) {
+    float res = 0.0f;
+    int i0 = 0;
+    if (n >= 8) {
+        const int q = n >> 3;  // 8-value blocks, 1..16
+        const int j = lane & 7;
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = a[8 * i + j];
+        float r = x[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) r = i < q ? r + x[i] : r;
+        r = r + bitcast<float>(__builtin_amdgcn_update_dpp(0, bitcast<int>(r), 0xB1, 0xF, 0xF, false));
+        r = r + bitcast<float>(__builtin_amdgcn_update_dpp(0, bitcast<int>(r), 0x4E, 0xF, 0xF, false));
+        r = r + bitcast<float>(__builtin_amdgcn_update_dpp(0, bitcast<int>(r), 0x141, 0xF, 0xF, false));
+        res = bitcast<float>(__builtin_amdgcn_readlane(bitcast<int>(r), 0));
+        i0 = 8 * q;
+    }
+    for (int i = i0; i < n; ++i) {
+        const int l = i & 63;
+        const int xv = i < 64 ? __builtin_amdgcn_readlane(bitcast<int>(v0), l)
+                              : __builtin_amdgcn_readlane(bitcast<int>(v1), l);
+        res += bitcast<float>(xv);
+    }
+    return res;
+}
+
+// Route token t with one wave.  `exw` is the wave's 256-float LDS row.
+// Lane i < K ends with the i-th selection (expert `my_id`, final weight
 // `my_w`), which it also stores to topk_ids/topk_w and to sids/sws[tl*K + i].
+// Values sit one per lane in nc <= 4 slots (expert lane + 64 c); slots past
+// nc are skipped by uniform branches.  Everything stays in registers except
+// the exp row of the softmax sum.
 FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw, int* sids,
-                        float* sws) {
+                        float* sws, int& my_id, float& my_w) {
     const int E = a.E, K = a.K;
+    const int nc = (E + 63) >> 6;
     float sel[4], p[4];
     const float* s = a.logits + (size_t)t * E;
-    // every logit (and bias) load goes out at once, indices clamped: a
-    // guarded load per use would be one serialized memory round trip each
+    // the logit (and bias) loads go out together, indices clamped
     float lv[4], bv4[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const int e = lane + 64 * c;
         const int ec = e < E ? e : E - 1;
-        lv[c] = s[ec];
-        bv4[c] = a.bias ? a.bias[ec] : 0.0f;
+        lv[c] = c < nc ? s[ec] : 0.0f;
+        bv4[c] = (c < nc && a.bias) ? a.bias[ec] : 0.0f;
     }
     const float slog = (a.scoef && a.slogit) ? a.slogit[t] : 0.0f;
     if (a.scoring == 0) {
-        float m = -__builtin_inff();
+        uint32_t mk = 0;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const int e = lane + 64 * c;
-            if (e < E) m = fmaxf(m, lv[c]);
+            const uint32_t k = order_key(lv[c]);
+            if (c < nc && lane + 64 * c < E && k > mk) mk = k;
         }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float m = key_float(wave_umax(mk));
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-            const int e = lane + 64 * c;
-            if (e < E) exw[e] = np_expf(lv[c] - m);
+            p[c] = 0.0f;
+            if (c < nc) {
+                const int e = lane + 64 * c;
+                p[c] = e < E ? np_expf(lv[c] - m) : 0.0f;
+                exw[e] = p[c];
+            }
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        const float z = np_sum_wave(exw, E, lane);
+        const float z = E <= 128 ? np_sum_wave128(exw, E, lane, p[0], p[1]) : np_sum_wave(exw, E, lane);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int e = lane + 64 * c;
-            p[c] = (e < E) ? exw[e] / z : 0.f;
-            sel[c] = (e < E) ? p[c] : -__builtin_inff();
+            p[c] = (c < nc && e < E) ? p[c] / z : 0.f;
+            sel[c] = (c < nc && e < E) ? p[c] : -__builtin_inff();
         }
     } else {
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int e = lane + 64 * c;
-            if (e < E) {
+            p[c] = 0.f;
+            sel[c] = -__builtin_inff();
+            if (c < nc && e < E) {
                 const float d = 1.0f + np_expf(-lv[c]);
                 p[c] = 1.0f / d;
                 sel[c] = a.bias ? p[c] + bv4[c] : p[c] + 0.0f;
-            } else {
-                p[c] = 0.f;
-                sel[c] = -__builtin_inff();
             }
         }
     }
@@ -440,73 +514,60 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
             if (e < E && !kg) sel[c] = -__builtin_inff();
         }
     }
-    // top-k by (value desc, index asc) through ranks: with the selection
-    // values in LDS, every expert counts the experts ahead of it; the K
-    // experts of rank < K are the picks and the rank is the selection order.
-    // (One pass of broadcast LDS reads instead of K dependent wave-wide
-    // arg-max shuffle trees.)
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    const int E4 = (E + 3) & ~3;
+    // top-k by (value desc, index asc): K rounds of a wave-wide maximum over
+    // order-preserving integer keys, the lowest expert index among equal
+    // keys through a ballot; round i's pick lands in lane i.
+    uint32_t key[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const int e = lane + 64 * c;
-        if (e < E4) exw[e] = e < E ? sel[c] : -__builtin_inff();
+        key[c] = (c < nc && e < E) ? order_key(sel[c]) : 0u;  // 0: never picked
     }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    const int nc = (E + 63) >> 6;
-    int rk[4] = {0, 0, 0, 0};
-    for (int j = 0; j < E4; j += 4) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(exw + j);
+    my_id = 0;
+    my_w = 0.f;
+    for (int i = 0; i < K; ++i) {
+        const uint32_t m = wave_umax(umax4(key[0], key[1], key[2], key[3]));
+        int e = 0;
+        float w = 0.f;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            if (c >= nc) break;
-            const int e = lane + 64 * c;
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                rk[c] += (v[q] > sel[c] || (v[q] == sel[c] && j + q < e)) ? 1 : 0;
+        for (int c = 3; c >= 0; --c) {  // the lowest slot c holding m wins
+            if (c < nc) {
+                const unsigned long long bm = __ballot(key[c] == m);
+                if (bm) {
+                    const int l = __builtin_ctzll(bm);
+                    e = 64 * c + l;
+                    w = bitcast<float>(__builtin_amdgcn_readlane(bitcast<int>(p[c]), l));
+                }
+            }
         }
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    int* pid = reinterpret_cast<int*>(exw);        // exw is dead: picks in rank order
-    float* pwv = exw + kMaxTopK;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        const int e = lane + 64 * c;
-        if (e < E && rk[c] < K) {
-            pid[rk[c]] = e;
-            pwv[rk[c]] = p[c];
+        for (int c = 0; c < 4; ++c)
+            if (lane + 64 * c == e) key[c] = 0u;
+        if (lane == i) {
+            my_id = e;
+            my_w = w;
         }
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    int my_id = 0;
-    float my_w = 0.f;
-    if (lane < K) {
-        my_id = pid[lane];
-        my_w = pwv[lane];
     }
     if (a.norm) {
         // numpy row sum of the k weights (selection order), + 1e-20: below 8
         // a plain loop; else 8 accumulators (a second round of 8 when
         // k == 16), their tree, then the leftovers one by one
+        const int wbits = bitcast<int>(my_w);
         float den;
         if (K < 8) {
             den = 0.0f;
-            for (int i = 0; i < K; ++i) den += __shfl(my_w, i, 64);
+            for (int i = 0; i < K; ++i) den += bitcast<float>(__builtin_amdgcn_readlane(wbits, i));
         } else {
             float r[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) r[j] = __shfl(my_w, j, 64);
+            for (int j = 0; j < 8; ++j) r[j] = bitcast<float>(__builtin_amdgcn_readlane(wbits, j));
             if (K == 16) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) r[j] += __shfl(my_w, 8 + j, 64);
+                for (int j = 0; j < 8; ++j) r[j] += bitcast<float>(__builtin_amdgcn_readlane(wbits, 8 + j));
             }
             den = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
             if (K < 16)
-                for (int i = 8; i < K; ++i) den += __shfl(my_w, i, 64);
+                for (int i = 8; i < K; ++i) den += bitcast<float>(__builtin_amdgcn_readlane(wbits, i));
         }
         den = den + 1e-20f;
         my_w = my_w / den;
@@ -522,8 +583,8 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
     if (a.rw) {
         float w[4] = {0.f, 0.f, 0.f, 0.f};
         for (int i = 0; i < K; ++i) {
-            const int id = __builtin_amdgcn_readfirstlane(__shfl(my_id, i, 64));
-            const float wi = __shfl(my_w, i, 64);
+            const int id = __builtin_amdgcn_readlane(my_id, i);
+            const float wi = bitcast<float>(__builtin_amdgcn_readlane(bitcast<int>(my_w), i));
 #pragma unroll
             for (int c = 0; c < 4; ++c)
                 if (lane + 64 * c == id) w[c] = wi;
@@ -531,7 +592,7 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int e = lane + 64 * c;
-            if (e < E) a.rw[(size_t)t * E + e] = w[c];
+            if (c < nc && e < E) a.rw[(size_t)t * E + e] = w[c];
         }
     }
 }
@@ -548,24 +609,25 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nw = blockDim.x >> 6;
+    int my_id = 0;
+    float my_w = 0.f;
     for (int tl = wv; tl < 16; tl += nw) {
         const int t = blockIdx.x * 16 + tl;
         if (t >= a.T) break;
-        route_token(a, t, tl, lane, ex[wv], sids, sws);
+        route_token(a, t, tl, lane, ex[wv], sids, sws, my_id, my_w);
     }
     if (gridDim.x == 1 && a.lists.n_active) {
         if (a.T == 1) {
             // one token: its K picks are the K slots, ordered by expert id
             // (the experts are distinct, so the ranks are too)
             const int K = a.K;
+            int rank = 0;
+            for (int j = 0; j < K; ++j) rank += __builtin_amdgcn_readlane(my_id, j) < my_id ? 1 : 0;
             if (lane < K) {
-                const int id = sids[lane];
-                int rank = 0;
-                for (int j = 0; j < K; ++j) rank += sids[j] < id ? 1 : 0;
-                a.lists.active[rank] = id;
+                a.lists.active[rank] = my_id;
                 a.lists.offsets[rank] = rank;
                 a.lists.tok[rank] = 0;
-                a.lists.tokw[rank] = sws[lane];
+                a.lists.tokw[rank] = my_w;
                 if (lane == 0) {
                     a.lists.offsets[K] = K;
                     *a.lists.n_active = K;
