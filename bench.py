@@ -182,7 +182,8 @@ def run_fp8(torch, lib, stream, M_list=(1, 8)):
 def run_moe(torch, lib, stream, T_list=(1, 16)):
     """Fused Qwen1.5-MoE-A2.7B INT4 layer: router from fp16 logits ~ N(0,1)
     (top-4 softmax, no renorm) + routed experts + shared expert (sigmoid gate).
-    Timed unit = one layer: route + gate/up + down launches."""
+    Timed unit = one layer: router + gate/up + down launches
+    (moe_route_forward)."""
     from fastllm_py.expert_router import route_topk_device
     from fastllm_py.kernels import moe_int4
 
@@ -219,13 +220,11 @@ def run_moe(torch, lib, stream, T_list=(1, 16)):
         ws = torch.empty((moe_int4.moe_workspace_bytes(T, hidden, inter, sinter, T * K),),
                          dtype=torch.uint8, device="cuda")
 
-        def mk(st, sh, T=T, logits=logits, x=x, slog=slog, bufs=bufs, y=y, ws=ws):
+        def mk(st, sh, logits=logits, x=x, slog=slog, bufs=bufs, y=y, ws=ws):
             def go(h):
-                route_topk_device(logits, K, shared_logit=slog, out=bufs, stream=h)
-                moe_int4.moe_forward(x, st, E, hidden, inter, bufs, max_slots=min(E, T * K),
-                                     max_entries=T * K, shared=sh, shared_inter=sinter,
-                                     shared_coef=bufs["shared_coef"], out=y, workspace=ws,
-                                     stream=h)
+                moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, shared=sh,
+                                           shared_inter=sinter, shared_logit=slog, route=bufs,
+                                           out=y, workspace=ws, stream=h)
             return go
         rounds = max(1, -(-48 // nl))
         seq = [mk(st, sh) for _ in range(rounds) for st, sh in layers]

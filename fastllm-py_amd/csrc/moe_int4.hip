@@ -275,45 +275,61 @@ struct RouteArgs {
     MoeLists lists;  // built by route_k itself when the batch is one workgroup
 };
 
-// MoE lists from T*K routed entries (ids/ws token-major; each token's K
-// experts distinct, all < E <= 256).  One workgroup of >= 64 threads; the
-// first wave scans the expert counts, entries are placed with a stable
-// counting sort in chunks of blockDim.x.  cnt/base: E ints of LDS, chunk:
-// blockDim.x ints of LDS.
+// Inclusive prefix sum over the wave: shifts by 1, 2, 4, 8 inside each
+// 16-lane row (DPP), then the totals of the rows before a lane's row.
+FL_DEV int wave_incl_scan(int x, int lane) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+    const int t0 = __builtin_amdgcn_readlane(x, 15);
+    const int t1 = __builtin_amdgcn_readlane(x, 31);
+    const int t2 = __builtin_amdgcn_readlane(x, 47);
+    const int row = lane >> 4;
+    return x + (row == 0 ? 0 : (row == 1 ? t0 : (row == 2 ? t0 + t1 : t0 + t1 + t2)));
+}
+
+// MoE lists from the T*K routed entries of one workgroup (ids/ws
+// token-major, T <= 32, each token's K experts distinct, all < E <= 256,
+// blockDim.x >= 64).  Entry (t, k) of expert e goes to
+//   base[e] + #{t' < t : t' chose e},
+// the popcount of the expert's token mask sel[e] below bit t: one pass of
+// LDS atomics (counts, masks), one scan of the counts by the first wave
+// (slot offsets, active list), one pass of placements.  cnt/base/sel: E
+// words of LDS each.
 FL_DEV void build_lists(const int* ids, const float* ws, int T, int K, int E, MoeLists L,
-                        int* cnt, int* base, int* chunk) {
+                        int* cnt, int* base, unsigned* sel) {
     const int TK = T * K;
     const int tid = threadIdx.x, bd = blockDim.x;
-    for (int e = tid; e < E; e += bd) cnt[e] = 0;
+    for (int e = tid; e < E; e += bd) {
+        cnt[e] = 0;
+        sel[e] = 0u;
+    }
     __syncthreads();
-    for (int i = tid; i < TK; i += bd) atomicAdd(&cnt[ids[i]], 1);
+    for (int i = tid; i < TK; i += bd) {
+        const int e = ids[i];
+        atomicAdd(&cnt[e], 1);
+        atomicOr(&sel[e], 1u << (i / K));
+    }
     __syncthreads();
     if (tid < 64) {
         int c[4], tot = 0, act = 0;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int e = 4 * tid + q;
-            c[q] = e < E ? cnt[e] : 0;
+            const int ee = 4 * tid + q;
+            c[q] = ee < E ? cnt[ee] : 0;
             tot += c[q];
             act += c[q] > 0 ? 1 : 0;
         }
-        int it = tot, ia = act;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int vt = __shfl_up(it, o, 64), va = __shfl_up(ia, o, 64);
-            if (tid >= o) {
-                it += vt;
-                ia += va;
-            }
-        }
+        const int it = wave_incl_scan(tot, tid), ia = wave_incl_scan(act, tid);
         int off = it - tot, na = ia - act;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int e = 4 * tid + q;
-            if (e < E) {
-                base[e] = off;
+            const int ee = 4 * tid + q;
+            if (ee < E) {
+                base[ee] = off;
                 if (c[q] > 0) {
-                    L.active[na] = e;
+                    L.active[na] = ee;
                     L.offsets[na] = off;
                     ++na;
                 }
@@ -326,21 +342,11 @@ FL_DEV void build_lists(const int* ids, const float* ws, int T, int K, int E, Mo
         }
     }
     __syncthreads();
-    for (int c0 = 0; c0 < TK; c0 += bd) {
-        const int i = c0 + tid;
-        const int e = i < TK ? ids[i] : -1;
-        chunk[tid] = e;
-        __syncthreads();
-        if (i < TK) {
-            int r = 0;
-            for (int j = 0; j < tid; ++j) r += (chunk[j] == e) ? 1 : 0;
-            const int p = base[e] + r;
-            L.tok[p] = i / K;
-            L.tokw[p] = ws[i];
-        }
-        __syncthreads();
-        if (i < TK) atomicAdd(&base[e], 1);
-        __syncthreads();
+    for (int i = tid; i < TK; i += bd) {
+        const int e = ids[i], t = i / K;
+        const int pos = base[e] + __builtin_popcount(sel[e] & ((1u << t) - 1u));
+        L.tok[pos] = t;
+        L.tokw[pos] = ws[i];
     }
 }
 
@@ -605,7 +611,7 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
     __shared__ float sws[16 * kMaxTopK];
     __shared__ int cnt[256];
     __shared__ int base[256];
-    __shared__ int chunk[1024];
+    __shared__ unsigned selm[256];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nw = blockDim.x >> 6;
@@ -636,7 +642,7 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
             return;
         }
         __syncthreads();
-        build_lists(sids, sws, a.T, a.K, a.E, a.lists, cnt, base, chunk);
+        build_lists(sids, sws, a.T, a.K, a.E, a.lists, cnt, base, selm);
     }
 }
 
@@ -1681,15 +1687,16 @@ size_t fastllm_moe_int4_workspace_bytes(int T, int hidden, int inter, int shared
     return moe_plan(T, hidden, inter, shared_inter, max_entries, p) ? p.bytes : 0;
 }
 
-int fastllm_moe_int4_fused(const float* x, int T, int hidden, int group_size, int E, int inter,
-                           const uint8_t* gq, const uint32_t* gsz, const uint8_t* uq,
-                           const uint32_t* usz, const uint8_t* dq, const uint32_t* dsz,
-                           int shared_inter, const uint8_t* sgq, const uint32_t* sgsz,
-                           const uint8_t* suq, const uint32_t* susz, const uint8_t* sdq,
-                           const uint32_t* sdsz, const float* shared_coef, const int* n_active,
-                           const int* active, const int* offsets, const int* tok,
-                           const float* tokw, int max_slots, int max_entries, void* workspace,
-                           size_t workspace_bytes, float* y, void* stream) {
+// The fused MoE entry; launch = false only validates the arguments.
+static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int E, int inter,
+                          const uint8_t* gq, const uint32_t* gsz, const uint8_t* uq,
+                          const uint32_t* usz, const uint8_t* dq, const uint32_t* dsz,
+                          int shared_inter, const uint8_t* sgq, const uint32_t* sgsz,
+                          const uint8_t* suq, const uint32_t* susz, const uint8_t* sdq,
+                          const uint32_t* sdsz, const float* shared_coef, const int* n_active,
+                          const int* active, const int* offsets, const int* tok,
+                          const float* tokw, int max_slots, int max_entries, void* workspace,
+                          size_t workspace_bytes, float* y, void* stream, bool launch) {
     if (!x || !y || E <= 0 || !gq || !gsz || !uq || !usz || !dq || !dsz) return 1;
     if (group_size != 32 && group_size != 64 && group_size != 128) return 1;
     if (!n_active || !active || !offsets || !tok || !tokw) return 1;
@@ -1704,6 +1711,7 @@ int fastllm_moe_int4_fused(const float* x, int T, int hidden, int group_size, in
                     (!has_shared || (fl_aligned(sgq, 16) && fl_aligned(suq, 16) && fl_aligned(sdq, 16)));
     if (!al) return 1;
     if (!fl_current_device_supported()) return 2;
+    if (!launch) return 0;
     MoeArgs a;
     a.x = x;
     a.T = T;
@@ -1735,6 +1743,59 @@ int fastllm_moe_int4_fused(const float* x, int T, int hidden, int group_size, in
     else
         moe_launch<false>(a, p, st);
     return finish("fastllm_moe_int4_fused");
+}
+
+int fastllm_moe_int4_fused(const float* x, int T, int hidden, int group_size, int E, int inter,
+                           const uint8_t* gq, const uint32_t* gsz, const uint8_t* uq,
+                           const uint32_t* usz, const uint8_t* dq, const uint32_t* dsz,
+                           int shared_inter, const uint8_t* sgq, const uint32_t* sgsz,
+                           const uint8_t* suq, const uint32_t* susz, const uint8_t* sdq,
+                           const uint32_t* sdsz, const float* shared_coef, const int* n_active,
+                           const int* active, const int* offsets, const int* tok,
+                           const float* tokw, int max_slots, int max_entries, void* workspace,
+                           size_t workspace_bytes, float* y, void* stream) {
+    return moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz, shared_inter,
+                          sgq, sgsz, suq, susz, sdq, sdsz, shared_coef, n_active, active, offsets,
+                          tok, tokw, max_slots, max_entries, workspace, workspace_bytes, y, stream,
+                          true);
+}
+
+int fastllm_moe_int4_routed(const float* logits, int top_k, int scoring, int norm,
+                            float routed_scaling, const float* e_score_bias, int n_group,
+                            int topk_group, const float* shared_logit, int* topk_ids,
+                            float* topk_w, float* rw, float* shared_coef, int* n_active,
+                            int* active, int* offsets, int* tok, float* tokw, const float* x,
+                            int T, int hidden, int group_size, int E, int inter,
+                            const uint8_t* gq, const uint32_t* gsz, const uint8_t* uq,
+                            const uint32_t* usz, const uint8_t* dq, const uint32_t* dsz,
+                            int shared_inter, const uint8_t* sgq, const uint32_t* sgsz,
+                            const uint8_t* suq, const uint32_t* susz, const uint8_t* sdq,
+                            const uint32_t* sdsz, void* workspace, size_t workspace_bytes, float* y,
+                            void* stream) {
+    if (!logits || T <= 0 || T > 16 || E <= 0 || E > 256 || top_k <= 0 || top_k > 16 || top_k > E)
+        return 1;
+    if (!topk_ids || !topk_w || !n_active || !active || !offsets || !tok || !tokw) return 1;
+    if (scoring != 0 && scoring != 1) return 1;
+    if (n_group > 1 && (E % n_group || n_group > 64)) return 1;
+    if (shared_inter > 0 && shared_logit && !shared_coef) return 1;
+    const int max_entries = T * top_k, max_slots = E < max_entries ? E : max_entries;
+    // the MoE arguments are checked before anything is launched
+    const int rc = moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz,
+                                  shared_inter, sgq, sgsz, suq, susz, sdq, sdsz, shared_coef,
+                                  n_active, active, offsets, tok, tokw, max_slots, max_entries,
+                                  workspace, workspace_bytes, y, stream, false);
+    if (rc) return rc;
+    const MoeLists lists{n_active, active, offsets, tok, tokw};
+    const RouteArgs r{logits, e_score_bias, shared_logit, T, E, top_k, scoring, norm, n_group,
+                      topk_group, routed_scaling, topk_ids, topk_w, rw, shared_coef, lists};
+    hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(route_k, dim3(1), dim3(64 * T), 0, st, r);
+    const int rr = finish("fastllm_moe_int4_routed");
+    if (rr) return rr;
+    return moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz,
+                          shared_inter, sgq, sgsz, suq, susz, sdq, sdsz,
+                          shared_logit ? shared_coef : nullptr, n_active, active, offsets, tok, tokw,
+                          max_slots, max_entries, workspace, workspace_bytes, y, stream, true);
 }
 
 }  // extern "C"

@@ -311,6 +311,71 @@ def moe_forward(x, stacked, E, hidden, inter, lists, *, max_slots=None, max_entr
     return y
 
 
+def moe_route_forward(x, logits, stacked, top_k, E, hidden, inter, *, norm_topk_prob=False,
+                      scoring="softmax", routed_scaling=1.0, e_score_bias=None, n_group=0,
+                      topk_group=0, shared=None, shared_inter=0, shared_logit=None, route=None,
+                      out=None, workspace=None, stream=None):
+    """Router + fused MoE of T <= 16 tokens in one native call: routes
+    ``logits`` (T, E) exactly like ``route_topk_device`` (same keyword
+    meaning, same outputs, which land in ``route``: topk_ids, topk_w, rw,
+    lists, shared_coef) and returns y (T, hidden) fp32 = moe_forward over
+    those lists (graph_decode._moe_branch, graph_decode.py:669-700).
+    ``route`` / ``workspace`` / ``out`` may carry persistent buffers for
+    graph capture."""
+    t = nat.torch()
+    xd = nat.to_device(x, t.float32)
+    x2 = xd.reshape(-1, hidden).contiguous()
+    T = x2.shape[0]
+    if T > 16:
+        raise ValueError("moe_route_forward: at most 16 tokens (route_topk_device + moe_forward "
+                         "take larger batches)")
+    s = nat.to_device(logits)
+    if s.dtype != t.float32:
+        s = s.to(t.float32)
+    s = s.reshape(T, E).contiguous()
+    dev = x2.device
+    o = route if route is not None else {}
+
+    def buf(name, shape, dtype):
+        if name not in o:
+            o[name] = t.empty(shape, dtype=dtype, device=dev)
+        return o[name]
+
+    ids = buf("topk_ids", (T, top_k), t.int32)
+    w = buf("topk_w", (T, top_k), t.float32)
+    rw = buf("rw", (T, E), t.float32)
+    na = buf("n_active", (1,), t.int32)
+    act = buf("active", (E,), t.int32)
+    offs = buf("offsets", (E + 1,), t.int32)
+    tok = buf("tok", (T * top_k,), t.int32)
+    tokw = buf("tokw", (T * top_k,), t.float32)
+    bias = None
+    if scoring == "sigmoid" and e_score_bias is not None:
+        bias = nat.to_device(e_score_bias, t.float32)
+    sl = sc = None
+    if shared_logit is not None:
+        sl = nat.to_device(shared_logit, t.float32).reshape(-1)
+        sc = buf("shared_coef", (T,), t.float32)
+    sint = int(shared_inter or 0) if shared is not None else 0
+    need = moe_workspace_bytes(T, hidden, inter, sint, T * top_k)
+    ws = workspace
+    if ws is None or ws.numel() * ws.element_size() < need or not ws.is_contiguous():
+        ws = t.empty((need,), dtype=t.uint8, device=dev)
+    y = out if out is not None else t.empty((T, hidden), dtype=t.float32, device=dev)
+    sp = _stacked_ptrs(shared) if shared is not None else [None] * 6
+    h = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
+    rc = nat.lib().fastllm_moe_int4_routed(
+        nat.ptr(s), int(top_k), 1 if scoring == "sigmoid" else 0, 1 if norm_topk_prob else 0,
+        float(routed_scaling), nat.ptr(bias) if bias is not None else None, int(n_group or 0),
+        int(topk_group or 0), nat.ptr(sl) if sl is not None else None, nat.ptr(ids), nat.ptr(w),
+        nat.ptr(rw), nat.ptr(sc) if sc is not None else None, nat.ptr(na), nat.ptr(act),
+        nat.ptr(offs), nat.ptr(tok), nat.ptr(tokw), nat.ptr(x2), T, hidden, stacked["group"], E,
+        inter, *_stacked_ptrs(stacked), sint, *sp, nat.ptr(ws), ws.numel() * ws.element_size(),
+        nat.ptr(y), h)
+    nat.check_rc(rc, "fastllm_moe_int4_routed")
+    return y
+
+
 def fused_moe_weighted(x, stacked, rw, E, hidden, inter, out=None, inter_buf=None,
                        threads=256, rpb=8, aidx=None):
     """(E,)-routing-weight-driven selective MoE FFN (moe_int4.py:263-294):
@@ -362,9 +427,10 @@ def route_topk_gpu(logits, top_k, *, norm=False, scale=1.0, rw=None, aidx=None):
 
 def moe_branch(x, gate_w, stacked, top_k, *, E, hidden, inter, norm=False, scale=1.0,
                shared=None, shared_inter=0, shared_gate_w=None, bufs=None, stream=None):
-    """One fused MoE layer for T <= 16 tokens, all on the device with no host
-    sync (graph_decode._moe_branch, graph_decode.py:669-700):
-    gate matvec (+ shared gate) -> router -> fused routed + shared FFN.
+    """One fused MoE layer, all on the device with no host sync
+    (graph_decode._moe_branch, graph_decode.py:669-700): gate matvec (+
+    shared gate) -> router -> fused routed + shared FFN (one native call for
+    T <= 16 tokens).
     Returns (T, hidden) fp32.  ``bufs`` may carry persistent buffers for
     graph capture (keys of route_topk_device plus logits, slogit, workspace,
     out); missing ones are allocated and stored there."""
@@ -390,6 +456,18 @@ def moe_branch(x, gate_w, stacked, top_k, *, E, hidden, inter, norm=False, scale
                                        nat.ptr(logits), nat.ptr(sl) if sl is not None else None,
                                        T, E, hidden, h)
     nat.check_rc(rc, "fastllm_gate_matvec")
+    if T <= 16:
+        if "workspace" not in b:
+            b["workspace"] = t.empty((moe_workspace_bytes(T, hidden, inter,
+                                                          shared_inter if shared is not None else 0,
+                                                          T * top_k),),
+                                     dtype=t.uint8, device=xd.device)
+        if "out" not in b:
+            b["out"] = t.empty((T, hidden), dtype=t.float32, device=xd.device)
+        return moe_route_forward(xd, logits, stacked, top_k, E, hidden, inter,
+                                 norm_topk_prob=norm, routed_scaling=scale, shared=shared,
+                                 shared_inter=shared_inter, shared_logit=sl, route=b,
+                                 out=b["out"], workspace=b["workspace"], stream=stream)
     r = route_topk_device(logits, top_k, norm_topk_prob=norm, routed_scaling=scale,
                           shared_logit=sl, out=b, stream=stream)
     if "workspace" not in b:

@@ -307,21 +307,24 @@ int fastllm_moe_int4_tile_unpack(const uint8_t *qtile, const uint32_t *sz,
 size_t fastllm_moe_int4_workspace_bytes(int T, int hidden, int inter,
                                         int shared_inter, int max_entries);
 
-/* Fused selective INT4 MoE FFN for T <= 16 tokens (x fp32 [T, hidden],
- * hidden % 128 == 0, hidden <= 4096, inter <= 8192):
+/* Fused selective INT4 MoE FFN (x fp32 [T, hidden], hidden % 128 == 0):
  *   y[t] = sum_{entries p of t} tokw[p] * down_e(silu(gate_e x_t) * up_e x_t)
  *          + shared_coef[t] * shared(x_t)          (y fp32 [T, hidden])
  * driven by MoE lists (fastllm_route_topk / fastllm_moe_build_lists) with at
- * most max_slots slots and max_entries entries.  Experts in the tile layout
- * (fastllm_moe_int4_tile_repack of the stacked row-major arrays): gq/gsz,
- * uq/usz over rows E*inter, in_f hidden; dq/dsz over rows E*hidden, in_f
- * inter; the shared expert the same with E = 1 and shared_inter (0 = none;
- * shared_coef null = 1).  workspace: fastllm_moe_int4_workspace_bytes(T,
- * hidden, inter, shared_inter, max_entries) bytes, 16-byte aligned; calls
- * sharing one workspace must not overlap.  Two launches: gate/up + SwiGLU
- * over the routed tokens only (also zeroes y); down projection adding each
- * term into y with fp32 atomics, as the reference's moew_down does (the
- * last bits of y depend on the order of arrival).
+ * most max_slots (<= 256) slots and max_entries entries.  Experts in the tile
+ * layout (fastllm_moe_int4_tile_repack of the stacked row-major arrays):
+ * gq/gsz, uq/usz over rows E*inter, in_f hidden; dq/dsz over rows E*hidden,
+ * in_f inter; the shared expert the same with E = 1 and shared_inter (0 =
+ * none; shared_coef null = 1).  workspace: fastllm_moe_int4_workspace_bytes(
+ * T, hidden, inter, shared_inter, max_entries) bytes, 16-byte aligned; calls
+ * sharing one workspace must not overlap.
+ * T <= 16 (decode; hidden <= 4096, inter <= 8192): two launches --
+ * gate/up + SwiGLU over the routed tokens only (also zeroes y), then the
+ * down projection adding each term into y with fp32 atomics, as the
+ * reference's moew_down does (the last bits of y depend on the order of
+ * arrival).
+ * T > 16 (prefill, hidden % 256 == 0): grouped GEMM kernels on the matrix
+ * cores (fp16 copy of x, gate/up per slot in 64-row chunks, down).
  * Replaces: fused_moe_weighted (fastllm_py/kernels/moe_int4.py:175-294),
  * fused_moe_ffn2 (:300-396), fused_moe_ffn (:402-487) and the routed+shared
  * part of _moe_branch (fastllm_py/graph_decode.py:688-699). */
@@ -338,6 +341,33 @@ int fastllm_moe_int4_fused(const float *x, int T, int hidden, int group_size,
                            const int *tok, const float *tokw, int max_slots,
                            int max_entries, void *workspace,
                            size_t workspace_bytes, float *y, void *stream);
+
+/* Router + fused MoE of T <= 16 tokens in one call: fastllm_route_topk
+ * (same arguments, same outputs topk_ids/topk_w/rw/shared_coef and lists,
+ * bit for bit) followed by fastllm_moe_int4_fused over its lists with
+ * max_slots = min(E, T * top_k), max_entries = T * top_k and, when
+ * shared_logit is given, shared_coef = sigmoid(shared_logit) (shared_coef
+ * must then be given).  Every argument is checked before the first launch.
+ * Expert arguments and workspace as fastllm_moe_int4_fused.
+ * Replaces: the router + routed/shared expert launches of _moe_branch
+ * (fastllm_py/graph_decode.py:669-700). */
+int fastllm_moe_int4_routed(const float *logits, int top_k, int scoring,
+                            int norm, float routed_scaling,
+                            const float *e_score_bias, int n_group,
+                            int topk_group, const float *shared_logit,
+                            int *topk_ids, float *topk_w, float *rw,
+                            float *shared_coef, int *n_active, int *active,
+                            int *offsets, int *tok, float *tokw,
+                            const float *x, int T, int hidden, int group_size,
+                            int E, int inter, const uint8_t *gq,
+                            const uint32_t *gsz, const uint8_t *uq,
+                            const uint32_t *usz, const uint8_t *dq,
+                            const uint32_t *dsz, int shared_inter,
+                            const uint8_t *sgq, const uint32_t *sgsz,
+                            const uint8_t *suq, const uint32_t *susz,
+                            const uint8_t *sdq, const uint32_t *sdsz,
+                            void *workspace, size_t workspace_bytes, float *y,
+                            void *stream);
 
 #ifdef __cplusplus
 }

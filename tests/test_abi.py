@@ -48,7 +48,9 @@ def test_moe_entry_argument_checks():
     p = 1 << 20  # never dereferenced: validation fails or stops at the device check
     ws = lib.fastllm_moe_int4_workspace_bytes(1, 2048, 1408, 5632, 4)
     assert ws == (4 + 1) * 5632 * 2
-    assert lib.fastllm_moe_int4_workspace_bytes(17, 2048, 1408, 0, 4) == 0
+    # T > 16 takes the grouped kernels (hidden % 256 == 0)
+    assert lib.fastllm_moe_int4_workspace_bytes(17, 2048, 1408, 0, 68) > 0
+    assert lib.fastllm_moe_int4_workspace_bytes(17, 384, 1408, 0, 68) == 0
     assert lib.fastllm_moe_int4_workspace_bytes(1, 2000, 1408, 0, 4) == 0
 
     def fused(T=1, hidden=2048, gs=128, inter=1408, sinter=5632, ws_bytes=ws, slots=4, entries=4):
@@ -63,6 +65,22 @@ def test_moe_entry_argument_checks():
     assert fused(hidden=2000) == 1
     assert fused(ws_bytes=ws - 1) == 1
     assert fused(slots=0) == 1
-    assert fused(T=17) == 1
+    assert fused(T=17) == 1  # workspace sized for T = 1
+
+    def routed(T=1, E=60, k=4, scoring=0, sinter=5632, ws_bytes=ws, logits=p):
+        sh = [p] * 6 if sinter else [None] * 6
+        return lib.fastllm_moe_int4_routed(logits, k, scoring, 0, 1.0, None, 0, 0, p, *([p] * 9),
+                                           p, T, 2048, 128, E, 1408, *([p] * 6), sinter, *sh, p,
+                                           ws_bytes, p, None)
+
+    if not torch.cuda.is_available():
+        assert routed() == 2
+    assert routed(T=17) == 1
+    assert routed(k=0) == 1
+    assert routed(k=17) == 1
+    assert routed(E=300) == 1
+    assert routed(scoring=2) == 1
+    assert routed(logits=None) == 1
+    assert routed(ws_bytes=ws - 1) == 1
     assert lib.fastllm_moe_int4_tile_repack(p, p, p, p, p, 24, 256, 128, None) == 1  # rows % 16
     assert lib.fastllm_moe_int4_tile_repack(p, p, p, p, p, 32, 200, 128, None) == 1  # in % 128

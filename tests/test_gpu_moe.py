@@ -435,6 +435,61 @@ def test_fused_moe_shapes(torch_gpu, T, E, K, hidden, inter, sinter, gs):
     assert Q.max_abs_rel(y.cpu().numpy(), ref) < 5e-3
 
 
+@pytest.mark.parametrize("T,E,K,hidden,inter,sinter,gs,norm", [
+    (1, 60, 4, 2048, 1408, 5632, 128, False),  # config 4, one token
+    (16, 60, 4, 2048, 1408, 5632, 128, False),  # config 4, 16 tokens
+    (3, 16, 4, 512, 768, 1536, 128, True),
+    (16, 128, 16, 256, 256, 0, 64, True),        # 256 entries, group 64
+    (5, 6, 3, 384, 384, 3200, 32, False),         # group 32, shared in 9 pieces
+])
+def test_moe_route_forward(torch_gpu, T, E, K, hidden, inter, sinter, gs, norm):
+    """Router + fused MoE in one native call: routing outputs bit-exact vs the
+    router entry, y vs the two-call path (up to the atomic summation order)
+    and vs the fp32 oracle, over three calls in a row and a second stream."""
+    from fastllm_py.expert_router import route_topk_device
+    from fastllm_py.kernels import moe_int4
+
+    torch = torch_gpu
+    rng = np.random.default_rng(9000 + T * 13 + E + hidden)
+    st = moe_int4.build_stacked_experts(_experts(rng, E, hidden, inter, 0.05), gs)
+    sh = moe_int4.build_stacked_experts(_experts(rng, 1, hidden, sinter, 0.05), gs) if sinter else None
+    x = torch.from_numpy((rng.standard_normal((T, hidden)) * 0.5).astype(np.float32)).cuda()
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float16).astype(np.float32)).cuda()
+    sl = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).cuda() if sinter else None
+    ref_r = route_topk_device(logits, K, norm_topk_prob=norm, shared_logit=sl)
+    y2 = moe_int4.moe_forward(x, st, E, hidden, inter, ref_r, max_slots=min(E, T * K),
+                              max_entries=T * K, shared=sh, shared_inter=sinter,
+                              shared_coef=ref_r.get("shared_coef"))
+    ids, w = ref_r["topk_ids"].cpu().numpy(), ref_r["topk_w"].cpu().numpy()
+    coef = 1.0 / (1.0 + np.exp(-sl.cpu().numpy())) if sinter else None
+    ref = OM.moe_ref(x.cpu().numpy(), OM.dequant_stacked(_np_stacked(st), gs), ids, w,
+                     OM.dequant_stacked(_np_stacked(sh), gs) if sh else None, coef)
+    s2 = torch.cuda.Stream()
+    for call in range(4):
+        stream = s2 if call == 3 else None
+        r = {}
+        with torch.cuda.stream(s2 if stream is not None else torch.cuda.current_stream()):
+            y = moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, norm_topk_prob=norm,
+                                           shared=sh, shared_inter=sinter, shared_logit=sl,
+                                           route=r, stream=stream)
+        torch.cuda.synchronize()
+        for k in ("topk_ids", "topk_w", "rw", "n_active"):
+            np.testing.assert_array_equal(r[k].cpu().numpy().view(np.uint32),
+                                          ref_r[k].cpu().numpy().view(np.uint32), err_msg=k)
+        na = int(r["n_active"].item())
+        n_ent = int(ref_r["offsets"][na].item())
+        for k, n in (("active", na), ("offsets", na + 1), ("tok", n_ent), ("tokw", n_ent)):
+            np.testing.assert_array_equal(r[k][:n].cpu().numpy().view(np.uint32),
+                                          ref_r[k][:n].cpu().numpy().view(np.uint32), err_msg=k)
+        if sinter:
+            np.testing.assert_array_equal(r["shared_coef"].cpu().numpy().view(np.uint32),
+                                          ref_r["shared_coef"].cpu().numpy().view(np.uint32))
+        yc = y.cpu().numpy()
+        assert np.isfinite(yc).all(), call
+        assert Q.max_abs_rel(yc, y2.cpu().numpy()) < 1e-5, call
+        assert Q.max_abs_rel(yc, ref) < 5e-3, call
+
+
 def test_fused_moe_edge_lists(torch_gpu):
     """ffn2 with a repeated expert (two slots, summed), zero weights (dropped)
     and all-zero routing without a shared expert (y == 0)."""
