@@ -896,7 +896,10 @@ struct MoeArgs {
     float* y;  // (T, hidden) fp32
 };
 
-constexpr int kGuTiles = 2;  // 16-row tiles of gate and of up per workgroup
+// 16-row tiles of gate and of up per gate/up workgroup: one for up to
+// kGuOwnT tokens (more, smaller workgroups: one generation of them covers
+// the chip), four above (fewer, larger ones: more bytes per dispatch).
+constexpr int gu_tiles(int T) { return T <= 4 ? 1 : 4; }
 constexpr int kGuOwnT = 4;    // up to this many tokens each wave stages its own activations
 
 FL_DEV int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
@@ -927,15 +930,14 @@ FL_DEV int moe_kb(int wave, int i, int nwaves) {
 FL_DEV uint16_t sz_scale(uint32_t v) { return (uint16_t)(v & 0xFFFFu); }
 FL_DEV uint16_t sz_zero(uint32_t v) { return (uint16_t)(v >> 16); }
 
-// gate/up for kGuTiles 16-row tiles of one slot's expert over only the tokens
+// gate/up for TR 16-row tiles of one slot's expert over only the tokens
 // routed to it: h = silu(x Wg^T) * (x Wu^T) * w, stored fp16 in inter_buf.
 // The waves split the hidden (K) blocks, NB each; every weight load of a wave
 // (one 1 KB block per load) is issued before the token rows are gathered
 // into LDS.  Workgroup 0 also zeroes y for the down kernel's accumulation.
-template <bool G128, int NB>
+template <bool G128, int NB, int TR>
 __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    constexpr int TR = kGuTiles;
     const int nwaves = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1454,7 +1456,7 @@ void rm_dispatch(int nb, const void* X, const uint8_t* W, const uint16_t* S, con
 struct MoePlan {
     bool grouped;   // T > 16: the grouped-GEMM kernels
     size_t xh_off;  // grouped: workspace offset of the fp16 copy of x
-    int nb_gu, waves_gu, nb_d, trd, waves_d, pieces, inter_pad;
+    int nb_gu, waves_gu, tr_gu, nb_d, trd, waves_d, pieces, inter_pad;
     size_t lds_gu, lds_d, bytes;
 };
 
@@ -1480,8 +1482,9 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
     p.waves_gu = (nfh + p.nb_gu - 1) / p.nb_gu;
     const size_t as_bytes = T <= kGuOwnT ? (size_t)p.waves_gu * p.nb_gu * T * 256
                                          : (((size_t)T * (hidden + 8) * 2) + 15) & ~(size_t)15;
-    const size_t red_bytes = (size_t)p.waves_gu * 2 * kGuTiles * 1024;
-    p.lds_gu = (as_bytes > red_bytes ? as_bytes : red_bytes) + (size_t)2 * kGuTiles * 1024 + 16 * 4;
+    p.tr_gu = gu_tiles(T);
+    const size_t red_bytes = (size_t)p.waves_gu * 2 * p.tr_gu * 1024;
+    p.lds_gu = (as_bytes > red_bytes ? as_bytes : red_bytes) + (size_t)2 * p.tr_gu * 1024 + 16 * 4;
     if (p.lds_gu > 160 * 1024) return false;
     const int nfr = inter / 128;
     const int nb = (nfr + 7) / 8;
@@ -1499,8 +1502,14 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
 }
 
 template <bool G128, int NB>
-void launch_gate_up(const MoeArgs& a, int grid, const MoePlan& p, hipStream_t st) {
-    hipLaunchKernelGGL((moe_gate_up_k<G128, NB>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu, st, a);
+void launch_gate_up(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
+    const int TR = p.tr_gu;
+    const int grid = a.max_slots * (a.routed.inter / (16 * TR)) +
+                     (a.has_shared ? a.shared.inter / (16 * TR) : 0);
+    if (TR == 1)
+        hipLaunchKernelGGL((moe_gate_up_k<G128, NB, 1>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu, st, a);
+    else
+        hipLaunchKernelGGL((moe_gate_up_k<G128, NB, 4>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu, st, a);
 }
 
 template <bool G128, int NB>
@@ -1528,13 +1537,11 @@ void moe_launch_grouped(const MoeArgs& a, hipStream_t st) {
 
 template <bool G128>
 void moe_launch(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
-    const int grid_gu = a.max_slots * (a.routed.inter / (16 * kGuTiles)) +
-                        (a.has_shared ? a.shared.inter / (16 * kGuTiles) : 0);
     switch (p.nb_gu) {
-        case 1: launch_gate_up<G128, 1>(a, grid_gu, p, st); break;
-        case 2: launch_gate_up<G128, 2>(a, grid_gu, p, st); break;
-        case 3: launch_gate_up<G128, 3>(a, grid_gu, p, st); break;
-        default: launch_gate_up<G128, 4>(a, grid_gu, p, st); break;
+        case 1: launch_gate_up<G128, 1>(a, p, st); break;
+        case 2: launch_gate_up<G128, 2>(a, p, st); break;
+        case 3: launch_gate_up<G128, 3>(a, p, st); break;
+        default: launch_gate_up<G128, 4>(a, p, st); break;
     }
     switch (p.nb_d) {
         case 1: launch_down<G128, 1>(a, p, st); break;
