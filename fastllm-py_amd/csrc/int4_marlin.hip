@@ -242,7 +242,13 @@ __global__ __launch_bounds__(1024) void int4_tile_mm(
 //         system, which serialises the compute tail behind the stream;
 //       AM 1: the M x K rows are staged once per workgroup in LDS (row stride
 //         K+8 halves) behind an LDS-only barrier;
-//       AM 2: MFMA A operands are read from global memory at use.
+//       AM 2: MFMA A operands are read from global memory at use;
+//       AM 3 (M > 4, NB <= 4): each lane loads its own MFMA A operands of all
+//         its blocks from global memory into registers (4 x 16 B per block),
+//         first of all, so they arrive ahead of the weights in issue order;
+//         no LDS and no barrier -- the whole M x K staging of AM 1 needs so
+//         much LDS per workgroup (64 KB at M = 8, K = 4096) that only one
+//         workgroup fits a CU.
 //     MFMA rows >= M read row M-1: C rows are independent and rows >= M are
 //     never stored, so no masking is needed.
 //   * A trailing 64-k block (group 32 only) is done by wave 0 at the end.
@@ -298,6 +304,18 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
     // AM 0: lane l of block slot i copies row min(l / 16, M - 1), 16-byte
     // piece l % 16 of the block into this wave's LDS slot
     unsigned char* aslot = smem + (size_t)wave * NB * 1024;
+    const int arow_m = col < M ? col : M - 1;
+    f16x8 ar[NB][4];
+    if (AM == 3) {
+        const f16* ap = A + (size_t)arow_m * K + 8 * kq;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+            kb = kb < nfull ? kb : nfull - 1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ar[i][j] = *reinterpret_cast<const f16x8*>(ap + kb * 128 + 32 * j);
+        }
+    }
     if (AM == 0) {
         const int own_m = (lane >> 4) < M ? (lane >> 4) : M - 1;
         const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)M * K * 2);
@@ -353,7 +371,6 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
     }
 
     const uint32_t mlo = 0x64006400u, mhi = 0x54005400u;
-    const int arow_m = col < M ? col : M - 1;
     const f16* arow = ALDS ? As + (size_t)arow_m * lda + 8 * kq : A + (size_t)arow_m * K + 8 * kq;
     (void)aslot;
     f32x4 acc[T];
@@ -375,6 +392,8 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
             if (AM == 0)
                 a[j] = *reinterpret_cast<const f16x8*>(aslot + (size_t)i * 1024 + arow_m * 256 +
                                                        2 * (32 * j + 8 * kq));
+            else if (AM == 3)
+                a[j] = ar[i][j];
             else
                 a[j] = *reinterpret_cast<const f16x8*>(arow + kb * 128 + 32 * j);
         }
@@ -411,7 +430,7 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
     if (G32 && (K & 127) && wave == 0) {
         // trailing 64-k block: two 32-k groups
         f16x8 a[2];
-        const f16* arow_t = AM == 0 ? A + (size_t)arow_m * K + 8 * kq : arow;
+        const f16* arow_t = (AM == 0 || AM == 3) ? A + (size_t)arow_m * K + 8 * kq : arow;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
             a[j] = *reinterpret_cast<const f16x8*>(arow_t + nfull * 128 + 32 * j);
@@ -704,6 +723,9 @@ hipError_t launch_gemv_nb(const f16* A, const uint32_t* Wq, const uint16_t* S, c
     if (M <= 4 && own + red <= 160 * 1024)
         hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 0>), grid, block, own + red, stream, A, Wq, S, Z,
                            C, M, N, K);
+    else if (NB <= 4)
+        hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 3>), grid, block, red, stream, A, Wq, S, Z, C, M,
+                           N, K);
     else if (shared <= kGemvLdsCap)
         hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 1>), grid, block, shared + red, stream, A, Wq, S,
                            Z, C, M, N, K);
@@ -728,9 +750,28 @@ hipError_t dispatch_nb(int nb, const f16* A, const uint32_t* Wq, const uint16_t*
     }
 }
 
+// Four n-tiles per workgroup: half the workgroups of two tiles, so half the
+// activation reads per output (each workgroup reads all of A: M x K x 2
+// bytes, 128 KB at M = 16, K = 4096).  Register activations (AM 3) only.
+template <int NB, bool G32>
+hipError_t launch_gemv_t4(const f16* A, const uint32_t* Wq, const uint16_t* S, const uint32_t* Z,
+                          f16* C, int M, int N, int K, int waves, hipStream_t stream) {
+    const size_t red = (size_t)waves * 4 * 256 * sizeof(float);
+    hipLaunchKernelGGL((int4_gemv_nb<4, NB, G32, 3>), dim3(N / 64), dim3(64 * waves), red, stream, A, Wq,
+                       S, Z, C, M, N, K);
+    return hipGetLastError();
+}
+
 template <bool G32>
 hipError_t dispatch_gemv(const GemvCfg& c, const f16* A, const uint32_t* Wq, const uint16_t* S,
                          const uint32_t* Z, f16* C, int M, int N, int K, hipStream_t stream) {
+    if (c.tiles == 4) {
+        switch (c.nb) {
+            case 1: return launch_gemv_t4<1, G32>(A, Wq, S, Z, C, M, N, K, c.waves, stream);
+            case 2: return launch_gemv_t4<2, G32>(A, Wq, S, Z, C, M, N, K, c.waves, stream);
+            default: return launch_gemv_t4<4, G32>(A, Wq, S, Z, C, M, N, K, c.waves, stream);
+        }
+    }
     if (c.tiles == 2) return dispatch_nb<2, G32>(c.nb, A, Wq, S, Z, C, M, N, K, c.waves, stream);
     return dispatch_nb<1, G32>(c.nb, A, Wq, S, Z, C, M, N, K, c.waves, stream);
 }
@@ -749,21 +790,26 @@ int nb_bucket(int need) {
 // two tiles).  The register-slot count is the exact per-wave block share.
 GemvCfg default_gemv_cfg(int M, int N, int K, bool g32) {
     GemvCfg c;
-    c.tiles = ((N >= 16384) || (N >= 6144 && M >= 4)) ? 2 : 1;
+    // four tiles above M = 8 on wide N: each workgroup reads all of A, and
+    // the A bytes (M x K x 2 per workgroup) load the L1/TD path more than
+    // the weights do there
+    c.tiles = N >= 16384 ? (M > 8 ? 4 : 2) : ((N >= 6144 && M >= 4) ? 2 : 1);
     if (N % (16 * c.tiles)) c.tiles = 1;
     const int nfull = K / 128 > 0 ? K / 128 : 1;
     const int cap = g32 ? 4 : 8;
-    int waves = (N >= 16384 && M <= 4) ? 8 : 16;
+    int waves = (N >= 16384 && M <= 8) ? 8 : 16;
     while (waves > 1 && nfull < waves) waves /= 2;  // at least one block per wave
     while ((nfull + waves - 1) / waves > cap && waves < 16) waves *= 2;
     c.waves = waves;
     c.nb = nb_bucket((nfull + waves - 1) / waves);
     if (c.nb > cap) c.nb = cap;
+    if (c.tiles == 4 && c.nb > 4) c.tiles = 2;  // four tiles take register activations: nb <= 4
     return c;
 }
 
 bool gemv_cfg_ok(const GemvCfg& c, int M, int N, int K, bool g32) {
-    if (c.tiles != 1 && c.tiles != 2) return false;
+    if (c.tiles != 1 && c.tiles != 2 && c.tiles != 4) return false;
+    if (c.tiles == 4 && c.nb > 4) return false;
     if (c.waves < 1 || c.waves > 16) return false;
     if (N % (16 * c.tiles)) return false;
     const int nfull = K / 128;

@@ -163,3 +163,31 @@ def test_rejects_bad_shapes(torch_gpu):
     # group 64 is not a Marlin group size: the entry returns false, no launch
     assert not lib.FastllmCudaMarlinHalfInt4Gemm(a.data_ptr(), a.data_ptr(), a.data_ptr(),
                                                  a.data_ptr(), a.data_ptr(), 1, 64, 128, 64, None)
+
+
+@pytest.mark.parametrize("M", [5, 9, 16])
+@pytest.mark.parametrize("gs", [128, 32])
+def test_gemv_four_tiles(torch_gpu, M, gs):
+    """Wide N above M = 8 takes four n-tiles per workgroup with the
+    activations in registers; explicit launch configs of that variant too."""
+    from fastllm_py import _native
+    from fastllm_py.kernels import marlin
+
+    torch = torch_gpu
+    K, N = 2048, 16384
+    rng = np.random.default_rng(300 + M + gs)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    pay, w_hat, _ = _prep(torch, W, gs)
+    ref = Q.matmul_ref(a.astype(np.float32), w_hat)
+    ad = torch.from_numpy(a).cuda()
+    out = marlin.marlin_gemm_int4(ad, pay["qweight"], pay["scales"], pay["zeros"])
+    assert Q.max_abs_rel(out.float().cpu().numpy(), ref) < TOL
+    lib = _native.lib()
+    for tiles, waves, nb in ((4, 16, 1), (4, 8, 2), (4, 4, 4)):
+        y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        assert lib.fastllm_int4_gemm_config(ad.data_ptr(), pay["qweight"].data_ptr(),
+                                            pay["scales"].data_ptr(), pay["zeros"].data_ptr(),
+                                            y.data_ptr(), M, N, K, gs, tiles, waves, nb, None)
+        torch.cuda.synchronize()
+        assert Q.max_abs_rel(y.float().cpu().numpy(), ref) < TOL, (tiles, waves, nb)
