@@ -60,9 +60,15 @@ FL_DEV float act_to_f32(uint16_t v) {
 
 // INLINE: row stride `rs` bytes, block stride 132, scale after the codes.
 // !INLINE: row stride rs (= K), block stride 128, scales [N/128, nks].
-// ALDS: activations staged in LDS (M x K small enough); otherwise MFMA A
-// fragments are read from global memory (L2) at use.
-template <int T, int NB, bool INLINE, bool BF16, bool ALDS>
+// Activations (AM):
+//   AM 0 (M <= 4): each wave copies the rows of its own blocks global -> LDS
+//     (buffer_load ... lds, 1 KB = 4 rows x 128 k per block) before its
+//     weight loads and waits only for them -- no workgroup barrier;
+//   AM 1: M x K staged in LDS per workgroup (barrier that waits for LDS only);
+//   AM 2: MFMA A fragments read from global memory (L2) at use;
+//   AM 3 (M > 4, NB <= 4): each lane loads its own A fragments of all its
+//     blocks into registers first of all (no LDS, no barrier).
+template <int T, int NB, bool INLINE, bool BF16, int AM>
 __global__ __launch_bounds__(1024) void fp8_gemv_nb(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ Sc,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int rs,
@@ -77,8 +83,11 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
     const int col = lane & 15;
     const int kq = lane >> 4;
     const int lda = K + 8;
+    constexpr bool ALDS = AM == 1;
     uint16_t* As = reinterpret_cast<uint16_t*>(smem);
-    float* red = reinterpret_cast<float*>(smem + (ALDS ? (((size_t)M * lda * 2 + 15) & ~(size_t)15) : 0));
+    const size_t abytes = AM == 0 ? (size_t)nwaves * NB * 1024
+                                  : (ALDS ? (((size_t)M * lda * 2 + 15) & ~(size_t)15) : 0);
+    float* red = reinterpret_cast<float*>(smem + abytes);
 
     const int nb = wave < nfull ? (nfull - wave + nwaves - 1) / nwaves : 0;
     const int sw = ALDS ? stage_waves(M, K) : 0;
@@ -86,6 +95,34 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
     RowStager stg;
     const bool stager = ALDS && early && wave < sw;
     if (stager) stg.load(A, M, K, lda, wave, lane);
+    const int arow_m = col < M ? col : M - 1;
+    // AM 0: lane l of block slot i copies row min(l / 16, M - 1), 16-byte
+    // piece l % 16 of the block into this wave's LDS slot
+    unsigned char* aslot = smem + (size_t)wave * NB * 1024;
+    if (AM == 0) {
+        const int own_m = (lane >> 4) < M ? (lane >> 4) : M - 1;
+        const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)M * K * 2);
+        const uint32_t ao = 2u * ((uint32_t)own_m * K + 8 * (lane & 15));
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+            kb = kb < nfull ? kb : nfull - 1;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(aslot + i * 1024), 16, ao, kb * 256, 0, 0);
+        }
+    }
+    u32x4 ar[NB][4];
+    if (AM == 3) {
+        const uint16_t* ap = A + (size_t)arow_m * K + 16 * kq;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+            kb = kb < nfull ? kb : nfull - 1;
+            ar[i][0] = *reinterpret_cast<const u32x4*>(ap + kb * 128);
+            ar[i][1] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 8);
+            ar[i][2] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 64);
+            ar[i][3] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 72);
+        }
+    }
 
     const uint8_t* rbase[T];
     int nrow[T];
@@ -114,13 +151,21 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    if (AM == 0) {
+        // this wave's activation copies, issued before its weight loads, are
+        // done once at most the weight loads are outstanding: two vector
+        // loads per (block, tile) of codes; the block scale may be a third
+        // (inline rows) or a scalar load (uniform address in the 128 x 128
+        // format), so count only the two -- a stricter wait, never a shorter
+        constexpr int WL = NB * T * 2;
+        wait_vmcnt<(WL < 63 ? WL : 63)>();
+    }
     if (ALDS) {
         if (stager) stg.store(As);
         if (!early) stage_rows_loop(A, As, M, K, lda);
         lds_barrier();  // the weight loads stay in flight
     }
 
-    const int arow_m = col < M ? col : M - 1;
     const uint16_t* arow = ALDS ? As + (size_t)arow_m * lda + 16 * kq : A + (size_t)arow_m * K + 16 * kq;
     f32x4 acc[T];
 #pragma unroll
@@ -131,11 +176,25 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
         const bool live = i < nb;
         int kb = wave + (live ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
         kb = kb < nfull ? kb : nfull - 1;
-        const uint16_t* ak = arow + kb * 128;
-        const u32x4 a0 = *reinterpret_cast<const u32x4*>(ak);
-        const u32x4 a1 = *reinterpret_cast<const u32x4*>(ak + 8);
-        const u32x4 a2 = *reinterpret_cast<const u32x4*>(ak + 64);
-        const u32x4 a3 = *reinterpret_cast<const u32x4*>(ak + 72);
+        u32x4 a0, a1, a2, a3;
+        if (AM == 0) {
+            const unsigned char* ak = aslot + (size_t)i * 1024 + arow_m * 256 + 32 * kq;
+            a0 = *reinterpret_cast<const u32x4*>(ak);
+            a1 = *reinterpret_cast<const u32x4*>(ak + 16);
+            a2 = *reinterpret_cast<const u32x4*>(ak + 128);
+            a3 = *reinterpret_cast<const u32x4*>(ak + 144);
+        } else if (AM == 3) {
+            a0 = ar[i][0];
+            a1 = ar[i][1];
+            a2 = ar[i][2];
+            a3 = ar[i][3];
+        } else {
+            const uint16_t* ak = arow + kb * 128;
+            a0 = *reinterpret_cast<const u32x4*>(ak);
+            a1 = *reinterpret_cast<const u32x4*>(ak + 8);
+            a2 = *reinterpret_cast<const u32x4*>(ak + 64);
+            a3 = *reinterpret_cast<const u32x4*>(ak + 72);
+        }
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -152,7 +211,7 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
 
     if (!INLINE && (K & 127) && wave == 0) {
         // trailing 64-wide block: bytes [16q, 16q+16) only
-        const uint16_t* ak = arow + nfull * 128;
+        const uint16_t* ak = (AM == 0 || AM == 3 ? A + (size_t)arow_m * K + 16 * kq : arow) + nfull * 128;
         const u32x4 a0 = *reinterpret_cast<const u32x4*>(ak);
         const u32x4 a1 = *reinterpret_cast<const u32x4*>(ak + 8);
 #pragma unroll
@@ -323,6 +382,146 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q4(
     }
 }
 
+// Decode GEMV for 4 < M <= 8 on 8-row tiles ("halved" MFMA), the q4 scheme
+// with two k-parts: B column 8 h + r = weight row r in half h of K, A row
+// 8 h' + m = activation row m in half h'; the diagonal blocks h' == h are the
+// half partial sums.  A workgroup needs 8 weight rows (N = 2048: 256
+// workgroups instead of 128).  M x K activations are too large for LDS here
+// (8 x 10944 bf16 = 175 KB), so each lane loads its own A fragments of all
+// its slots into registers, ahead of its weight loads.
+//   * Half h holds blocks [h HB, (h + 1) HB) (HB = ceil(nfull / 2)); waves
+//     take slots round-robin, NB at most; blocks past nfull repeat the last
+//     one with a zero scale.
+//   * Accumulator element e of lane l is A row 4 (l / 16) + e: half
+//     (l / 16) / 2, activation row 4 ((l / 16) % 2) + e; it is a diagonal
+//     element when that half equals the lane's column half.
+template <int NB, bool INLINE, bool BF16>
+__global__ __launch_bounds__(1024) void fp8_gemv_q2(
+    const uint16_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ Sc,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int rs,
+    int nks) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int BSTRIDE = INLINE ? 132 : 128;
+    const int nwaves = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row0 = blockIdx.x * 8;
+    const int nfull = K >> 7;
+    const int HB = (nfull + 1) >> 1;
+    const int col = lane & 15, kq = lane >> 4;
+    const int r = col & 7, h = col >> 3;  // B column (row, half) and A row (half, activation row)
+    const int nb = wave < HB ? (HB - wave + nwaves - 1) / nwaves : 0;
+    auto slot_b = [&](int i) { return wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves; };
+
+    // A fragments first: lane (col, kq) = activation row col % 8 (clamped),
+    // half col / 8, k 16 kq + {0, 8, 64, 72} of the slot's block
+    const int arow = (col & 7) < M ? (col & 7) : M - 1;
+    const uint16_t* ap = A + (size_t)arow * K + 16 * kq;
+    u32x4 ar[NB][4];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        int kb = h * HB + slot_b(i);
+        kb = kb < nfull ? kb : nfull - 1;
+        ar[i][0] = *reinterpret_cast<const u32x4*>(ap + kb * 128);
+        ar[i][1] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 8);
+        ar[i][2] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 64);
+        ar[i][3] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 72);
+    }
+    const int wrow = row0 + r < N ? row0 + r : N - 1;
+    const uint8_t* rbase = W + (size_t)wrow * rs;
+    u32x4 lo[NB], hi[NB];
+    float sv[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const int kbr = h * HB + slot_b(i);
+        const int kb = kbr < nfull ? kbr : nfull - 1;
+        const uint8_t* bp = rbase + (size_t)kb * BSTRIDE;
+        lo[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(bp + 16 * kq));
+        hi[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(bp + 64 + 16 * kq));
+        const float sc = INLINE ? *reinterpret_cast<const float*>(bp + 128) : Sc[(size_t)(wrow >> 7) * nks + kb];
+        sv[i] = (i < nb && kbr < nfull) ? sc : 0.0f;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+        part = mfma16<BF16>(ar[i][0], fp8x8_to_16<BF16>(lo[i][0], lo[i][1]), part);
+        part = mfma16<BF16>(ar[i][1], fp8x8_to_16<BF16>(lo[i][2], lo[i][3]), part);
+        part = mfma16<BF16>(ar[i][2], fp8x8_to_16<BF16>(hi[i][0], hi[i][1]), part);
+        part = mfma16<BF16>(ar[i][3], fp8x8_to_16<BF16>(hi[i][2], hi[i][3]), part);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(sv[i], part[e], acc[e]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    if (!INLINE && (K & 127) && wave == 0) {
+        // trailing 64-wide block, through half 0 only (columns and A rows of
+        // half 1 carry zeros)
+        const int kt = nfull * 128;
+        u32x4 a0 = u32x4{0u, 0u, 0u, 0u}, a1 = a0, w = a0;
+        if (h == 0) {
+            const uint16_t* at = A + (size_t)arow * K + kt + 16 * kq;
+            a0 = *reinterpret_cast<const u32x4*>(at);
+            a1 = *reinterpret_cast<const u32x4*>(at + 8);
+            w = *reinterpret_cast<const u32x4_a4*>(rbase + (size_t)nfull * BSTRIDE + 16 * kq);
+        }
+        f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+        part = mfma16<BF16>(a0, fp8x8_to_16<BF16>(w[0], w[1]), part);
+        part = mfma16<BF16>(a1, fp8x8_to_16<BF16>(w[2], w[3]), part);
+        const float st = Sc[(size_t)(wrow >> 7) * nks + nfull];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(st, part[e], acc[e]);
+    }
+
+    // diagonal elements: half (kq / 2) == h, activation row 4 (kq % 2) + e
+    float* red = reinterpret_cast<float*>(smem);
+    if ((kq >> 1) == h) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) red[(wave * 16 + col) * 8 + 4 * (kq & 1) + e] = acc[e];
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int rr = threadIdx.x >> 3, m = threadIdx.x & 7;
+        const int n = row0 + rr;
+        if (m < M && n < N) {
+            float v = 0.f;
+            for (int w = 0; w < nwaves; ++w)
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) v += red[(w * 16 + 8 * hh + rr) * 8 + m];
+            if (bias) v += act_to_f32<BF16>(bias[n]);
+            C[(size_t)m * N + n] = f32_to_act<BF16>(v);
+        }
+    }
+}
+
+template <int NB, bool INLINE, bool BF16>
+hipError_t launch_fp8_q2(const uint16_t* A, const uint8_t* W, const float* Sc, const uint16_t* bias,
+                         uint16_t* C, int M, int N, int K, int rs, int nks, int waves,
+                         hipStream_t st) {
+    const size_t lds = (size_t)waves * 16 * 8 * sizeof(float);
+    hipLaunchKernelGGL((fp8_gemv_q2<NB, INLINE, BF16>), dim3((N + 7) / 8), dim3(64 * waves), lds, st,
+                       A, W, Sc, bias, C, M, N, K, rs, nks);
+    return hipGetLastError();
+}
+
+// 4 < M <= 8 and few 16-row strips: the halved 8-row kernel
+template <bool INLINE, bool BF16>
+hipError_t fp8_q2(const uint16_t* A, const uint8_t* W, const float* Sc, const uint16_t* bias,
+                  uint16_t* C, int M, int N, int K, int rs, int nks, hipStream_t st) {
+    const int HB = ((K >> 7) + 1) >> 1;
+    const int nb = (HB + 15) / 16;
+    const int waves = (HB + nb - 1) / nb;
+    switch (nb) {
+        case 1: return launch_fp8_q2<1, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        case 2: return launch_fp8_q2<2, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        case 3: return launch_fp8_q2<3, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        case 4: return launch_fp8_q2<4, INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, waves, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 template <int NB, bool INLINE, bool BF16>
 hipError_t launch_fp8_q4(const uint16_t* A, const uint8_t* W, const float* Sc, const uint16_t* bias,
                          uint16_t* C, int M, int N, int K, int rs, int nks, int waves,
@@ -375,15 +574,21 @@ hipError_t launch_fp8(const uint16_t* A, const uint8_t* W, const float* Sc, cons
                       uint16_t* C, int M, int N, int K, int rs, int nks, int waves,
                       hipStream_t st) {
     const size_t abytes = (((size_t)M * (K + 8) * 2 + 15) & ~(size_t)15);
-    const bool alds = abytes <= kFp8LdsCap;
-    const size_t lds = (alds ? abytes : 0) + (size_t)waves * T * 1024;
+    const size_t red = (size_t)waves * T * 1024;
+    const size_t own = (size_t)waves * NB * 1024;
     const int strips = (N + 16 * T - 1) / (16 * T);
-    if (alds)
-        hipLaunchKernelGGL((fp8_gemv_nb<T, NB, INLINE, BF16, true>), dim3(strips), dim3(64 * waves),
-                           lds, st, A, W, Sc, bias, C, M, N, K, rs, nks);
+    if (M <= 4 && own + red <= 160 * 1024)
+        hipLaunchKernelGGL((fp8_gemv_nb<T, NB, INLINE, BF16, 0>), dim3(strips), dim3(64 * waves),
+                           own + red, st, A, W, Sc, bias, C, M, N, K, rs, nks);
+    else if (NB <= 4)
+        hipLaunchKernelGGL((fp8_gemv_nb<T, NB, INLINE, BF16, 3>), dim3(strips), dim3(64 * waves), red,
+                           st, A, W, Sc, bias, C, M, N, K, rs, nks);
+    else if (abytes <= kFp8LdsCap)
+        hipLaunchKernelGGL((fp8_gemv_nb<T, NB, INLINE, BF16, 1>), dim3(strips), dim3(64 * waves),
+                           abytes + red, st, A, W, Sc, bias, C, M, N, K, rs, nks);
     else
-        hipLaunchKernelGGL((fp8_gemv_nb<T, NB, INLINE, BF16, false>), dim3(strips),
-                           dim3(64 * waves), lds, st, A, W, Sc, bias, C, M, N, K, rs, nks);
+        hipLaunchKernelGGL((fp8_gemv_nb<T, NB, INLINE, BF16, 2>), dim3(strips), dim3(64 * waves), red,
+                           st, A, W, Sc, bias, C, M, N, K, rs, nks);
     return hipGetLastError();
 }
 
@@ -408,6 +613,9 @@ hipError_t fp8_gemm(const uint16_t* A, const uint8_t* W, const float* Sc, const 
     // few 16-row strips and M <= 4: the quartered 4-row kernel
     if (M <= 4 && K >= 512 && K <= 32768 && N < 8192 && N % 4 == 0)
         return fp8_q4<INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, st);
+    // 4 < M <= 8 there: the halved 8-row kernel (K <= 128 x 2 x 64)
+    if (M <= 8 && K >= 512 && K <= 16384 && N < 8192 && N % 8 == 0)
+        return fp8_q2<INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, st);
     // decode-shaped kernel, 16 activation rows per launch
     for (int m0 = 0; m0 < M; m0 += 16) {
         const int Mc = (M - m0) < 16 ? (M - m0) : 16;

@@ -139,13 +139,15 @@ def test_fp8_block_gemv_config3(torch_gpu, M, N, K):
     assert Q.max_abs_rel(out.float().cpu().numpy(), ref) < TOL
 
 
-def test_fp8_block_gemv_fp16_bias_ragged(torch_gpu):
+# N not a multiple of 16, K ending in a 64-wide block; the last two take the
+# halved 8-row kernel (4 < M <= 8, K >= 512)
+@pytest.mark.parametrize("N,K,M", [(200, 320, 5), (200, 704, 6), (2000, 1088, 8)])
+def test_fp8_block_gemv_fp16_bias_ragged(torch_gpu, N, K, M):
     from fastllm_py import quantizer
     from fastllm_py.kernels import fp8
 
     torch = torch_gpu
-    rng = np.random.default_rng(77)
-    N, K, M = 200, 320, 5  # N not a multiple of 16, K ends in a 64-wide block
+    rng = np.random.default_rng(77 + N + K + M)
     W = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda().half()
     b = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).cuda().half()
