@@ -371,6 +371,73 @@ def cpu_baseline_int4(budget_s=15.0):
     }
 
 
+def cpu_baseline_fp8(budget_s=6.0):
+    """Config 3 at M=1 on the host through the numpy oracle: per call,
+    dequantize the 128x128-block e4m3 weight to fp32, then the fp32 GEMV
+    (the three shapes, summed)."""
+    from oracle import quant as Q
+
+    rng = np.random.default_rng(3100)
+    mats = []
+    for _, N, K in FP8_SHAPES:
+        W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        q, sc = Q.quantize_fp8_block(W, 128)
+        mats.append((q, sc, rng.standard_normal((1, K)).astype(np.float32)))
+        del W
+    reps, t_total = 0, 0.0
+    while t_total < budget_s and reps < 30:
+        t0 = time.perf_counter()
+        for q, sc, x in mats:
+            _ = Q.matmul_ref(x, Q.dequantize_fp8_block(q, sc, 128))
+        t_total += time.perf_counter() - t0
+        reps += 1
+    return {"us_per_sum_M1": round(t_total / reps * 1e6, 1), "cores": os.cpu_count(), "kind": "port",
+            "sample": f"numpy oracle: dequantize-then-fp32-GEMV of the 3 config-3 shapes at M=1, "
+                      f"{reps} reps in {t_total:.1f}s"}
+
+
+def cpu_baseline_moe(budget_s=6.0):
+    """Config 4 at T=1 on the host through the numpy oracle, the reference's
+    CPU semantics (fastllm_py/moe.py:161-175): route_topk, then per routed
+    expert and for the shared expert dequantize the row-major INT4 weights to
+    fp32 and run the FFN; only the touched experts are dequantized.  The four
+    routed experts are built once and stand for whichever the router picks
+    (the cost does not depend on which)."""
+    from oracle import moe as OM
+    from oracle import quant as Q
+    from oracle import router as R
+
+    E, hidden, inter, sinter, K = 60, 2048, 1408, 5632, 4
+    rng = np.random.default_rng(3200)
+
+    def expert(n_inter):
+        return {f"{p}.{k}": v for p, shp in (("gate", (n_inter, hidden)), ("up", (n_inter, hidden)),
+                                             ("down", (hidden, n_inter)))
+                for k, v in zip(("qweight", "scales", "zeros"),
+                                Q.quantize_int4_rowmajor((rng.standard_normal(shp) * 0.02)
+                                                         .astype(np.float32)[None], 128))}
+    routed = [expert(inter) for _ in range(K)]
+    shared = expert(sinter)
+    x = rng.standard_normal((1, hidden)).astype(np.float16).astype(np.float32)
+    logits = rng.standard_normal((1, E)).astype(np.float16).astype(np.float32)
+    reps, t_total = 0, 0.0
+    while t_total < budget_s and reps < 30:
+        t0 = time.perf_counter()
+        _, idx, w = R.route_topk(logits, K, return_arrays=True)
+        y = np.zeros((1, hidden), np.float32)
+        for j in range(K):
+            d = OM.dequant_stacked(routed[j], 128)
+            y += w[0, j] * OM.expert_ffn(x, d["gate"][0], d["up"][0], d["down"][0])
+        d = OM.dequant_stacked(shared, 128)
+        y += OM.expert_ffn(x, d["gate"][0], d["up"][0], d["down"][0])
+        t_total += time.perf_counter() - t0
+        reps += 1
+    return {"us_per_layer_T1": round(t_total / reps * 1e6, 1), "cores": os.cpu_count(),
+            "kind": "port",
+            "sample": f"numpy oracle: route_topk + dequantize-then-fp32 FFN of 4 routed experts and "
+                      f"the shared one at T=1, {reps} reps in {t_total:.1f}s"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -460,6 +527,12 @@ def main():
     if not args.no_cpu_baseline:
         log("timing CPU baseline (numpy oracle) ...")
         cpu = cpu_baseline_int4()
+        if "fp8_b128x128_bf16" in breakdown:
+            breakdown["fp8_b128x128_bf16"]["cpu_baseline"] = cpu_baseline_fp8()
+        if "moe_qwen15_a27b_int4" in breakdown:
+            breakdown["moe_qwen15_a27b_int4"]["cpu_baseline"] = cpu_baseline_moe()
+        log(f"CPU baselines: fp8 {breakdown.get('fp8_b128x128_bf16', {}).get('cpu_baseline')} "
+            f"moe {breakdown.get('moe_qwen15_a27b_int4', {}).get('cpu_baseline')}")
 
     out = {
         "metric": "INT4/FP8 GEMV HBM GB/s (% of peak) at Qwen3-8B shapes; fused-MoE us/layer",
