@@ -139,6 +139,44 @@ def run_int4(torch, lib, layers, M, steps, stream):
     return ms_step, per, reps * per_graph
 
 
+def run_swiglu(torch, lib, layers, stream, M_list=(1, 8)):
+    """gate_up 24576x4096 with the SwiGLU epilogue in one launch
+    (fastllm_int4_gemm_swiglu), beside the gate_up GEMV alone -- the unfused
+    pair costs that plus a separate swiglu kernel launch."""
+    N, K = 24576, 4096
+    res = {}
+    for M in M_list:
+        x = torch.randn((M, K), device="cuda").to(torch.float16)
+        y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        hbuf = torch.empty((M, N // 2), dtype=torch.float16, device="cuda")
+
+        def fused(p):
+            args = (x.data_ptr(), p["qweight"].data_ptr(), p["scales"].data_ptr(),
+                    p["zeros"].data_ptr(), hbuf.data_ptr(), M, N, K, GS)
+
+            def go(h):
+                if lib.fastllm_int4_gemm_swiglu(*args, h) != 0:
+                    raise RuntimeError("swiglu GEMV rejected")
+            return go
+
+        def gemv(p):
+            args = (x.data_ptr(), p["qweight"].data_ptr(), p["scales"].data_ptr(),
+                    p["zeros"].data_ptr(), y.data_ptr(), M, N, K, GS, None)
+
+            def go(h):
+                if not lib.FastllmCudaMarlinHalfInt4GemmStream(*args, h):
+                    raise RuntimeError("INT4 GEMM rejected")
+            return go
+        L = len(layers)
+        r1 = max(1, -(-48 // L))
+        tf = graph_time(torch, stream, [fused(layers[c]["gate_up"]) for _ in range(r1)
+                                        for c in range(L)], 4) / (r1 * L) * 1e3
+        tg = graph_time(torch, stream, [gemv(layers[c]["gate_up"]) for _ in range(r1)
+                                        for c in range(L)], 4) / (r1 * L) * 1e3
+        res[f"M{M}"] = {"fused_us": round(tf, 3), "gemv_alone_us": round(tg, 3)}
+    return res
+
+
 # ------------------------------------------------------------------- FP8
 def run_fp8(torch, lib, stream, M_list=(1, 8)):
     from fastllm_py import quantizer
@@ -445,7 +483,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--only", default="int4,fp8,moe,gemm")
+    ap.add_argument("--only", default="int4,swiglu,fp8,moe,gemm")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy a 64 MiB buffer 5 times (a known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -494,6 +532,9 @@ def main():
                  "us_per_layer": round(v["ms_per_layer"] * 1e3, 3),
                  "us_per_call": {k: round(u, 3) for k, u in v["us_per_call"].items()}}
         for m, v in per_m.items()}
+    if "swiglu" in only:
+        breakdown["int4_gate_up_swiglu"] = run_swiglu(torch, lib, layers, stream)
+        log(f"gate_up + SwiGLU: {breakdown['int4_gate_up_swiglu']}")
     del layers
     torch.cuda.empty_cache()
 

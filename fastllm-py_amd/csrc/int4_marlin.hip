@@ -253,7 +253,13 @@ __global__ __launch_bounds__(1024) void int4_tile_mm(
 //     never stored, so no masking is needed.
 //   * A trailing 64-k block (group 32 only) is done by wave 0 at the end.
 //   * Cross-wave reduction through LDS in fixed wave order.
-template <int T, int NB, bool G32, int AM>
+// SWI (T = 2): gate/up with the SwiGLU epilogue -- N = 2 I columns, gate
+// rows [0, I) and up rows [I, 2 I); strip s pairs gate n-tile s (tile 0)
+// with up n-tile I/16 + s (tile 1) and stores H[m, 16 s + c] =
+// fp16(silu(g) * u) from the fp16-rounded g and u, which is what the
+// unfused GEMV followed by the reference's swiglu computes
+// (fastllm_py/kernels/ops.py:157-163).  C is then H, M x I.
+template <int T, int NB, bool G32, int AM, bool SWI = false>
 __global__ __launch_bounds__(1024) void int4_gemv_nb(
     const f16* __restrict__ A, const uint32_t* __restrict__ Wq, const uint16_t* __restrict__ S,
     const uint32_t* __restrict__ Z, f16* __restrict__ C, int M, int N, int K) {
@@ -281,12 +287,13 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
     const uint32_t* tbase[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        const int n = (strip * T + t) * 16 + col;
+        const int nt = SWI ? t * (N >> 5) + strip : strip * T + t;  // n-tile of tile t
+        const int n = nt * 16 + col;
         spos[t] = marlin_scale_pos(n);
         const int cl = n & 63;
         zw[t] = ((n >> 6) << 3) + (cl & 7);
         zsh[t] = 4 * slot_of(cl >> 3);
-        tbase[t] = Wq + (size_t)(strip * T + t) * (2 * (size_t)K);
+        tbase[t] = Wq + (size_t)nt * (2 * (size_t)K);
     }
 
     // Activations are staged by the first `sw` waves (RowStager: their
@@ -456,6 +463,21 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
     for (int t = 0; t < T; ++t)
         *reinterpret_cast<f32x4*>(red + (wave * T + t) * 256 + lane * 4) = acc[t];
     __syncthreads();
+    if (SWI) {
+        for (int idx = threadIdx.x; idx < 256; idx += blockDim.x) {
+            const int l = idx >> 2, e = idx & 3;
+            const int m = 4 * (l >> 4) + e;
+            if (m >= M) continue;
+            float g = 0.f, u = 0.f;
+            for (int w = 0; w < nwaves; ++w) {
+                g += red[(w * T) * 256 + idx];
+                u += red[(w * T + 1) * 256 + idx];
+            }
+            const float gf = (float)(f16)g, uf = (float)(f16)u;
+            C[(size_t)m * (N >> 1) + strip * 16 + (l & 15)] = (f16)(gf / (1.0f + expf(-gf)) * uf);
+        }
+        return;
+    }
     for (int idx = threadIdx.x; idx < T * 256; idx += blockDim.x) {
         const int l = (idx & 255) >> 2, e = idx & 3, t = idx >> 8;
         const int m = 4 * (l >> 4) + e;
@@ -919,6 +941,42 @@ bool int4_marlin_abi_gemm(const void* a, const uint32_t* q, const void* scales,
     return report(e, "FastllmCudaMarlinHalfInt4Gemm");
 }
 
+// gate/up GEMV + SwiGLU (M <= 16, N = 2 I, I % 64 == 0): two n-tiles per
+// workgroup (gate s, up s), per-wave activation copies up to M = 4, register
+// activations above.
+template <int NB, bool G32>
+hipError_t launch_gemv_swiglu(const f16* A, const uint32_t* Wq, const uint16_t* S, const uint32_t* Z,
+                              f16* H, int M, int N, int K, int waves, hipStream_t stream) {
+    const size_t red = (size_t)waves * 2 * 256 * sizeof(float);
+    const size_t own = (size_t)waves * NB * 1024;
+    const dim3 grid(N / 32), block(64 * waves);
+    if (M <= 4)
+        hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 0, true>), grid, block, own + red, stream, A, Wq, S,
+                           Z, H, M, N, K);
+    else
+        hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 3, true>), grid, block, red, stream, A, Wq, S, Z, H,
+                           M, N, K);
+    return hipGetLastError();
+}
+
+template <bool G32>
+hipError_t dispatch_swiglu(const f16* A, const uint32_t* Wq, const uint16_t* S, const uint32_t* Z,
+                           f16* H, int M, int N, int K, hipStream_t stream) {
+    // the decode config of this shape, with NB <= 4 (register activations)
+    const int nfull = K / 128 > 0 ? K / 128 : 1;
+    int waves = (N >= 16384 && M <= 8) ? 8 : 16;
+    while (waves > 1 && nfull < waves) waves /= 2;
+    while ((nfull + waves - 1) / waves > 4 && waves < 16) waves *= 2;
+    const int nb = (nfull + waves - 1) / waves;
+    switch (nb) {
+        case 1: return launch_gemv_swiglu<1, G32>(A, Wq, S, Z, H, M, N, K, waves, stream);
+        case 2: return launch_gemv_swiglu<2, G32>(A, Wq, S, Z, H, M, N, K, waves, stream);
+        case 3: return launch_gemv_swiglu<3, G32>(A, Wq, S, Z, H, M, N, K, waves, stream);
+        case 4: return launch_gemv_swiglu<4, G32>(A, Wq, S, Z, H, M, N, K, waves, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 bool int4_repack(const uint32_t* src, uint32_t* dst, int K, int N, bool inverse,
                  hipStream_t stream) {
     if (!src || !dst || K <= 0 || N <= 0 || K % 64 != 0 || N % 64 != 0) return false;
@@ -984,6 +1042,27 @@ bool fastllm_int4_gemm_config(const void* a, const uint32_t* b_q_weight, const v
     if (size_m > 16) return false;
     return int4_marlin_abi_gemm(a, b_q_weight, b_scales, b_zeros, c, size_m, size_n, size_k,
                                 group_size, (hipStream_t)stream, &cfg);
+}
+
+int fastllm_int4_gemm_swiglu(const void* a, const uint32_t* b_q_weight, const void* b_scales,
+                             const uint32_t* b_zeros, void* h, int size_m, int size_n, int size_k,
+                             int group_size, void* stream) {
+    if (size_m < 1 || size_m > 16 || size_n % 128 != 0 || size_k % 128 != 0 || size_k > 65536)
+        return 1;
+    if (group_size != 32 && group_size != 128) return 1;
+    if (!a || !b_q_weight || !b_scales || !b_zeros || !h) return 1;
+    if (!fl_aligned(a, 16) || !fl_aligned(b_q_weight, 16) || !fl_aligned(h, 2) ||
+        !fl_aligned(b_scales, 2) || !fl_aligned(b_zeros, 4))
+        return 1;
+    if (!fl_current_device_supported()) return 2;
+    const f16* A = static_cast<const f16*>(a);
+    const uint16_t* S = static_cast<const uint16_t*>(b_scales);
+    f16* H = static_cast<f16*>(h);
+    const hipError_t e =
+        group_size == 32
+            ? dispatch_swiglu<true>(A, b_q_weight, S, b_zeros, H, size_m, size_n, size_k, (hipStream_t)stream)
+            : dispatch_swiglu<false>(A, b_q_weight, S, b_zeros, H, size_m, size_n, size_k, (hipStream_t)stream);
+    return report(e, "fastllm_int4_gemm_swiglu") ? 0 : 2;
 }
 
 }  // extern "C"

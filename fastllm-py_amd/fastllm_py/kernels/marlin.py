@@ -169,6 +169,29 @@ def gemm_fast(a_fp16, qweight, scales, zeros, size_n, size_k, stream=None, works
     return c
 
 
+def gemm_swiglu(a_fp16, qweight, scales, zeros, size_n, size_k, out=None, stream=None):
+    """Gate/up GEMV fused with SwiGLU for decode (M <= 16): the Marlin-format
+    weight stacks gate rows [0, I) and up rows [I, 2I) (size_n = 2I); returns
+    h (M, I) fp16 = swiglu(g, u) of the fp16 g, u that gemm_fast would
+    return, in one launch (the reference runs gemm_fast then ops.swiglu,
+    fastllm_py/kernels/ops.py:157-163)."""
+    t = nat.torch()
+    a = nat.to_device(a_fp16, t.float16)
+    a = a.reshape(-1, size_k).contiguous()
+    size_m = a.shape[0]
+    group_size = size_k // scales.shape[0]
+    h = out if out is not None else t.empty((size_m, size_n // 2), dtype=t.float16, device=a.device)
+    hs = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
+    rc = nat.lib().fastllm_int4_gemm_swiglu(nat.ptr(a), nat.ptr(qweight), nat.ptr(scales),
+                                            nat.ptr(zeros), nat.ptr(h), size_m, size_n, size_k,
+                                            group_size, hs)
+    if rc == 1:
+        raise ValueError(f"gemm_swiglu: unsupported shape M={size_m} N={size_n} K={size_k} "
+                         f"group={group_size}")
+    nat.check_rc(rc, "fastllm_int4_gemm_swiglu")
+    return h
+
+
 def marlin_gemm_int4(a_fp16, packed_weights, scales, zeros, workspace=None, size_n=None,
                      sync=True):
     """INT4 GEMM with validation (marlin.py:250-299).

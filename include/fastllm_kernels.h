@@ -70,7 +70,8 @@ bool FastllmCudaMarlinHalfInt4GemmStream(const void *a,
                                          void *stream);
 
 /* FastllmCudaMarlinHalfInt4GemmStream with an explicit launch configuration
- * for size_m <= 16: `tiles` 16-column n-tiles per workgroup (1 or 2), `waves`
+ * for size_m <= 16: `tiles` 16-column n-tiles per workgroup (1, 2 or 4;
+ * 4 only with nb <= 4), `waves`
  * waves per workgroup (1..16), `nb` the register budget in 128-k blocks per
  * wave (1, 2, 4, 6 or 8; at least ceil((size_k/128)/waves); 4 at most for
  * group 32).
@@ -82,6 +83,21 @@ bool fastllm_int4_gemm_config(const void *a, const uint32_t *b_q_weight,
                               void *c, int size_m, int size_n, int size_k,
                               int group_size, int tiles, int waves, int nb,
                               void *stream);
+
+/* Gate/up projection with the SwiGLU epilogue, decode-shaped (size_m <= 16):
+ * the Marlin-format weight holds size_n = 2 I output columns, gate rows
+ * [0, I) then up rows [I, 2 I) (I % 64 == 0, size_k % 128 == 0); writes
+ * h[size_m, I] (fp16) = silu(g) * u from the fp16 g, u the plain GEMV would
+ * store -- one launch instead of the GEMV and the swiglu kernel.
+ * Returns 0, 1 for arguments the kernel cannot take, 2 for a device or
+ * launch error.
+ * Replaces: the gate_up GEMV + swiglu pair of the reference's decode MLP
+ * (fastllm_py/kernels/ops.py:144-163, fastllm_py/graph_decode.py's dense
+ * FFN); no single reference entry. */
+int fastllm_int4_gemm_swiglu(const void *a, const uint32_t *b_q_weight,
+                             const void *b_scales, const uint32_t *b_zeros,
+                             void *h, int size_m, int size_n, int size_k,
+                             int group_size, void *stream);
 
 /* Inverse of the repack: tile layout -> GPTQ u32 [size_k/8, size_n].
  * No counterpart in the reference (its repacked layout is opaque); used to

@@ -191,3 +191,40 @@ def test_gemv_four_tiles(torch_gpu, M, gs):
                                             y.data_ptr(), M, N, K, gs, tiles, waves, nb, None)
         torch.cuda.synchronize()
         assert Q.max_abs_rel(y.float().cpu().numpy(), ref) < TOL, (tiles, waves, nb)
+
+
+@pytest.mark.parametrize("M,I,K,gs", [(1, 12288, 4096, 128), (4, 1408, 2048, 128), (8, 3072, 1024, 32),
+                                      (16, 512, 4096, 128), (3, 64, 256, 128)])
+def test_gemm_swiglu(torch_gpu, M, I, K, gs):
+    """Gate/up GEMV with the SwiGLU epilogue equals the plain GEMV followed by
+    swiglu of its fp16 outputs (up to the device exp), and the fp32 oracle."""
+    from fastllm_py.kernels import marlin
+
+    torch = torch_gpu
+    rng = np.random.default_rng(400 + M + I + K + gs)
+    W = (rng.standard_normal((2 * I, K)) * 0.02).astype(np.float32)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    pay, w_hat, _ = _prep(torch, W, gs)
+    ad = torch.from_numpy(a).cuda()
+    h = marlin.gemm_swiglu(ad, pay["qweight"], pay["scales"], pay["zeros"], 2 * I, K)
+    assert h.shape == (M, I) and h.dtype == torch.float16
+    gu = marlin.marlin_gemm_int4(ad, pay["qweight"], pay["scales"], pay["zeros"]).float().cpu().numpy()
+    g, u = gu[:, :I], gu[:, I:]
+    want = (g / (1.0 + np.exp(-g)) * u).astype(np.float16).astype(np.float32)
+    got = h.float().cpu().numpy()
+    np.testing.assert_allclose(got, want, rtol=2e-3, atol=1e-6)
+    ref = Q.matmul_ref(a.astype(np.float32), w_hat)
+    rg, ru = ref[:, :I], ref[:, I:]
+    assert Q.max_abs_rel(got, rg / (1.0 + np.exp(-rg)) * ru) < TOL
+
+
+def test_gemm_swiglu_rejects(torch_gpu):
+    from fastllm_py import _native
+
+    torch = torch_gpu
+    lib = _native.lib()
+    p = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda").data_ptr()
+    assert lib.fastllm_int4_gemm_swiglu(p, p, p, p, p, 17, 256, 256, 128, None) == 1  # M > 16
+    assert lib.fastllm_int4_gemm_swiglu(p, p, p, p, p, 1, 192, 256, 128, None) == 1   # I % 64
+    assert lib.fastllm_int4_gemm_swiglu(p, p, p, p, p, 1, 256, 192, 128, None) == 1   # K % 128
+    assert lib.fastllm_int4_gemm_swiglu(p, p, p, p, p, 1, 256, 256, 64, None) == 1    # group
