@@ -79,3 +79,11 @@ FL_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
 static inline hipError_t fl_last_error() { return hipGetLastError(); }
 
 static inline int fl_ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Workgroup index regrouped by XCD: the hardware deals workgroup b to XCD
+// b % 8, so with the grid a multiple of 8 XCD x takes the contiguous range
+// [x G/8, (x+1) G/8) and neighbouring tiles share that XCD's L2.
+FL_DEV int xcd_block() {
+    return (gridDim.x & 7) ? (int)blockIdx.x
+                           : (int)(blockIdx.x & 7) * (int)(gridDim.x >> 3) + (int)(blockIdx.x >> 3);
+}

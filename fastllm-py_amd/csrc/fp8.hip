@@ -78,7 +78,7 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
     const int nwaves = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int strip = blockIdx.x;
+    const int strip = xcd_block();  // XCD-grouped: neighbours share scale rows in L2
     const int nfull = K >> 7;
     const int col = lane & 15;
     const int kq = lane >> 4;
@@ -269,7 +269,7 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q4(
     const int nwaves = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int row0 = blockIdx.x * 4;
+    const int row0 = xcd_block() * 4;
     const int nfull = K >> 7;
     const int QB = (nfull + 3) >> 2;
     const int col = lane & 15, kq = lane >> 4;
@@ -405,7 +405,7 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
     const int nwaves = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int row0 = blockIdx.x * 8;
+    const int row0 = xcd_block() * 8;
     const int nfull = K >> 7;
     const int HB = (nfull + 1) >> 1;
     const int col = lane & 15, kq = lane >> 4;

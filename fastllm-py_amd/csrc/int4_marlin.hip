@@ -268,7 +268,10 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
     const int nwaves = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int strip = blockIdx.x;
+    // XCD-grouped strips: workgroup b runs on XCD b % 8, so each XCD takes a
+    // contiguous range of strips and neighbours share its L2 (scale / zero
+    // lines cover 64 columns, the activations every strip)
+    const int strip = xcd_block();
     const int nfull = K >> 7;
     const int col = lane & 15;
     const int kq = lane >> 4;
