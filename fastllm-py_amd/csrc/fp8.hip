@@ -13,10 +13,15 @@
 // Kernel: same decomposition as the INT4 GEMV (strip of T 16-row weight
 // tiles per workgroup, waves splitting the 128-k blocks, every load of a wave
 // issued up front, activations staged in LDS, fixed-order LDS reduction).  A
-// lane of the v_mfma_f32_16x16x32_{f16,bf16} B operand owns weight row
-// 16t + lane%16 and reads bytes [16q, 16q+16) and [64+16q, 64+16q+16) of each
-// 128-byte block (q = lane/16); its A fragments are taken at the same k
-// offsets, so the MFMA k order is a permutation applied to both operands.
+// lane (q = lane/16, c = lane%16) of the v_mfma_f32_16x16x32_{f16,bf16} B
+// operand owns column c (a weight row) and ends up with bytes [32q, 32q+32)
+// of each 128-byte block; its A fragments are taken at the same k offsets.
+// Weights are loaded whole-line: each load instruction reads eight complete
+// 128-byte block rows (the 16 B pieces 2q and 2q+1 of columns c and c^8 come
+// in through lanes c and c^8, one of the two in the other's place), and one
+// DPP row rotation by 8 trades the misplaced pieces (trade_pieces).  Reading
+// only half of each line per instruction -- the 64 B a column's four lanes
+// own -- costs a quarter of the bandwidth on row-major weights.
 // e4m3 codes become fp16/bf16 exactly through v_cvt_scalef32_pk_*_fp8
 // (scale 1.0); the block scale multiplies the fp32 partial.
 #include "common.cuh"
@@ -38,6 +43,23 @@ FL_DEV u32x4 fp8x8_to_16(uint32_t w0, uint32_t w1) {
                      bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true)),
                      bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false)),
                      bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true))};
+    }
+}
+
+// Whole-line weight loads.  Columns c < 8 and c >= 8 of a 16-lane row form
+// pairs (c, c^8).  Load i0 of lane (q, c) holds piece 2q + (c >= 8) of the
+// lower block of the pair, load i1 piece 2q + 1 - (c >= 8) of the upper one,
+// so each load reads the full 128 B of eight blocks.  Afterwards lane (q, c)
+// keeps its own piece 2q (own) and receives piece 2q + 1 of its own block
+// from lane c^8 (mate); "lower" and "upper" are whatever column groups the
+// kernel pairs.
+FL_DEV void trade_pieces(const u32x4& i0, const u32x4& i1, bool up, u32x4& own, u32x4& mate) {
+    const u32x4 send = up ? i0 : i1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        own[e] = up ? i1[e] : i0[e];
+        mate[e] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)send[e], 0x128 /* row_ror:8 */, 0xF,
+                                                        0xF, false);
     }
 }
 
@@ -112,28 +134,30 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
     }
     u32x4 ar[NB][4];
     if (AM == 3) {
-        const uint16_t* ap = A + (size_t)arow_m * K + 16 * kq;
+        const uint16_t* ap = A + (size_t)arow_m * K + 32 * kq;
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
             kb = kb < nfull ? kb : nfull - 1;
-            ar[i][0] = *reinterpret_cast<const u32x4*>(ap + kb * 128);
-            ar[i][1] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 8);
-            ar[i][2] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 64);
-            ar[i][3] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 72);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) ar[i][j] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 8 * j);
         }
     }
 
-    const uint8_t* rbase[T];
-    int nrow[T];
+    // tile rows paired (c, c + 8): load 0 reads rows 0..7 of the tile, load 1
+    // rows 8..15, each all 128 B of its block
+    const bool up = col >= 8;
+    const int p0 = 16 * (2 * kq + (up ? 1 : 0)), p1 = 16 * (2 * kq + (up ? 0 : 1));
+    const uint8_t* rb0[T];
+    const uint8_t* rb1[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-        const int n = (strip * T + t) * 16 + col;
-        nrow[t] = n;
-        rbase[t] = W + (size_t)(n < N ? n : N - 1) * rs;
+        const int n0 = (strip * T + t) * 16 + (col & 7), n1 = n0 + 8;
+        rb0[t] = W + (size_t)(n0 < N ? n0 : N - 1) * rs;
+        rb1[t] = W + (size_t)(n1 < N ? n1 : N - 1) * rs;
     }
 
-    u32x4 lo[NB][T], hi[NB][T];
+    u32x4 ld0[NB][T], ld1[NB][T];
     float sv[NB][T];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
@@ -141,11 +165,13 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
         kb = kb < nfull ? kb : nfull - 1;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const uint8_t* bp = rbase[t] + (size_t)kb * BSTRIDE;
-            lo[i][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(bp + 16 * kq));
-            hi[i][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(bp + 64 + 16 * kq));
+            const size_t bo = (size_t)kb * BSTRIDE;
+            ld0[i][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(rb0[t] + bo + p0));
+            ld1[i][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(rb1[t] + bo + p1));
+            // inline: the scale of the lane's own row (rb0 for c < 8, rb1 for
+            // c >= 8); 128 x 128: the tile's 16 rows share one scale band
             if (INLINE)
-                sv[i][t] = *reinterpret_cast<const float*>(bp + 128);
+                sv[i][t] = *reinterpret_cast<const float*>((up ? rb1[t] : rb0[t]) + bo + 128);
             else
                 sv[i][t] = Sc[(size_t)(((strip * T + t) * 16) >> 7) * nks + kb];
         }
@@ -166,7 +192,7 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
         lds_barrier();  // the weight loads stay in flight
     }
 
-    const uint16_t* arow = ALDS ? As + (size_t)arow_m * lda + 16 * kq : A + (size_t)arow_m * K + 16 * kq;
+    const uint16_t* arow = ALDS ? As + (size_t)arow_m * lda : A + (size_t)arow_m * K;
     f32x4 acc[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -176,32 +202,29 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
         const bool live = i < nb;
         int kb = wave + (live ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
         kb = kb < nfull ? kb : nfull - 1;
-        u32x4 a0, a1, a2, a3;
+        // k offsets 32 kq + 8 j of the block (bytes [32 kq, 32 kq + 32))
+        u32x4 a[4];
         if (AM == 0) {
-            const unsigned char* ak = aslot + (size_t)i * 1024 + arow_m * 256 + 32 * kq;
-            a0 = *reinterpret_cast<const u32x4*>(ak);
-            a1 = *reinterpret_cast<const u32x4*>(ak + 16);
-            a2 = *reinterpret_cast<const u32x4*>(ak + 128);
-            a3 = *reinterpret_cast<const u32x4*>(ak + 144);
+            const unsigned char* ak = aslot + (size_t)i * 1024 + arow_m * 256 + 64 * kq;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const u32x4*>(ak + 16 * j);
         } else if (AM == 3) {
-            a0 = ar[i][0];
-            a1 = ar[i][1];
-            a2 = ar[i][2];
-            a3 = ar[i][3];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a[j] = ar[i][j];
         } else {
-            const uint16_t* ak = arow + kb * 128;
-            a0 = *reinterpret_cast<const u32x4*>(ak);
-            a1 = *reinterpret_cast<const u32x4*>(ak + 8);
-            a2 = *reinterpret_cast<const u32x4*>(ak + 64);
-            a3 = *reinterpret_cast<const u32x4*>(ak + 72);
+            const uint16_t* ak = arow + kb * 128 + 32 * kq;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const u32x4*>(ak + 8 * j);
         }
 #pragma unroll
         for (int t = 0; t < T; ++t) {
+            u32x4 lo, hi;
+            trade_pieces(ld0[i][t], ld1[i][t], up, lo, hi);
             f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
-            part = mfma16<BF16>(a0, fp8x8_to_16<BF16>(lo[i][t][0], lo[i][t][1]), part);
-            part = mfma16<BF16>(a1, fp8x8_to_16<BF16>(lo[i][t][2], lo[i][t][3]), part);
-            part = mfma16<BF16>(a2, fp8x8_to_16<BF16>(hi[i][t][0], hi[i][t][1]), part);
-            part = mfma16<BF16>(a3, fp8x8_to_16<BF16>(hi[i][t][2], hi[i][t][3]), part);
+            part = mfma16<BF16>(a[0], fp8x8_to_16<BF16>(lo[0], lo[1]), part);
+            part = mfma16<BF16>(a[1], fp8x8_to_16<BF16>(lo[2], lo[3]), part);
+            part = mfma16<BF16>(a[2], fp8x8_to_16<BF16>(hi[0], hi[1]), part);
+            part = mfma16<BF16>(a[3], fp8x8_to_16<BF16>(hi[2], hi[3]), part);
             const float s = live ? sv[i][t] : 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[t][e] = __builtin_fmaf(s, part[e], acc[t][e]);
@@ -210,13 +233,15 @@ __global__ __launch_bounds__(1024) void fp8_gemv_nb(
     }
 
     if (!INLINE && (K & 127) && wave == 0) {
-        // trailing 64-wide block: bytes [16q, 16q+16) only
-        const uint16_t* ak = (AM == 0 || AM == 3 ? A + (size_t)arow_m * K + 16 * kq : arow) + nfull * 128;
+        // trailing 64-wide block: bytes [16q, 16q+16) only (four lanes read
+        // a row's 64 B)
+        const uint16_t* ak = (AM == 0 || AM == 3 ? A + (size_t)arow_m * K : arow) + nfull * 128 + 16 * kq;
         const u32x4 a0 = *reinterpret_cast<const u32x4*>(ak);
         const u32x4 a1 = *reinterpret_cast<const u32x4*>(ak + 8);
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const uint8_t* bp = rbase[t] + (size_t)nfull * BSTRIDE;
+            const int n = (strip * T + t) * 16 + col;
+            const uint8_t* bp = W + (size_t)(n < N ? n : N - 1) * rs + (size_t)nfull * BSTRIDE;
             const u32x4 w = *reinterpret_cast<const u32x4_a4*>(bp + 16 * kq);
             f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
             part = mfma16<BF16>(a0, fp8x8_to_16<BF16>(w[0], w[1]), part);
@@ -301,17 +326,23 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q4(
 
     const int wrow = row0 + r < N ? row0 + r : N - 1;
     const uint8_t* rbase = W + (size_t)wrow * rs;
-    u32x4 lo[NB], hi[NB];
+    // whole-line loads: columns (r, h) and (r, h + 2) are paired; load 0
+    // reads quarters 0 and 1, load 1 quarters 2 and 3
+    const bool up = h >= 2;
+    const int p0 = 16 * (2 * kq + (up ? 1 : 0)), p1 = 16 * (2 * kq + (up ? 0 : 1));
+    u32x4 ld0[NB], ld1[NB];
     float sv[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         const int b = slot_b(i);
-        const int kbr = h * QB + b;
+        const int k0 = (h & 1) * QB + b, k1 = (2 + (h & 1)) * QB + b;
+        ld0[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(
+            rbase + (size_t)(k0 < nfull ? k0 : nfull - 1) * BSTRIDE + p0));
+        ld1[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(
+            rbase + (size_t)(k1 < nfull ? k1 : nfull - 1) * BSTRIDE + p1));
+        const int kbr = h * QB + b;  // the lane's own block
         const int kb = kbr < nfull ? kbr : nfull - 1;
-        const uint8_t* bp = rbase + (size_t)kb * BSTRIDE;
-        lo[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(bp + 16 * kq));
-        hi[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(bp + 64 + 16 * kq));
-        float sc = INLINE ? *reinterpret_cast<const float*>(bp + 128)
+        float sc = INLINE ? *reinterpret_cast<const float*>(rbase + (size_t)kb * BSTRIDE + 128)
                           : Sc[(size_t)(wrow >> 7) * nks + kb];
         sv[i] = (i < nb && kbr < nfull) ? sc : 0.0f;
     }
@@ -327,16 +358,14 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q4(
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-        const unsigned char* ab = aslot + (i * 4 + arow) * 1024 + ah * 256 + 32 * kq;
-        const u32x4 a0 = *reinterpret_cast<const u32x4*>(ab);
-        const u32x4 a1 = *reinterpret_cast<const u32x4*>(ab + 16);
-        const u32x4 a2 = *reinterpret_cast<const u32x4*>(ab + 128);
-        const u32x4 a3 = *reinterpret_cast<const u32x4*>(ab + 144);
+        const unsigned char* ab = aslot + (i * 4 + arow) * 1024 + ah * 256 + 64 * kq;
+        u32x4 lo, hi;
+        trade_pieces(ld0[i], ld1[i], up, lo, hi);
         f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
-        part = mfma16<BF16>(a0, fp8x8_to_16<BF16>(lo[i][0], lo[i][1]), part);
-        part = mfma16<BF16>(a1, fp8x8_to_16<BF16>(lo[i][2], lo[i][3]), part);
-        part = mfma16<BF16>(a2, fp8x8_to_16<BF16>(hi[i][0], hi[i][1]), part);
-        part = mfma16<BF16>(a3, fp8x8_to_16<BF16>(hi[i][2], hi[i][3]), part);
+        part = mfma16<BF16>(*reinterpret_cast<const u32x4*>(ab), fp8x8_to_16<BF16>(lo[0], lo[1]), part);
+        part = mfma16<BF16>(*reinterpret_cast<const u32x4*>(ab + 16), fp8x8_to_16<BF16>(lo[2], lo[3]), part);
+        part = mfma16<BF16>(*reinterpret_cast<const u32x4*>(ab + 32), fp8x8_to_16<BF16>(hi[0], hi[1]), part);
+        part = mfma16<BF16>(*reinterpret_cast<const u32x4*>(ab + 48), fp8x8_to_16<BF16>(hi[2], hi[3]), part);
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(sv[i], part[e], acc[e]);
         __builtin_amdgcn_sched_barrier(0);
@@ -414,31 +443,37 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
     auto slot_b = [&](int i) { return wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves; };
 
     // A fragments first: lane (col, kq) = activation row col % 8 (clamped),
-    // half col / 8, k 16 kq + {0, 8, 64, 72} of the slot's block
+    // half col / 8, k 32 kq + {0, 8, 16, 24} of the slot's block
     const int arow = (col & 7) < M ? (col & 7) : M - 1;
-    const uint16_t* ap = A + (size_t)arow * K + 16 * kq;
+    const uint16_t* ap = A + (size_t)arow * K + 32 * kq;
     u32x4 ar[NB][4];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         int kb = h * HB + slot_b(i);
         kb = kb < nfull ? kb : nfull - 1;
-        ar[i][0] = *reinterpret_cast<const u32x4*>(ap + kb * 128);
-        ar[i][1] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 8);
-        ar[i][2] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 64);
-        ar[i][3] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 72);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ar[i][j] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 8 * j);
     }
     const int wrow = row0 + r < N ? row0 + r : N - 1;
     const uint8_t* rbase = W + (size_t)wrow * rs;
-    u32x4 lo[NB], hi[NB];
+    // whole-line loads: columns (r, 0) and (r, 1) are paired; load 0 reads
+    // half 0, load 1 half 1
+    const bool up = h == 1;
+    const int p0 = 16 * (2 * kq + h), p1 = 16 * (2 * kq + 1 - h);
+    u32x4 ld0[NB], ld1[NB];
     float sv[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-        const int kbr = h * HB + slot_b(i);
+        const int b = slot_b(i);
+        const int k0 = b, k1 = HB + b;
+        ld0[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(
+            rbase + (size_t)(k0 < nfull ? k0 : nfull - 1) * BSTRIDE + p0));
+        ld1[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(
+            rbase + (size_t)(k1 < nfull ? k1 : nfull - 1) * BSTRIDE + p1));
+        const int kbr = h * HB + b;  // the lane's own block
         const int kb = kbr < nfull ? kbr : nfull - 1;
-        const uint8_t* bp = rbase + (size_t)kb * BSTRIDE;
-        lo[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(bp + 16 * kq));
-        hi[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(bp + 64 + 16 * kq));
-        const float sc = INLINE ? *reinterpret_cast<const float*>(bp + 128) : Sc[(size_t)(wrow >> 7) * nks + kb];
+        const float sc = INLINE ? *reinterpret_cast<const float*>(rbase + (size_t)kb * BSTRIDE + 128)
+                                : Sc[(size_t)(wrow >> 7) * nks + kb];
         sv[i] = (i < nb && kbr < nfull) ? sc : 0.0f;
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -446,11 +481,13 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
+        u32x4 lo, hi;
+        trade_pieces(ld0[i], ld1[i], up, lo, hi);
         f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
-        part = mfma16<BF16>(ar[i][0], fp8x8_to_16<BF16>(lo[i][0], lo[i][1]), part);
-        part = mfma16<BF16>(ar[i][1], fp8x8_to_16<BF16>(lo[i][2], lo[i][3]), part);
-        part = mfma16<BF16>(ar[i][2], fp8x8_to_16<BF16>(hi[i][0], hi[i][1]), part);
-        part = mfma16<BF16>(ar[i][3], fp8x8_to_16<BF16>(hi[i][2], hi[i][3]), part);
+        part = mfma16<BF16>(ar[i][0], fp8x8_to_16<BF16>(lo[0], lo[1]), part);
+        part = mfma16<BF16>(ar[i][1], fp8x8_to_16<BF16>(lo[2], lo[3]), part);
+        part = mfma16<BF16>(ar[i][2], fp8x8_to_16<BF16>(hi[0], hi[1]), part);
+        part = mfma16<BF16>(ar[i][3], fp8x8_to_16<BF16>(hi[2], hi[3]), part);
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(sv[i], part[e], acc[e]);
         __builtin_amdgcn_sched_barrier(0);
@@ -557,9 +594,10 @@ Fp8Cfg fp8_cfg(int M, int N, int K) {
     Fp8Cfg c;
     const int nfull = K / 128 > 0 ? K / 128 : 1;
     // one 16-row tile per workgroup (twice the workgroups of two: 10944 x 2048
-    // measured 7.4 us against 8.2 at M = 1); eight waves on wide N up to M = 4
+    // measured 7.4 us against 8.2 at M = 1); on wide N eight waves up to
+    // M = 4 and four above (10944 x 2048, M = 8: 8.8 us against 9.0 with 16)
     c.tiles = 1;
-    int waves = (N >= 8192 && M <= 4) ? 8 : 16;
+    int waves = N >= 8192 ? (M <= 4 ? 8 : 4) : 16;
     while (waves > 1 && nfull < waves) waves /= 2;
     while ((nfull + waves - 1) / waves > 6 && waves < 16) waves *= 2;
     c.waves = waves;
@@ -611,10 +649,13 @@ hipError_t fp8_dispatch_nb(int nb, const uint16_t* A, const uint8_t* W, const fl
 template <bool INLINE, bool BF16>
 hipError_t fp8_gemm(const uint16_t* A, const uint8_t* W, const float* Sc, const uint16_t* bias,
                     uint16_t* C, int M, int N, int K, int rs, int nks, hipStream_t st) {
-    // few 16-row strips and M <= 4: the quartered 4-row kernel
-    if (M <= 4 && K >= 512 && K <= 32768 && N < 8192 && N % 4 == 0)
+    // few 16-row strips and M <= 4: the quartered 4-row kernel up to
+    // K = 8192; beyond, the halved kernel's activation traffic (half of the
+    // quartered one's per weight byte) wins (2048 x 10944, M = 1: 8.4 us
+    // against 8.8)
+    if (M <= 4 && K >= 512 && K < 8192 && N < 8192 && N % 4 == 0)
         return fp8_q4<INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, st);
-    // 4 < M <= 8 there: the halved 8-row kernel (K <= 128 x 2 x 64)
+    // M <= 8 there: the halved 8-row kernel (K <= 128 x 2 x 64)
     if (M <= 8 && K >= 512 && K <= 16384 && N < 8192 && N % 8 == 0)
         return fp8_q2<INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, st);
     // decode-shaped kernel, 16 activation rows per launch

@@ -36,7 +36,7 @@ def test_inline_quantize_bit_exact(torch_gpu, is_bf16):
 
 
 @pytest.mark.parametrize("n", [1, 3, 8, 16, 20])
-@pytest.mark.parametrize("m,k", [(1024, 512), (2048, 1408), (1408, 2048), (2048, 136)])
+@pytest.mark.parametrize("m,k", [(1024, 512), (2048, 1408), (1408, 2048), (2048, 136), (512, 8192)])
 def test_fp8_gemv_inline(torch_gpu, n, m, k):
     from fastllm_py.kernels import fp8
 
@@ -139,9 +139,10 @@ def test_fp8_block_gemv_config3(torch_gpu, M, N, K):
     assert Q.max_abs_rel(out.float().cpu().numpy(), ref) < TOL
 
 
-# N not a multiple of 16, K ending in a 64-wide block; the last two take the
-# halved 8-row kernel (4 < M <= 8, K >= 512)
-@pytest.mark.parametrize("N,K,M", [(200, 320, 5), (200, 704, 6), (2000, 1088, 8)])
+# N not a multiple of 16, K ending in a 64-wide block; all but the first take
+# the halved 8-row kernel (M <= 8 and K >= 512; at M <= 4 only from K = 8192)
+@pytest.mark.parametrize("N,K,M", [(200, 320, 5), (200, 704, 6), (2000, 1088, 8), (200, 8256, 3),
+                                   (2000, 8192, 1)])
 def test_fp8_block_gemv_fp16_bias_ragged(torch_gpu, N, K, M):
     from fastllm_py import quantizer
     from fastllm_py.kernels import fp8
