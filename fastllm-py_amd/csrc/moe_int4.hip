@@ -421,12 +421,13 @@ FL_DEV float np_sum_wave128(const float* a, int n, int lane, float v0, float v1)
 
 // Route token t with one wave.  `exw` is the wave's 256-float LDS row.
 // Lane i < K ends with the i-th selection (expert `my_id`, final weight
-// `my_w`), which it also stores to topk_ids/topk_w and to sids/sws[tl*K + i].
+// `my_w`), which it also stores to sids/sws[tl*K + i] and, when `store`, to
+// topk_ids/topk_w (and scoef, rw).
 // Values sit one per lane in nc <= 4 slots (expert lane + 64 c); slots past
 // nc are skipped by uniform branches.  Everything stays in registers except
 // the exp row of the softmax sum.
 FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw, int* sids,
-                        float* sws, int& my_id, float& my_w) {
+                        float* sws, int& my_id, float& my_w, bool store = true) {
     const int E = a.E, K = a.K;
     const int nc = (E + 63) >> 6;
     float sel[4], p[4];
@@ -580,11 +581,14 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
     }
     my_w = my_w * a.scale;
     if (lane < K) {
-        a.topk_ids[(size_t)t * K + lane] = my_id;
-        a.topk_w[(size_t)t * K + lane] = my_w;
+        if (store) {
+            a.topk_ids[(size_t)t * K + lane] = my_id;
+            a.topk_w[(size_t)t * K + lane] = my_w;
+        }
         sids[tl * K + lane] = my_id;
         sws[tl * K + lane] = my_w;
     }
+    if (!store) return;
     if (lane == 0 && a.scoef && a.slogit) a.scoef[t] = 1.0f / (1.0f + expf(-slog));
     if (a.rw) {
         float w[4] = {0.f, 0.f, 0.f, 0.f};
@@ -599,6 +603,29 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
         for (int c = 0; c < 4; ++c) {
             const int e = lane + 64 * c;
             if (c < nc && e < E) a.rw[(size_t)t * E + e] = w[c];
+        }
+    }
+}
+
+// One token: its K picks are the K slots, ordered by expert id (the experts
+// are distinct, so the ranks are too).  Returns the lane's slot.
+FL_DEV int one_token_rank(int K, int my_id) {
+    int rank = 0;
+    for (int j = 0; j < K; ++j) rank += __builtin_amdgcn_readlane(my_id, j) < my_id ? 1 : 0;
+    return rank;
+}
+
+FL_DEV void one_token_lists(const RouteArgs& a, int lane, int my_id, float my_w) {
+    const int K = a.K;
+    const int rank = one_token_rank(K, my_id);
+    if (lane < K) {
+        a.lists.active[rank] = my_id;
+        a.lists.offsets[rank] = rank;
+        a.lists.tok[rank] = 0;
+        a.lists.tokw[rank] = my_w;
+        if (lane == 0) {
+            a.lists.offsets[K] = K;
+            *a.lists.n_active = K;
         }
     }
 }
@@ -624,21 +651,7 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
     }
     if (gridDim.x == 1 && a.lists.n_active) {
         if (a.T == 1) {
-            // one token: its K picks are the K slots, ordered by expert id
-            // (the experts are distinct, so the ranks are too)
-            const int K = a.K;
-            int rank = 0;
-            for (int j = 0; j < K; ++j) rank += __builtin_amdgcn_readlane(my_id, j) < my_id ? 1 : 0;
-            if (lane < K) {
-                a.lists.active[rank] = my_id;
-                a.lists.offsets[rank] = rank;
-                a.lists.tok[rank] = 0;
-                a.lists.tokw[rank] = my_w;
-                if (lane == 0) {
-                    a.lists.offsets[K] = K;
-                    *a.lists.n_active = K;
-                }
-            }
+            one_token_lists(a, lane, my_id, my_w);
             return;
         }
         __syncthreads();
@@ -894,7 +907,39 @@ struct MoeArgs {
     uint16_t* inter_buf;
     const uint16_t* xh;  // (T, hidden) fp16 copy of x (grouped kernels only)
     float* y;  // (T, hidden) fp32
+    // T == 1 with routing: every routed gate/up workgroup routes the token
+    // itself (no router launch before it); workgroup 0 stores the router
+    // outputs and the lists the down kernel reads
+    int fuse_route;
+    RouteArgs ra;
 };
+
+// Fused routing of the one token (T == 1) in a routed gate/up workgroup:
+// wave 0 routes it, workgroup 0 also stores the router outputs and lists;
+// returns the expert of slot `slot` (the slot-th smallest of the K picks) and
+// its combine weight to every thread.
+FL_DEV void fused_route_slot(const RouteArgs& r, int slot, bool store, int& e, float& w) {
+    __shared__ float exw[256];
+    __shared__ int sids[kMaxTopK];
+    __shared__ float sws[kMaxTopK];
+    __shared__ int s_e;
+    __shared__ float s_w;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        int my_id = 0;
+        float my_w = 0.f;
+        route_token(r, 0, 0, lane, exw, sids, sws, my_id, my_w, store);
+        const int rank = one_token_rank(r.K, my_id);
+        if (lane < r.K && rank == slot) {
+            s_e = my_id;
+            s_w = my_w;
+        }
+        if (store) one_token_lists(r, lane, my_id, my_w);
+    }
+    __syncthreads();
+    e = s_e;
+    w = s_w;
+}
 
 // 16-row tiles of gate and of up per gate/up workgroup: one for up to
 // kGuOwnT tokens (more, smaller workgroups: one generation of them covers
@@ -969,12 +1014,20 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
 
     const int groups_r = a.routed.inter / (16 * TR);
     int slot, grp, e = 0, M = 0, row0 = 0;
+    float fw = 0.f;  // fused routing: the slot's combine weight
     const MoeExperts* ex;
     const int b = blockIdx.x;
     if (b < a.max_slots * groups_r) {
         slot = b / groups_r;
         grp = b - slot * groups_r;
-        if (!moe_slot(a, slot, e, row0, M)) return;
+        if (a.fuse_route) {
+            fused_route_slot(a.ra, slot, b == 0, e, fw);
+            e = clampi(e, 0, a.E - 1);
+            row0 = slot;
+            M = 1;
+        } else if (!moe_slot(a, slot, e, row0, M)) {
+            return;
+        }
         ex = &a.routed;
     } else {
         if (!a.has_shared) return;
@@ -990,9 +1043,15 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
     // the token of this lane's MFMA row and the entry weights, loaded now so
     // neither waits at the end
     const int jr = col < M ? col : M - 1;
-    const int tok_r = slot >= 0 ? clampi(a.tok[row0 + jr], 0, a.T - 1) : jr;
+    const int tok_r = (slot >= 0 && !a.fuse_route) ? clampi(a.tok[row0 + jr], 0, a.T - 1) : jr;
     const int jw = (int)threadIdx.x < M ? (int)threadIdx.x : 0;
-    const float wpre = slot >= 0 ? a.tokw[row0 + jw] : (a.scoef ? a.scoef[jw] : 1.0f);
+    float wpre;
+    if (slot >= 0)
+        wpre = a.fuse_route ? fw : a.tokw[row0 + jw];
+    else if (a.fuse_route)  // the router has not stored scoef yet: sigmoid of the shared logit here
+        wpre = (a.scoef && a.ra.slogit) ? 1.0f / (1.0f + expf(-a.ra.slogit[jw])) : 1.0f;
+    else
+        wpre = a.scoef ? a.scoef[jw] : 1.0f;
 
     u32x4 wg[NB][TR], wu[NB][TR];
     uint32_t szg[NB][TR], szu[NB][TR];
@@ -1703,7 +1762,8 @@ static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int
                           const uint32_t* sdsz, const float* shared_coef, const int* n_active,
                           const int* active, const int* offsets, const int* tok,
                           const float* tokw, int max_slots, int max_entries, void* workspace,
-                          size_t workspace_bytes, float* y, void* stream, bool launch) {
+                          size_t workspace_bytes, float* y, void* stream, bool launch,
+                          const RouteArgs* fuse = nullptr) {
     if (!x || !y || E <= 0 || !gq || !gsz || !uq || !usz || !dq || !dsz) return 1;
     if (group_size != 32 && group_size != 64 && group_size != 128) return 1;
     if (!n_active || !active || !offsets || !tok || !tokw) return 1;
@@ -1742,6 +1802,8 @@ static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int
     a.xh = p.grouped ? reinterpret_cast<const uint16_t*>(static_cast<char*>(workspace) + p.xh_off)
                      : nullptr;
     a.y = y;
+    a.fuse_route = (fuse && T == 1 && !p.grouped) ? 1 : 0;
+    if (a.fuse_route) a.ra = *fuse;
     hipStream_t st = (hipStream_t)stream;
     if (p.grouped)
         moe_launch_grouped(a, st);
@@ -1795,6 +1857,12 @@ int fastllm_moe_int4_routed(const float* logits, int top_k, int scoring, int nor
     const MoeLists lists{n_active, active, offsets, tok, tokw};
     const RouteArgs r{logits, e_score_bias, shared_logit, T, E, top_k, scoring, norm, n_group,
                       topk_group, routed_scaling, topk_ids, topk_w, rw, shared_coef, lists};
+    if (T == 1)  // routed inside the gate/up launch
+        return moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz,
+                              shared_inter, sgq, sgsz, suq, susz, sdq, sdsz,
+                              shared_logit ? shared_coef : nullptr, n_active, active, offsets, tok,
+                              tokw, max_slots, max_entries, workspace, workspace_bytes, y, stream,
+                              true, &r);
     hipStream_t st = (hipStream_t)stream;
     hipLaunchKernelGGL(route_k, dim3(1), dim3(64 * T), 0, st, r);
     const int rr = finish("fastllm_moe_int4_routed");

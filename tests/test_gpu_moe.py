@@ -441,6 +441,10 @@ def test_fused_moe_shapes(torch_gpu, T, E, K, hidden, inter, sinter, gs):
     (3, 16, 4, 512, 768, 1536, 128, True),
     (16, 128, 16, 256, 256, 0, 64, True),        # 256 entries, group 64
     (5, 6, 3, 384, 384, 3200, 32, False),         # group 32, shared in 9 pieces
+    # one token: routed inside the gate/up launch
+    (1, 16, 4, 512, 768, 1536, 128, True),
+    (1, 128, 16, 256, 256, 0, 64, True),
+    (1, 6, 3, 384, 384, 3200, 32, False),
 ])
 def test_moe_route_forward(torch_gpu, T, E, K, hidden, inter, sinter, gs, norm):
     """Router + fused MoE in one native call: routing outputs bit-exact vs the
@@ -488,6 +492,45 @@ def test_moe_route_forward(torch_gpu, T, E, K, hidden, inter, sinter, gs, norm):
         assert np.isfinite(yc).all(), call
         assert Q.max_abs_rel(yc, y2.cpu().numpy()) < 1e-5, call
         assert Q.max_abs_rel(yc, ref) < 5e-3, call
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_moe_route_forward_sigmoid_groups(torch_gpu, T):
+    """Sigmoid scoring with a score bias, group-limited selection and routed
+    scaling through the one-call path (T = 1 routes inside the gate/up
+    launch): routing bit-exact vs the router entry, y vs the two-call path."""
+    from fastllm_py.expert_router import route_topk_device
+    from fastllm_py.kernels import moe_int4
+
+    torch = torch_gpu
+    rng = np.random.default_rng(9100 + T)
+    E, K, hidden, inter, sinter, gs = 64, 6, 512, 256, 768, 128
+    kw = dict(norm_topk_prob=True, scoring="sigmoid", routed_scaling=2.5,
+              e_score_bias=torch.from_numpy((rng.standard_normal(E) * 0.1).astype(np.float32)).cuda(),
+              n_group=8, topk_group=3)
+    st = moe_int4.build_stacked_experts(_experts(rng, E, hidden, inter, 0.05), gs)
+    sh = moe_int4.build_stacked_experts(_experts(rng, 1, hidden, sinter, 0.05), gs)
+    x = torch.from_numpy((rng.standard_normal((T, hidden)) * 0.5).astype(np.float32)).cuda()
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).cuda()
+    sl = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).cuda()
+    ref_r = route_topk_device(logits, K, shared_logit=sl, **kw)
+    y2 = moe_int4.moe_forward(x, st, E, hidden, inter, ref_r, max_slots=min(E, T * K),
+                              max_entries=T * K, shared=sh, shared_inter=sinter,
+                              shared_coef=ref_r["shared_coef"])
+    for _ in range(2):
+        r = {}
+        y = moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, shared=sh,
+                                       shared_inter=sinter, shared_logit=sl, route=r, **kw)
+        torch.cuda.synchronize()
+        for k in ("topk_ids", "topk_w", "rw", "n_active", "shared_coef"):
+            np.testing.assert_array_equal(r[k].cpu().numpy().view(np.uint32),
+                                          ref_r[k].cpu().numpy().view(np.uint32), err_msg=k)
+        na = int(r["n_active"].item())
+        n_ent = int(ref_r["offsets"][na].item())
+        for k, n in (("active", na), ("offsets", na + 1), ("tok", n_ent), ("tokw", n_ent)):
+            np.testing.assert_array_equal(r[k][:n].cpu().numpy().view(np.uint32),
+                                          ref_r[k][:n].cpu().numpy().view(np.uint32), err_msg=k)
+        assert Q.max_abs_rel(y.cpu().numpy(), y2.cpu().numpy()) < 1e-5
 
 
 def test_fused_moe_edge_lists(torch_gpu):
