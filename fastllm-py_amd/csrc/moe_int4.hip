@@ -273,6 +273,10 @@ struct RouteArgs {
     float* rw;       // dense [T, E], optional
     float* scoef;    // sigmoid(slogit) [T], optional
     MoeLists lists;  // built by route_k itself when the batch is one workgroup
+    // optional: route_k also stores xh[t, :] = fp16(x[t, :]) (hidden <= 4096)
+    const float* x;
+    uint16_t* xh;
+    int hidden;
 };
 
 // Inclusive prefix sum over the wave: shifts by 1, 2, 4, 8 inside each
@@ -642,12 +646,44 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nw = blockDim.x >> 6;
+    // fp16 copy of the token rows (one wave per token: 64 x T threads): the
+    // row loads go out before the routing and are stored after it
+    constexpr int kXc = 8;  // 8-float chunks per lane (hidden <= 4096)
+    const int tx = blockIdx.x * 16 + wv;
+    const bool conv = a.xh && nw == a.T && tx < a.T;
+    const int n8 = a.hidden >> 3;
+    f32x4 xr[kXc][2];
+    if (conv) {
+        const float* src = a.x + (size_t)tx * a.hidden;
+#pragma unroll
+        for (int i = 0; i < kXc; ++i) {
+            const int c = lane + 64 * i;
+            const int cc = c < n8 ? c : n8 - 1;
+            xr[i][0] = *reinterpret_cast<const f32x4*>(src + 8 * cc);
+            xr[i][1] = *reinterpret_cast<const f32x4*>(src + 8 * cc + 4);
+        }
+    }
     int my_id = 0;
     float my_w = 0.f;
     for (int tl = wv; tl < 16; tl += nw) {
         const int t = blockIdx.x * 16 + tl;
         if (t >= a.T) break;
         route_token(a, t, tl, lane, ex[wv], sids, sws, my_id, my_w);
+    }
+    if (conv) {
+#pragma unroll
+        for (int i = 0; i < kXc; ++i) {
+            const int c = lane + 64 * i;
+            if (c < n8) {
+                f16x8 v;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    v[q] = (f16)xr[i][0][q];
+                    v[4 + q] = (f16)xr[i][1][q];
+                }
+                *reinterpret_cast<f16x8*>(a.xh + (size_t)tx * a.hidden + 8 * c) = v;
+            }
+        }
     }
     if (gridDim.x == 1 && a.lists.n_active) {
         if (a.T == 1) {
@@ -905,7 +941,8 @@ struct MoeArgs {
     const float* tokw;
     int max_slots, max_entries, inter_pad;
     uint16_t* inter_buf;
-    const uint16_t* xh;  // (T, hidden) fp16 copy of x (grouped kernels only)
+    const uint16_t* xh;  // (T, hidden) fp16 copy of x (grouped kernels; decode kernels for T > 4)
+    int xh_ready;        // xh already written (by the router) before the launch
     float* y;  // (T, hidden) fp32
     // T == 1 with routing: every routed gate/up workgroup routes the token
     // itself (no router launch before it); workgroup 0 stores the router
@@ -989,12 +1026,17 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
     const int col = lane & 15, kq = lane >> 4;
     const int K = a.hidden;
     const int nfull = K >> 7;
-    const int lda = K + 8;
-    // T <= 4: each wave converts every token's rows of its own blocks into
-    // its own LDS slot (NB blocks x T rows x 128 halves), loading them first
-    // of all -- they depend on nothing -- and reading them back without a
-    // workgroup barrier.  Larger T gathers the slot's rows per workgroup.
+    // Every wave stages all T token rows of its own blocks in its own LDS
+    // slot (NB blocks x Tp rows x 128 halves, Tp = T rounded up to 4) and
+    // reads them back without a workgroup barrier:
+    //   T <= 4: fp32 rows loaded first of all into registers (they depend on
+    //     nothing), converted and stored once the weight loads are out;
+    //   T > 4: copies global -> LDS (buffer_load ... lds) of the fp16 rows
+    //     of xh, issued right before the weight loads and waited for with a
+    //     vmcnt that leaves the weight loads in flight.
+    // Either way a block's MFMAs wait only for that block's weights.
     const bool own = a.T <= kGuOwnT;
+    const int Tp = (a.T + 3) & ~3;
     f32x4 xs[NB][2];
     if (own) {
         const int m = (lane >> 4) < a.T ? (lane >> 4) : a.T - 1;
@@ -1040,6 +1082,25 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
     if (M <= 0) return;
     const int G = K / a.gs;
     const size_t tb0 = (size_t)e * (ex->inter / 16) + (size_t)grp * TR;  // first row tile
+    unsigned char* oslot = smem + (size_t)wave * NB * Tp * 256;
+    if (!own) {
+        // lane l copies 16 B piece l % 16 of row m0 + l / 16 (rows past T
+        // repeat row T - 1 into the padding)
+        const __amdgpu_buffer_rsrc_t rX = buf_rsrc(a.xh, (uint32_t)a.T * K * 2);
+        const int rq = lane >> 4;
+        const uint32_t po = 16u * (lane & 15);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            int kb = moe_kb<NB>(wave, i, nwaves);
+            kb = kb < nfull ? kb : nfull - 1;
+            for (int m0 = 0; m0 < a.T; m0 += 4) {
+                const int m = m0 + rq < a.T ? m0 + rq : a.T - 1;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rX, (lptr_t)(oslot + ((size_t)i * Tp + m0) * 256), 16,
+                                                         2u * ((uint32_t)m * K + kb * 128) + po, 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the copies go out before the weight loads
+    }
     // the token of this lane's MFMA row and the entry weights, loaded now so
     // neither waits at the end
     const int jr = col < M ? col : M - 1;
@@ -1071,8 +1132,6 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    f16* As = reinterpret_cast<f16*>(smem);
-    unsigned char* oslot = smem + (size_t)wave * NB * a.T * 256;
     if (own) {
         if ((lane >> 4) < a.T) {
 #pragma unroll
@@ -1083,30 +1142,16 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
                     v[q] = (f16)xs[i][0][q];
                     v[4 + q] = (f16)xs[i][1][q];
                 }
-                *reinterpret_cast<f16x8*>(oslot + ((size_t)i * a.T + (lane >> 4)) * 256 + 16 * (lane & 15)) = v;
+                *reinterpret_cast<f16x8*>(oslot + ((size_t)i * Tp + (lane >> 4)) * 256 + 16 * (lane & 15)) = v;
             }
         }
     } else {
-        // gather this slot's token rows (fp32 -> fp16)
-        const int k8 = K >> 3;
-        for (int c = threadIdx.x; c < M * k8; c += blockDim.x) {
-            const int j = c / k8, c8 = c - j * k8;
-            const int tkn = slot >= 0 ? clampi(a.tok[row0 + j], 0, a.T - 1) : j;
-            const float* src = a.x + (size_t)tkn * K + c8 * 8;
-            const f32x4 lo = *reinterpret_cast<const f32x4*>(src);
-            const f32x4 hi = *reinterpret_cast<const f32x4*>(src + 4);
-            f16x8 v;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                v[q] = (f16)lo[q];
-                v[4 + q] = (f16)hi[q];
-            }
-            *reinterpret_cast<f16x8*>(As + (size_t)j * lda + c8 * 8) = v;
-        }
-        lds_barrier();  // the weight loads stay in flight
+        // the copies went out before this wave's weight loads (wg, wu: 2 per
+        // tile and block; the scale|zero words only make the wait stricter)
+        constexpr int WL = NB * TR * 2;
+        wait_vmcnt<(WL < 63 ? WL : 63)>();
     }
 
-    const f16* arow = As + (size_t)jr * lda + 32 * kq;
     f32x4 acc[2 * TR];
 #pragma unroll
     for (int r = 0; r < 2 * TR; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1118,9 +1163,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
         u32x4 av[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            av[j] = own ? *reinterpret_cast<const u32x4*>(oslot + ((size_t)i * a.T + tok_r) * 256 +
-                                                          2 * (32 * kq + 8 * j))
-                        : *reinterpret_cast<const u32x4*>(arow + kb * 128 + 8 * j);
+            av[j] = *reinterpret_cast<const u32x4*>(oslot + ((size_t)i * Tp + tok_r) * 256 + 2 * (32 * kq + 8 * j));
 #pragma unroll
         for (int r = 0; r < TR; ++r) {
             tile_block_mma<G128>(acc[2 * r], av, wg[i][r], sz_scale(szg[i][r]), sz_zero(szg[i][r]), live);
@@ -1133,7 +1176,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
     // reduce the 2*TR tiles over the waves, then h = silu(g) * u * w
     float* red = reinterpret_cast<float*>(smem);
     const size_t red_bytes = (size_t)nwaves * 2 * TR * 1024;
-    const size_t as_bytes = own ? (size_t)nwaves * NB * a.T * 256 : (((size_t)a.T * lda * 2 + 15) & ~(size_t)15);
+    const size_t as_bytes = (size_t)nwaves * NB * Tp * 256;
     float* gu = reinterpret_cast<float*>(smem + (red_bytes > as_bytes ? red_bytes : as_bytes));
     float* wsm = gu + 2 * TR * 256;
     if ((int)threadIdx.x < M) wsm[threadIdx.x] = wpre;
@@ -1514,7 +1557,7 @@ void rm_dispatch(int nb, const void* X, const uint8_t* W, const uint16_t* S, con
 // Launch plan of the fused MoE for one problem shape (host side).
 struct MoePlan {
     bool grouped;   // T > 16: the grouped-GEMM kernels
-    size_t xh_off;  // grouped: workspace offset of the fp16 copy of x
+    size_t xh_off;  // grouped, or T > 4: workspace offset of the fp16 copy of x (else 0)
     int nb_gu, waves_gu, tr_gu, nb_d, trd, waves_d, pieces, inter_pad;
     size_t lds_gu, lds_d, bytes;
 };
@@ -1527,6 +1570,7 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
     if (T <= 0 || hidden <= 0 || hidden % 128 || inter <= 0 || inter % 128) return false;
     if (shared_inter < 0 || shared_inter % 128 || max_entries <= 0) return false;
     p.grouped = T > 16;
+    p.xh_off = 0;
     p.inter_pad = inter > shared_inter ? inter : shared_inter;
     p.bytes = (size_t)(max_entries + T) * p.inter_pad * 2;
     if (p.grouped) {
@@ -1539,8 +1583,7 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
     p.nb_gu = (nfh + 7) / 8;
     if (p.nb_gu > 4) return false;  // hidden <= 4096
     p.waves_gu = (nfh + p.nb_gu - 1) / p.nb_gu;
-    const size_t as_bytes = T <= kGuOwnT ? (size_t)p.waves_gu * p.nb_gu * T * 256
-                                         : (((size_t)T * (hidden + 8) * 2) + 15) & ~(size_t)15;
+    const size_t as_bytes = (size_t)p.waves_gu * p.nb_gu * ((T + 3) & ~3) * 256;
     p.tr_gu = gu_tiles(T);
     const size_t red_bytes = (size_t)p.waves_gu * 2 * p.tr_gu * 1024;
     p.lds_gu = (as_bytes > red_bytes ? as_bytes : red_bytes) + (size_t)2 * p.tr_gu * 1024 + 16 * 4;
@@ -1557,6 +1600,10 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
     p.lds_d = (size_t)p.waves_d * p.trd * 1024;
     p.inter_pad = inter > shared_inter ? inter : shared_inter;
     p.bytes = (size_t)(max_entries + T) * p.inter_pad * 2;
+    if (T > kGuOwnT) {  // + the fp16 copy of x the gate/up kernel stages from
+        p.xh_off = (p.bytes + 255) & ~(size_t)255;
+        p.bytes = p.xh_off + (size_t)T * hidden * 2;
+    }
     return true;
 }
 
@@ -1596,6 +1643,11 @@ void moe_launch_grouped(const MoeArgs& a, hipStream_t st) {
 
 template <bool G128>
 void moe_launch(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
+    if (a.T > kGuOwnT && !a.xh_ready) {
+        const int n8 = a.T * a.hidden / 8;
+        hipLaunchKernelGGL(x_to_f16_k, dim3((n8 + 255) / 256), dim3(256), 0, st, a.x,
+                           const_cast<uint16_t*>(a.xh), n8);
+    }
     switch (p.nb_gu) {
         case 1: launch_gate_up<G128, 1>(a, p, st); break;
         case 2: launch_gate_up<G128, 2>(a, p, st); break;
@@ -1763,7 +1815,7 @@ static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int
                           const int* active, const int* offsets, const int* tok,
                           const float* tokw, int max_slots, int max_entries, void* workspace,
                           size_t workspace_bytes, float* y, void* stream, bool launch,
-                          const RouteArgs* fuse = nullptr) {
+                          const RouteArgs* fuse = nullptr, bool xh_ready = false) {
     if (!x || !y || E <= 0 || !gq || !gsz || !uq || !usz || !dq || !dsz) return 1;
     if (group_size != 32 && group_size != 64 && group_size != 128) return 1;
     if (!n_active || !active || !offsets || !tok || !tokw) return 1;
@@ -1799,8 +1851,9 @@ static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int
     a.max_entries = max_entries;
     a.inter_pad = p.inter_pad;
     a.inter_buf = static_cast<uint16_t*>(workspace);
-    a.xh = p.grouped ? reinterpret_cast<const uint16_t*>(static_cast<char*>(workspace) + p.xh_off)
-                     : nullptr;
+    a.xh = p.xh_off ? reinterpret_cast<const uint16_t*>(static_cast<char*>(workspace) + p.xh_off)
+                    : nullptr;
+    a.xh_ready = xh_ready ? 1 : 0;
     a.y = y;
     a.fuse_route = (fuse && T == 1 && !p.grouped) ? 1 : 0;
     if (a.fuse_route) a.ra = *fuse;
@@ -1863,14 +1916,25 @@ int fastllm_moe_int4_routed(const float* logits, int top_k, int scoring, int nor
                               shared_logit ? shared_coef : nullptr, n_active, active, offsets, tok,
                               tokw, max_slots, max_entries, workspace, workspace_bytes, y, stream,
                               true, &r);
+    // T > 4: the router also writes the fp16 token rows the gate/up kernel
+    // stages (the plan was validated above)
+    MoePlan p;
+    moe_plan(T, hidden, inter, shared_inter > 0 ? shared_inter : 0, max_entries, p);
+    RouteArgs rx = r;
+    if (p.xh_off) {
+        rx.x = x;
+        rx.xh = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + p.xh_off);
+        rx.hidden = hidden;
+    }
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(route_k, dim3(1), dim3(64 * T), 0, st, r);
+    hipLaunchKernelGGL(route_k, dim3(1), dim3(64 * T), 0, st, rx);
     const int rr = finish("fastllm_moe_int4_routed");
     if (rr) return rr;
     return moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz,
                           shared_inter, sgq, sgsz, suq, susz, sdq, sdsz,
                           shared_logit ? shared_coef : nullptr, n_active, active, offsets, tok, tokw,
-                          max_slots, max_entries, workspace, workspace_bytes, y, stream, true);
+                          max_slots, max_entries, workspace, workspace_bytes, y, stream, true,
+                          nullptr, p.xh_off != 0);
 }
 
 }  // extern "C"
