@@ -273,10 +273,11 @@ struct RouteArgs {
     float* rw;       // dense [T, E], optional
     float* scoef;    // sigmoid(slogit) [T], optional
     MoeLists lists;  // built by route_k itself when the batch is one workgroup
-    // optional: route_k also stores xh[t, :] = fp16(x[t, :]) (hidden <= 4096)
+    // optional: the last xh_blocks workgroups of route_k's grid store
+    // xh[t, :] = fp16(x[t, :]) while the others route
     const float* x;
     uint16_t* xh;
-    int hidden;
+    int hidden, xh_blocks;
 };
 
 // Inclusive prefix sum over the wave: shifts by 1, 2, 4, 8 inside each
@@ -646,22 +647,22 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nw = blockDim.x >> 6;
-    // fp16 copy of the token rows (one wave per token: 64 x T threads): the
-    // row loads go out before the routing and are stored after it
-    constexpr int kXc = 8;  // 8-float chunks per lane (hidden <= 4096)
-    const int tx = blockIdx.x * 16 + wv;
-    const bool conv = a.xh && nw == a.T && tx < a.T;
-    const int n8 = a.hidden >> 3;
-    f32x4 xr[kXc][2];
-    if (conv) {
-        const float* src = a.x + (size_t)tx * a.hidden;
+    const int rb = gridDim.x - a.xh_blocks;  // routing workgroups
+    if ((int)blockIdx.x >= rb) {
+        // fp16 copy of the token rows, beside the routing
+        const int n8 = a.T * a.hidden / 8;
+        for (int i = (blockIdx.x - rb) * blockDim.x + threadIdx.x; i < n8; i += a.xh_blocks * blockDim.x) {
+            const f32x4 lo = reinterpret_cast<const f32x4*>(a.x)[2 * i];
+            const f32x4 hi = reinterpret_cast<const f32x4*>(a.x)[2 * i + 1];
+            f16x8 v;
 #pragma unroll
-        for (int i = 0; i < kXc; ++i) {
-            const int c = lane + 64 * i;
-            const int cc = c < n8 ? c : n8 - 1;
-            xr[i][0] = *reinterpret_cast<const f32x4*>(src + 8 * cc);
-            xr[i][1] = *reinterpret_cast<const f32x4*>(src + 8 * cc + 4);
+            for (int q = 0; q < 4; ++q) {
+                v[q] = (f16)lo[q];
+                v[4 + q] = (f16)hi[q];
+            }
+            reinterpret_cast<f16x8*>(a.xh)[i] = v;
         }
+        return;
     }
     int my_id = 0;
     float my_w = 0.f;
@@ -670,22 +671,7 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
         if (t >= a.T) break;
         route_token(a, t, tl, lane, ex[wv], sids, sws, my_id, my_w);
     }
-    if (conv) {
-#pragma unroll
-        for (int i = 0; i < kXc; ++i) {
-            const int c = lane + 64 * i;
-            if (c < n8) {
-                f16x8 v;
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    v[q] = (f16)xr[i][0][q];
-                    v[4 + q] = (f16)xr[i][1][q];
-                }
-                *reinterpret_cast<f16x8*>(a.xh + (size_t)tx * a.hidden + 8 * c) = v;
-            }
-        }
-    }
-    if (gridDim.x == 1 && a.lists.n_active) {
+    if (rb == 1 && a.lists.n_active) {
         if (a.T == 1) {
             one_token_lists(a, lane, my_id, my_w);
             return;
@@ -1925,9 +1911,11 @@ int fastllm_moe_int4_routed(const float* logits, int top_k, int scoring, int nor
         rx.x = x;
         rx.xh = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + p.xh_off);
         rx.hidden = hidden;
+        const int n8 = T * hidden / 8, per = 64 * T;
+        rx.xh_blocks = (n8 + per - 1) / per;
     }
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(route_k, dim3(1), dim3(64 * T), 0, st, rx);
+    hipLaunchKernelGGL(route_k, dim3(1 + rx.xh_blocks), dim3(64 * T), 0, st, rx);
     const int rr = finish("fastllm_moe_int4_routed");
     if (rr) return rr;
     return moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz,
