@@ -37,7 +37,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch of the roofline kernel measured with rocprofv3 --pmc
 # FETCH_SIZE / WRITE_SIZE (x2.000 / x1.000 copy-kernel calibration); see
 # profiles/int4_gemv_gate_up_qwen3_8b_m1_traffic.md.  Keyed by (kernel, M).
-MEASURED_TRAFFIC = {("int4_gemv_nb<2,4,false,0>", 1): 56_816_977}
+MEASURED_TRAFFIC = {("int4_gemv_nb<2,4,false,0>", 1): 52_495_211}
 QWEN3_8B = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096),
             ("down", 4096, 12288)]
 FP8_SHAPES = [("2048x2048", 2048, 2048), ("10944x2048", 10944, 2048), ("2048x10944", 2048, 10944)]
