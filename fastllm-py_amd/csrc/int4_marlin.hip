@@ -259,10 +259,10 @@ __global__ __launch_bounds__(1024) void int4_tile_mm(
 // fp16(silu(g) * u) from the fp16-rounded g and u, which is what the
 // unfused GEMV followed by the reference's swiglu computes
 // (fastllm_py/kernels/ops.py:157-163).  C is then H, M x I.
-template <int T, int NB, bool G32, int AM, bool SWI = false>
-__global__ __launch_bounds__(1024) void int4_gemv_nb(
-    const f16* __restrict__ A, const uint32_t* __restrict__ Wq, const uint16_t* __restrict__ S,
-    const uint32_t* __restrict__ Z, f16* __restrict__ C, int M, int N, int K) {
+template <int T, int NB, bool G32, int AM, bool SWI>
+__device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const uint32_t* __restrict__ Wq,
+                                               const uint16_t* __restrict__ S, const uint32_t* __restrict__ Z,
+                                               f16* __restrict__ C, int M, int N, int K) {
     constexpr int SPB = G32 ? 4 : 1;  // scale groups per 128-k block
     extern __shared__ __align__(16) unsigned char smem[];
     const int nwaves = blockDim.x >> 6;
@@ -292,10 +292,19 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
     for (int t = 0; t < T; ++t) {
         const int nt = SWI ? t * (N >> 5) + strip : strip * T + t;  // n-tile of tile t
         const int n = nt * 16 + col;
-        spos[t] = marlin_scale_pos(n);
-        const int cl = n & 63;
-        zw[t] = ((n >> 6) << 3) + (cl & 7);
-        zsh[t] = 4 * slot_of(cl >> 3);
+        if (SWI && t > 0) {
+            // the up column n + N/2 lies in the same place of a 64-column
+            // chunk N/128 chunks on (N % 128 == 0): scale and zero word
+            // positions shift by uniform amounts, the nibble slot stays
+            spos[t] = spos[0] + (N >> 1);
+            zw[t] = zw[0] + (N >> 4);
+            zsh[t] = zsh[0];
+        } else {
+            spos[t] = marlin_scale_pos(n);
+            const int cl = n & 63;
+            zw[t] = ((n >> 6) << 3) + (cl & 7);
+            zsh[t] = 4 * slot_of(cl >> 3);
+        }
         tbase[t] = Wq + (size_t)nt * (2 * (size_t)K);
     }
 
@@ -489,6 +498,13 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
         for (int w = 0; w < nwaves; ++w) v += red[(w * T + t) * 256 + (idx & 255)];
         C[(size_t)m * N + (strip * T + t) * 16 + (l & 15)] = (f16)v;
     }
+}
+
+template <int T, int NB, bool G32, int AM, bool SWI = false>
+__global__ __launch_bounds__(1024) void int4_gemv_nb(
+    const f16* __restrict__ A, const uint32_t* __restrict__ Wq, const uint16_t* __restrict__ S,
+    const uint32_t* __restrict__ Z, f16* __restrict__ C, int M, int N, int K) {
+    int4_gemv_body<T, NB, G32, AM, SWI>(A, Wq, S, Z, C, M, N, K);
 }
 
 // Prefill-shaped GEMM (M > 64, K % 128 == 0) on the matrix cores.
@@ -965,9 +981,11 @@ hipError_t launch_gemv_swiglu(const f16* A, const uint32_t* Wq, const uint16_t* 
 template <bool G32>
 hipError_t dispatch_swiglu(const f16* A, const uint32_t* Wq, const uint16_t* S, const uint32_t* Z,
                            f16* H, int M, int N, int K, hipStream_t stream) {
-    // the decode config of this shape, with NB <= 4 (register activations)
+    // the decode config of this shape, with NB <= 4 (register activations);
+    // above M = 4 sixteen waves (NB = 2 at K = 4096): the NB = 4 register-A
+    // instantiation of this kernel needs more than 128 VGPRs and spills
     const int nfull = K / 128 > 0 ? K / 128 : 1;
-    int waves = (N >= 16384 && M <= 8) ? 8 : 16;
+    int waves = (N >= 16384 && M <= 4) ? 8 : 16;
     while (waves > 1 && nfull < waves) waves /= 2;
     while ((nfull + waves - 1) / waves > 4 && waves < 16) waves *= 2;
     const int nb = (nfull + waves - 1) / waves;
