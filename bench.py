@@ -177,6 +177,75 @@ def run_swiglu(torch, lib, layers, stream, M_list=(1, 8)):
     return res
 
 
+def run_layer_chain(torch, lib, layers, stream):
+    """One Qwen3-8B decoder layer's quantized-matmul chain at M=1, captured in
+    a HIP graph as the reference's GraphDecoder segment does
+    (graph_decode.py:782-874; attention itself is outside this library): the
+    input add_rmsnorm, qkv, o (on the q slice of qkv, the attention
+    stand-in), the post-attention add_rmsnorm, gate_up with the SwiGLU
+    epilogue and down -- six launches per layer, rotating over the layer
+    copies.  Reported per layer."""
+    H, NQKV, I = 4096, 6144, 12288
+    f32, f16 = torch.float32, torch.float16
+    z = lambda n, dt: torch.zeros(n, dtype=dt, device="cuda")  # noqa: E731
+    x, pend = torch.randn(H, device="cuda"), (torch.randn(H, device="cuda") * 0.5).to(f16)
+    ln1, ln2 = (1 + 0.1 * torch.randn(H, device="cuda")).to(f16), (1 + 0.1 * torch.randn(H, device="cuda")).to(f16)
+    xn1, h1, qkv, o, xn2, h2 = z(H, f32), z(H, f16), z(NQKV, f16), z(H, f16), z(H, f32), z(H, f16)
+    hh, out = z(I, f16), z(H, f16)
+    P = lambda t: t.data_ptr()  # noqa: E731
+
+    def chain(L):
+        def go(h):
+            ok = lib.fastllm_add_rmsnorm(P(x), 1, P(pend), 0, P(ln1), 0, P(xn1), P(h1), 1, H, 1e-6, h) == 0
+            for a, name, c, n, k in ((h1, "qkv", qkv, NQKV, H), (qkv, "o", o, H, H)):
+                p = L[name]
+                ok &= bool(lib.FastllmCudaMarlinHalfInt4GemmStream(
+                    P(a), P(p["qweight"]), P(p["scales"]), P(p["zeros"]), P(c), 1, n, k, GS, None, h))
+            ok &= lib.fastllm_add_rmsnorm(P(xn1), 1, P(o), 0, P(ln2), 0, P(xn2), P(h2), 1, H, 1e-6, h) == 0
+            p = L["gate_up"]
+            ok &= lib.fastllm_int4_gemm_swiglu(P(h2), P(p["qweight"]), P(p["scales"]), P(p["zeros"]),
+                                               P(hh), 1, 2 * I, H, GS, h) == 0
+            p = L["down"]
+            ok &= bool(lib.FastllmCudaMarlinHalfInt4GemmStream(
+                P(hh), P(p["qweight"]), P(p["scales"]), P(p["zeros"]), P(out), 1, H, I, GS, None, h))
+            if not ok:
+                raise RuntimeError("layer chain launch rejected")
+        return go
+
+    def fused(L):
+        # add_rmsnorm in the prologues of qkv and of gate_up + SwiGLU: 4 launches
+        def go(h):
+            p = L["qkv"]
+            ok = lib.fastllm_int4_gemm_add_rmsnorm(P(x), P(pend), P(ln1), 1e-6, P(xn1), P(p["qweight"]),
+                                                   P(p["scales"]), P(p["zeros"]), P(qkv), NQKV, H, GS, 0,
+                                                   h) == 0
+            p = L["o"]
+            ok &= bool(lib.FastllmCudaMarlinHalfInt4GemmStream(
+                P(qkv), P(p["qweight"]), P(p["scales"]), P(p["zeros"]), P(o), 1, H, H, GS, None, h))
+            p = L["gate_up"]
+            ok &= lib.fastllm_int4_gemm_add_rmsnorm(P(xn1), P(o), P(ln2), 1e-6, P(xn2), P(p["qweight"]),
+                                                    P(p["scales"]), P(p["zeros"]), P(hh), 2 * I, H, GS, 1,
+                                                    h) == 0
+            p = L["down"]
+            ok &= bool(lib.FastllmCudaMarlinHalfInt4GemmStream(
+                P(hh), P(p["qweight"]), P(p["scales"]), P(p["zeros"]), P(out), 1, H, I, GS, None, h))
+            if not ok:
+                raise RuntimeError("fused layer chain launch rejected")
+        return go
+
+    n = len(layers)
+    reps = max(1, -(-24 // n))
+    nb = sum(marlin_bytes(0, N, K) for _, N, K in QWEN3_8B)
+    res = {}
+    for name, fn, nl in (("separate_norms", chain, 6), ("norms_in_prologues", fused, 4)):
+        ms = graph_time(torch, stream, [fn(layers[c]) for _ in range(reps) for c in range(n)], 4)
+        us = ms / (reps * n) * 1e3
+        res[name] = {"us_per_layer": round(us, 3), "launches_per_layer": nl,
+                     "weight_GB/s": round(nb / us / 1e3, 1),
+                     "pct_of_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS * 100, 2)}
+    return res
+
+
 # ------------------------------------------------------------------- FP8
 def run_fp8(torch, lib, stream, M_list=(1, 8)):
     from fastllm_py import quantizer
@@ -483,7 +552,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--only", default="int4,swiglu,fp8,moe,gemm")
+    ap.add_argument("--only", default="int4,swiglu,layer,fp8,moe,gemm")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy a 64 MiB buffer 5 times (a known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -534,6 +603,8 @@ def main():
         for m, v in per_m.items()}
     if "swiglu" in only:
         breakdown["int4_gate_up_swiglu"] = run_swiglu(torch, lib, layers, stream)
+    if "layer" in only:
+        breakdown["int4_layer_chain_graph_M1"] = run_layer_chain(torch, lib, layers, stream)
         log(f"gate_up + SwiGLU: {breakdown['int4_gate_up_swiglu']}")
     del layers
     torch.cuda.empty_cache()

@@ -259,10 +259,23 @@ __global__ __launch_bounds__(1024) void int4_tile_mm(
 // fp16(silu(g) * u) from the fp16-rounded g and u, which is what the
 // unfused GEMV followed by the reference's swiglu computes
 // (fastllm_py/kernels/ops.py:157-163).  C is then H, M x I.
+// AM 4 (M = 1): the activation row is add_rmsnorm's output, formed in the
+// prologue from the residual x (fp32), the branch output d (fp16) and the
+// norm weight w (fp16): v = x + d, h = fp16((v * inv) * w) with
+// inv = 1 / sqrt(sum(v^2) / K + eps) (reference: graph_decode.py:300-322).
+struct NormArgs {
+    const float* x;
+    const uint16_t* d;
+    const uint16_t* w;
+    float* xnew;  // x + d, stored by workgroup 0
+    float eps;
+};
+
 template <int T, int NB, bool G32, int AM, bool SWI>
 __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const uint32_t* __restrict__ Wq,
                                                const uint16_t* __restrict__ S, const uint32_t* __restrict__ Z,
-                                               f16* __restrict__ C, int M, int N, int K) {
+                                               f16* __restrict__ C, int M, int N, int K,
+                                               const NormArgs& nrm = NormArgs{}) {
     constexpr int SPB = G32 ? 4 : 1;  // scale groups per 128-k block
     extern __shared__ __align__(16) unsigned char smem[];
     const int nwaves = blockDim.x >> 6;
@@ -280,7 +293,7 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
     const int lda = K + 8;
     f16* As = reinterpret_cast<f16*>(smem);
     // AM 0: wave w's slot of NB blocks x 1 KB (4 rows x 128 k) at w * NB KB
-    const size_t abytes = AM == 0 ? (size_t)nwaves * NB * 1024
+    const size_t abytes = (AM == 0 || AM == 4) ? (size_t)nwaves * NB * 1024
                                   : (ALDS ? (((size_t)M * lda * 2 + 15) & ~(size_t)15) : 0);
     float* red = reinterpret_cast<float*>(smem + abytes);
 
@@ -346,6 +359,26 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(aslot + i * 1024), 16, ao, kb * 256, 0, 0);
         }
     }
+    if (AM == 4) {
+        // slot i of this wave's blocks: [x: 128 fp32][d: 128 fp16][w: 128 fp16];
+        // a copy writes lane l's 16 B at slot + 16 l, so lanes 0-31 carry x,
+        // 32-47 d and 48-63 w (three copies, each with its lanes active)
+        const __amdgpu_buffer_rsrc_t rX = buf_rsrc(nrm.x, (uint32_t)K * 4);
+        const __amdgpu_buffer_rsrc_t rD = buf_rsrc(nrm.d, (uint32_t)K * 2);
+        const __amdgpu_buffer_rsrc_t rW = buf_rsrc(nrm.w, (uint32_t)K * 2);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+            kb = kb < nfull ? kb : nfull - 1;
+            lptr_t dst = (lptr_t)(aslot + i * 1024);
+            if (lane < 32)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rX, dst, 16, 4u * (kb * 128 + 4 * lane), 0, 0, 0);
+            else if (lane < 48)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rD, dst, 16, 2u * (kb * 128 + 8 * (lane - 32)), 0, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, dst, 16, 2u * (kb * 128 + 8 * (lane - 48)), 0, 0, 0);
+        }
+    }
 
     // One straight-line issue of every load this wave will need (block
     // indices clamped into range: no guard, so nothing derived from the loaded
@@ -370,12 +403,61 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    if (AM == 0) {
+    if (AM == 0 || AM == 4) {
         // this wave's activation copies, issued before its weight loads, are
         // done once at most the weight loads are outstanding (no barrier:
         // only this wave reads its slot)
         constexpr int WL = NB * T * (1 + 2 * SPB);
         wait_vmcnt<(WL < 63 ? WL : 63)>();
+    }
+    if (AM == 4) {
+        // add_rmsnorm of the one row: sum of v^2 over this wave's live
+        // blocks (lane l: elements 2l, 2l + 1), the waves' partials summed in
+        // wave order through LDS (an LDS-only barrier: the weights stay in
+        // flight), then h of each block into row 0 of its slot
+        float* npart = reinterpret_cast<float*>(smem + abytes + (size_t)nwaves * T * 1024);
+        float ss = 0.0f;
+        float2 v[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const unsigned char* sl = aslot + (size_t)i * 1024;
+            const float2 xv = *reinterpret_cast<const float2*>(sl + 8 * lane);
+            const uint32_t dv = *reinterpret_cast<const uint32_t*>(sl + 512 + 4 * lane);
+            v[i].x = xv.x + (float)bitcast<f16>((uint16_t)(dv & 0xFFFFu));
+            v[i].y = xv.y + (float)bitcast<f16>((uint16_t)(dv >> 16));
+            if (i < nb) {
+                ss = __builtin_fmaf(v[i].x, v[i].x, ss);
+                ss = __builtin_fmaf(v[i].y, v[i].y, ss);
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if (lane == 0) npart[wave] = ss;
+        lds_barrier();
+        float tot = 0.0f;
+        for (int w = 0; w < nwaves; ++w) tot += npart[w];
+        const float inv = (float)(1.0 / sqrt((double)tot / (double)K + (double)nrm.eps));
+        uint32_t hv[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const uint32_t wv2 = *reinterpret_cast<const uint32_t*>(aslot + (size_t)i * 1024 + 768 + 4 * lane);
+            float y0 = v[i].x * inv * (float)bitcast<f16>((uint16_t)(wv2 & 0xFFFFu));
+            float y1 = v[i].y * inv * (float)bitcast<f16>((uint16_t)(wv2 >> 16));
+            // rounded to fp32 first, as the reference does (no fused
+            // multiply-and-convert)
+            asm volatile("" : "+v"(y0), "+v"(y1));
+            hv[i] = (uint32_t)bitcast<uint16_t>((f16)y0) | ((uint32_t)bitcast<uint16_t>((f16)y1) << 16);
+        }
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < NB; ++i) *reinterpret_cast<uint32_t*>(aslot + (size_t)i * 1024 + 4 * lane) = hv[i];
+        if (blockIdx.x == 0) {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                const int kb = wave + i * nwaves;
+                if (i < nb) *reinterpret_cast<float2*>(nrm.xnew + kb * 128 + 2 * lane) = v[i];
+            }
+        }
     }
     if (ALDS) {
         if (stager) stg.store(As);
@@ -408,7 +490,7 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
         f16x8 a[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            if (AM == 0)
+            if (AM == 0 || AM == 4)
                 a[j] = *reinterpret_cast<const f16x8*>(aslot + (size_t)i * 1024 + arow_m * 256 +
                                                        2 * (32 * j + 8 * kq));
             else if (AM == 3)
@@ -505,6 +587,16 @@ __global__ __launch_bounds__(1024) void int4_gemv_nb(
     const f16* __restrict__ A, const uint32_t* __restrict__ Wq, const uint16_t* __restrict__ S,
     const uint32_t* __restrict__ Z, f16* __restrict__ C, int M, int N, int K) {
     int4_gemv_body<T, NB, G32, AM, SWI>(A, Wq, S, Z, C, M, N, K);
+}
+
+// One decode row (M = 1) with add_rmsnorm in the prologue (AM 4): the GEMV of
+// h = add_rmsnorm(x, d, w) without h ever leaving the chip.
+template <int T, int NB, bool G32, bool SWI>
+__global__ __launch_bounds__(1024) void int4_gemv_norm(NormArgs nrm, const uint32_t* __restrict__ Wq,
+                                                       const uint16_t* __restrict__ S,
+                                                       const uint32_t* __restrict__ Z,
+                                                       f16* __restrict__ C, int N, int K) {
+    int4_gemv_body<T, NB, G32, 4, SWI>(nullptr, Wq, S, Z, C, 1, N, K, nrm);
 }
 
 // Prefill-shaped GEMM (M > 64, K % 128 == 0) on the matrix cores.
@@ -998,6 +1090,54 @@ hipError_t dispatch_swiglu(const f16* A, const uint32_t* Wq, const uint16_t* S, 
     }
 }
 
+template <int T, int NB, bool G32, bool SWI>
+hipError_t launch_gemv_norm(const NormArgs& nrm, const uint32_t* Wq, const uint16_t* S,
+                            const uint32_t* Z, f16* C, int N, int K, int waves, hipStream_t st) {
+    const size_t lds = (size_t)waves * NB * 1024 + (size_t)waves * T * 1024 + 256;
+    const dim3 grid(SWI ? N / 32 : N / (16 * T)), block(64 * waves);
+    hipLaunchKernelGGL((int4_gemv_norm<T, NB, G32, SWI>), grid, block, lds, st, nrm, Wq, S, Z, C, N, K);
+    return hipGetLastError();
+}
+
+template <int T, bool G32, bool SWI>
+hipError_t dispatch_gemv_norm(int nb, const NormArgs& nrm, const uint32_t* Wq, const uint16_t* S,
+                              const uint32_t* Z, f16* C, int N, int K, int waves, hipStream_t st) {
+    switch (nb) {
+        case 1: return launch_gemv_norm<T, 1, G32, SWI>(nrm, Wq, S, Z, C, N, K, waves, st);
+        case 2: return launch_gemv_norm<T, 2, G32, SWI>(nrm, Wq, S, Z, C, N, K, waves, st);
+        case 3: return launch_gemv_norm<T, 3, G32, SWI>(nrm, Wq, S, Z, C, N, K, waves, st);
+        case 4: return launch_gemv_norm<T, 4, G32, SWI>(nrm, Wq, S, Z, C, N, K, waves, st);
+        case 6: return launch_gemv_norm<T, 6, G32, SWI>(nrm, Wq, S, Z, C, N, K, waves, st);
+        default: return launch_gemv_norm<T, 8, G32, SWI>(nrm, Wq, S, Z, C, N, K, waves, st);
+    }
+}
+
+// add_rmsnorm + one decode row's GEMV (or gate/up GEMV with the SwiGLU
+// epilogue).  The plain GEMV's M = 1 shape choice, four blocks per wave at
+// most with 32-groups and eight otherwise.
+template <bool G32>
+hipError_t gemv_norm(const NormArgs& nrm, const uint32_t* Wq, const uint16_t* S, const uint32_t* Z,
+                     f16* C, int N, int K, bool swi, hipStream_t st) {
+    const int nfull = K / 128;
+    const int cap = G32 ? 4 : 8;
+    int waves, tiles;
+    if (swi) {
+        tiles = 2;
+        waves = N >= 16384 ? 8 : 16;
+        while (waves > 1 && nfull < waves) waves /= 2;
+        while ((nfull + waves - 1) / waves > cap && waves < 16) waves *= 2;
+    } else {
+        const GemvCfg c = default_gemv_cfg(1, N, K, G32);
+        tiles = c.tiles == 2 ? 2 : 1;
+        waves = c.waves;
+    }
+    int nb = nb_bucket((nfull + waves - 1) / waves);
+    if (nb > cap) return hipErrorInvalidValue;
+    if (swi) return dispatch_gemv_norm<2, G32, true>(nb, nrm, Wq, S, Z, C, N, K, waves, st);
+    if (tiles == 2) return dispatch_gemv_norm<2, G32, false>(nb, nrm, Wq, S, Z, C, N, K, waves, st);
+    return dispatch_gemv_norm<1, G32, false>(nb, nrm, Wq, S, Z, C, N, K, waves, st);
+}
+
 bool int4_repack(const uint32_t* src, uint32_t* dst, int K, int N, bool inverse,
                  hipStream_t stream) {
     if (!src || !dst || K <= 0 || N <= 0 || K % 64 != 0 || N % 64 != 0) return false;
@@ -1084,6 +1224,30 @@ int fastllm_int4_gemm_swiglu(const void* a, const uint32_t* b_q_weight, const vo
             ? dispatch_swiglu<true>(A, b_q_weight, S, b_zeros, H, size_m, size_n, size_k, (hipStream_t)stream)
             : dispatch_swiglu<false>(A, b_q_weight, S, b_zeros, H, size_m, size_n, size_k, (hipStream_t)stream);
     return report(e, "fastllm_int4_gemm_swiglu") ? 0 : 2;
+}
+
+int fastllm_int4_gemm_add_rmsnorm(const float* x, const void* delta, const void* norm_w, float eps,
+                                  float* xnew, const uint32_t* b_q_weight, const void* b_scales,
+                                  const uint32_t* b_zeros, void* c, int size_n, int size_k,
+                                  int group_size, int swiglu, void* stream) {
+    if (!x || !delta || !norm_w || !xnew || !b_q_weight || !b_scales || !b_zeros || !c) return 1;
+    if (size_k < 128 || size_k % 128 || size_k > 65536 || size_n <= 0 || size_n % 64) return 1;
+    if (swiglu && size_n % 128) return 1;
+    if (group_size != 32 && group_size != 128) return 1;
+    if (!fl_aligned(x, 16) || !fl_aligned(delta, 16) || !fl_aligned(norm_w, 16) || !fl_aligned(xnew, 16) ||
+        !fl_aligned(b_q_weight, 16))
+        return 1;
+    if (!fl_current_device_supported()) return 2;
+    const NormArgs nrm{x, static_cast<const uint16_t*>(delta), static_cast<const uint16_t*>(norm_w), xnew,
+                       eps};
+    const uint16_t* S = static_cast<const uint16_t*>(b_scales);
+    f16* C = static_cast<f16*>(c);
+    const hipError_t e =
+        group_size == 32
+            ? gemv_norm<true>(nrm, b_q_weight, S, b_zeros, C, size_n, size_k, swiglu != 0, (hipStream_t)stream)
+            : gemv_norm<false>(nrm, b_q_weight, S, b_zeros, C, size_n, size_k, swiglu != 0, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return 1;
+    return report(e, "fastllm_int4_gemm_add_rmsnorm") ? 0 : 2;
 }
 
 }  // extern "C"

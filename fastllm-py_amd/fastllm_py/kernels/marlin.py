@@ -144,19 +144,21 @@ def get_workspace(size_n: int):
     return _workspaces[key]
 
 
-def gemm_fast(a_fp16, qweight, scales, zeros, size_n, size_k, stream=None, workspace=None):
+def gemm_fast(a_fp16, qweight, scales, zeros, size_n, size_k, stream=None, workspace=None,
+              out=None):
     """Lean GEMV/GEMM for the decode hot path (marlin.py:205-247).
 
     Trusts that a_fp16 is a contiguous fp16 device tensor and that
     qweight/scales/zeros were validated at load time.  stream: a
     torch.cuda.Stream (or raw handle) to launch on through the stream entry;
     None launches on the null stream.  Like the reference it does not check
-    the entry's return value."""
+    the entry's return value.  ``out``: an optional preallocated contiguous
+    (M, size_n) fp16 tensor (persistent buffers for graph capture)."""
     t = nat.torch()
     lib = nat.lib()
     size_m = a_fp16.shape[0]
     group_size = size_k // scales.shape[0]
-    c = t.empty((size_m, size_n), dtype=t.float16, device=a_fp16.device)
+    c = out if out is not None else t.empty((size_m, size_n), dtype=t.float16, device=a_fp16.device)
     ws = workspace if workspace is not None else get_workspace(size_n)
     if stream is not None:
         lib.FastllmCudaMarlinHalfInt4GemmStream(
@@ -190,6 +192,32 @@ def gemm_swiglu(a_fp16, qweight, scales, zeros, size_n, size_k, out=None, stream
                          f"group={group_size}")
     nat.check_rc(rc, "fastllm_int4_gemm_swiglu")
     return h
+
+
+def gemm_add_rmsnorm(x, delta, norm_w, eps, qweight, scales, zeros, size_n, size_k, swiglu=False,
+                     out=None, xnew=None, stream=None):
+    """One decode row: xnew = x + delta and the Marlin GEMV of
+    h = rmsnorm(xnew) * norm_w in one launch (h stays on chip); with
+    ``swiglu`` the gate/up weight's SwiGLU epilogue as in ``gemm_swiglu``.
+    x (1, K) fp32, delta (1, K) fp16, norm_w (K,) fp16.  Returns (xnew fp32,
+    out fp16 (1, size_n) or (1, size_n/2)).  The reference issues
+    add_rmsnorm then the projection (graph_decode.py:818-826, 858-866)."""
+    t = nat.torch()
+    xd = nat.to_device(x, t.float32).reshape(1, size_k).contiguous()
+    dd = nat.to_device(delta, t.float16).reshape(1, size_k).contiguous()
+    wd = nat.to_device(norm_w, t.float16).reshape(size_k).contiguous()
+    n_out = size_n // 2 if swiglu else size_n
+    c = out if out is not None else t.empty((1, n_out), dtype=t.float16, device=xd.device)
+    xn = xnew if xnew is not None else t.empty((1, size_k), dtype=t.float32, device=xd.device)
+    group_size = size_k // scales.shape[0]
+    hs = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
+    rc = nat.lib().fastllm_int4_gemm_add_rmsnorm(
+        nat.ptr(xd), nat.ptr(dd), nat.ptr(wd), float(eps), nat.ptr(xn), nat.ptr(qweight),
+        nat.ptr(scales), nat.ptr(zeros), nat.ptr(c), size_n, size_k, group_size, int(bool(swiglu)), hs)
+    if rc == 1:
+        raise ValueError(f"gemm_add_rmsnorm: unsupported shape N={size_n} K={size_k} group={group_size}")
+    nat.check_rc(rc, "fastllm_int4_gemm_add_rmsnorm")
+    return xn, c
 
 
 def marlin_gemm_int4(a_fp16, packed_weights, scales, zeros, workspace=None, size_n=None,

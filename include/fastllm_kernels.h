@@ -99,6 +99,37 @@ int fastllm_int4_gemm_swiglu(const void *a, const uint32_t *b_q_weight,
                              void *h, int size_m, int size_n, int size_k,
                              int group_size, void *stream);
 
+/* Residual add + RMSNorm feeding a decode GEMV:
+ *   xnew = x + delta (fp32), h = fp16(xnew * (1/sqrt(mean(xnew^2) + eps)) * w)
+ * per row of `dim`; x, delta, w each fp32 (*_f32 = 1) or fp16 (0).  One
+ * workgroup per row with the reference's thread count and summation order
+ * (sum of squares bit-identical; 1/sqrt(mean + eps) in double rounded once,
+ * where the reference uses rsqrtf).  Returns 0, 1 for bad arguments, 2 for a device or launch
+ * error.
+ * Replaces: add_rmsnorm / GraphDecoder._add_rmsnorm
+ * (fastllm_py/graph_decode.py:291-326, 715-731). */
+int fastllm_add_rmsnorm(const void *x, int x_f32, const void *delta, int delta_f32,
+                        const void *w, int w_f32, float *xnew, uint16_t *h, int rows,
+                        int dim, float eps, void *stream);
+
+/* add_rmsnorm fused into the prologue of one decode row's Marlin GEMV (M = 1):
+ * xnew = x + delta (fp32, stored), h = fp16(xnew * inv * norm_w) with
+ * inv = 1/sqrt(sum(xnew^2)/size_k + eps), and c = h @ dequant(W)^T (fp16,
+ * 1 x size_n) -- or, with swiglu != 0, the SwiGLU epilogue of
+ * fastllm_int4_gemm_swiglu (c is then 1 x size_n/2).  x fp32, delta and
+ * norm_w fp16, 16-byte aligned; size_k % 128 == 0.  h never leaves the chip:
+ * every workgroup forms its own blocks of it while its weight loads are in
+ * flight (the sum of squares is taken in a different order from the
+ * standalone op, so h may differ from it in the last bit).  Returns 0, 1 for
+ * arguments the kernel cannot take, 2 for a device or launch error.
+ * Replaces: the add_rmsnorm launch before a projection plus that projection
+ * (fastllm_py/graph_decode.py:818-826, 858-866); no single reference entry. */
+int fastllm_int4_gemm_add_rmsnorm(const float *x, const void *delta, const void *norm_w,
+                                  float eps, float *xnew, const uint32_t *b_q_weight,
+                                  const void *b_scales, const uint32_t *b_zeros, void *c,
+                                  int size_n, int size_k, int group_size, int swiglu,
+                                  void *stream);
+
 /* Inverse of the repack: tile layout -> GPTQ u32 [size_k/8, size_n].
  * No counterpart in the reference (its repacked layout is opaque); used to
  * prove the repack is a bijection. */
