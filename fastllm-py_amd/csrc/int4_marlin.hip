@@ -1090,6 +1090,38 @@ hipError_t dispatch_swiglu(const f16* A, const uint32_t* Wq, const uint16_t* S, 
     }
 }
 
+// Marlin payload of one expert matrix -> its slot of the fused MoE's stacked
+// tile layout, with the payload's own integers, scales and zeros (no fp16
+// round trip, no requantization).  Both layouts keep, per 16-row tile and
+// 128-k block, 256 u32 of 8 nibbles each in the same nibble order; the u32
+// holding k = 128 kb + 32 a + 8 b + r (r = 0..7) of column c sits at index
+// 4 c + 64 b + a in the Marlin block and 4 c + 64 a + b in the MoE block, so
+// the blocks differ by a 4 x 4 transpose of (a, b) per column.
+//   sz[tile][g][c] = fp16 scale bits | fp16(zero) bits << 16 of row 16 tile + c.
+__global__ void marlin_to_moe_tile_k(const uint32_t* __restrict__ qw, const uint16_t* __restrict__ S,
+                                     const uint32_t* __restrict__ Z, uint32_t* __restrict__ qt,
+                                     uint32_t* __restrict__ sz, int N, int K, int G) {
+    const long nq = (long)N * K / 8, nsz = (long)(N / 16) * G * 16;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < nq + nsz;
+         i += (long)gridDim.x * blockDim.x) {
+        if (i < nq) {
+            const long blk = i >> 8;
+            const int w = (int)(i & 255);
+            const int c = (w >> 2) & 15, a = w >> 6, b = w & 3;
+            qt[i] = qw[(blk << 8) + 4 * c + 64 * b + a];
+        } else {
+            const long j = i - nq;
+            const int c = (int)(j & 15);
+            const long tg = j >> 4;
+            const int g = (int)(tg % G);
+            const int n = (int)(tg / G) * 16 + c;
+            const uint32_t sb = S[(size_t)g * N + marlin_scale_pos(n)];
+            const int z = marlin_zero(Z + (size_t)g * (N / 8), n);
+            sz[j] = sb | ((uint32_t)bitcast<uint16_t>((f16)(float)z) << 16);
+        }
+    }
+}
+
 template <int T, int NB, bool G32, bool SWI>
 hipError_t launch_gemv_norm(const NormArgs& nrm, const uint32_t* Wq, const uint16_t* S,
                             const uint32_t* Z, f16* C, int N, int K, int waves, hipStream_t st) {
@@ -1224,6 +1256,22 @@ int fastllm_int4_gemm_swiglu(const void* a, const uint32_t* b_q_weight, const vo
             ? dispatch_swiglu<true>(A, b_q_weight, S, b_zeros, H, size_m, size_n, size_k, (hipStream_t)stream)
             : dispatch_swiglu<false>(A, b_q_weight, S, b_zeros, H, size_m, size_n, size_k, (hipStream_t)stream);
     return report(e, "fastllm_int4_gemm_swiglu") ? 0 : 2;
+}
+
+int fastllm_marlin_to_moe_tile(const uint32_t* b_q_weight, const void* b_scales,
+                               const uint32_t* b_zeros, uint8_t* qtile, uint32_t* sz, int size_n,
+                               int size_k, int group_size, void* stream) {
+    if (!b_q_weight || !b_scales || !b_zeros || !qtile || !sz) return 1;
+    if (size_n <= 0 || size_n % 64 || size_k <= 0 || size_k % 128) return 1;
+    if (group_size != 32 && group_size != 128) return 1;
+    if (!fl_aligned(b_q_weight, 4) || !fl_aligned(qtile, 4) || !fl_aligned(sz, 4)) return 1;
+    if (!fl_current_device_supported()) return 2;
+    const long work = (long)size_n * size_k / 8 + (long)(size_n / 16) * (size_k / group_size) * 16;
+    const int grid = (int)((work + 255) / 256 < 16384 ? (work + 255) / 256 : 16384);
+    hipLaunchKernelGGL(marlin_to_moe_tile_k, dim3(grid), dim3(256), 0, (hipStream_t)stream, b_q_weight,
+                       static_cast<const uint16_t*>(b_scales), b_zeros, reinterpret_cast<uint32_t*>(qtile),
+                       sz, size_n, size_k, size_k / group_size);
+    return report(hipGetLastError(), "fastllm_marlin_to_moe_tile") ? 0 : 2;
 }
 
 int fastllm_int4_gemm_add_rmsnorm(const float* x, const void* delta, const void* norm_w, float eps,

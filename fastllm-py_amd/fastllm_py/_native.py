@@ -30,6 +30,7 @@ SIGNATURES: dict[str, tuple] = {
     "fastllm_int4_gemm_config": (_B, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "fastllm_int4_gemm_swiglu": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "fastllm_add_rmsnorm": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _I, _I, _F, _P]),
+    "fastllm_marlin_to_moe_tile": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "fastllm_int4_gemm_add_rmsnorm": (_I, [_P, _P, _P, _F, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     # packers / unpackers
     "fastllm_pack_gptq_qweight": (_I, [_P, _P, _I, _I, _P]),

@@ -130,6 +130,38 @@ def build_stacked_experts(expert_ws, group_size: int = 128, xp=np) -> dict:
     return out
 
 
+def stack_marlin_experts(payloads, group_size: int = 128) -> dict:
+    """Stacked experts straight from resident Marlin payloads: ``payloads`` is
+    a list over experts of {"gate", "up", "down"} -> Marlin dicts (qweight,
+    scales, zeros, as ``moe.quantize_marlin_matrix_device`` makes them).  Each
+    matrix is copied on the GPU into its expert's slot of the tile layout with
+    its own integers, scales and zeros -- no fp16 round trip and no
+    requantization (the reference dequantizes to fp16 and quantizes again,
+    moe_int4.py:116-133; docs/next-optimizations.md:108-135)."""
+    t = nat.torch()
+    out = {"group": group_size, "layout": "tile16x128"}
+    E = len(payloads)
+    hs = nat.current_stream_handle()
+    for proj in ("gate", "up", "down"):
+        p0 = payloads[0][proj]
+        out_f = p0["scales"].shape[1]
+        G = p0["scales"].shape[0]
+        in_f = G * group_size
+        dev = p0["qweight"].device
+        qt = t.empty((E, out_f // 16, in_f // 128, 1024), dtype=t.uint8, device=dev)
+        sz = t.empty((E, out_f // 16, G, 16), dtype=t.int32, device=dev)
+        for e, pe in enumerate(payloads):
+            p = pe[proj]
+            if tuple(p["scales"].shape) != (G, out_f):
+                raise ValueError(f"stack_marlin_experts: expert {e} {proj} scales {tuple(p['scales'].shape)}")
+            rc = nat.lib().fastllm_marlin_to_moe_tile(nat.ptr(p["qweight"]), nat.ptr(p["scales"]),
+                                                      nat.ptr(p["zeros"]), nat.ptr(qt[e]), nat.ptr(sz[e]),
+                                                      out_f, in_f, group_size, hs)
+            nat.check_rc(rc, "fastllm_marlin_to_moe_tile")
+        out[f"{proj}.qtile"], out[f"{proj}.sz"], out[f"{proj}.shape"] = qt, sz, (out_f, in_f)
+    return out
+
+
 def stack_tiles(proj: str, qw, sc, ze, group_size: int) -> dict:
     """Row-major stacked (E, out, in/2) / (E, out, in/gs) -> the tile-layout
     entries of one projection of a stacked-experts dict."""

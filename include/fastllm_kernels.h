@@ -130,6 +130,20 @@ int fastllm_int4_gemm_add_rmsnorm(const float *x, const void *delta, const void 
                                   int size_n, int size_k, int group_size, int swiglu,
                                   void *stream);
 
+/* Marlin payload of one matrix (this library's repacked qweight, permuted
+ * fp16 scales, packed zeros; size_n % 64 == 0, size_k % 128 == 0, group 32 or
+ * 128) -> the fused MoE's stacked tile layout for those rows: qtile
+ * (size_n/16, size_k/128, 1024) u8 and sz (size_n/16, size_k/group, 16) u32
+ * (fp16 scale | fp16 zero << 16).  Bit-exact: the payload's own integers,
+ * scales and zeros, no fp16 round trip.  Returns 0, 1 for bad arguments, 2
+ * for a device or launch error.
+ * Replaces: build_stacked_experts's dequantize-Marlin-to-fp16 then
+ * requantize path for resident Marlin experts (fastllm_py/kernels/
+ * moe_int4.py:116-133; docs/next-optimizations.md:108-135). */
+int fastllm_marlin_to_moe_tile(const uint32_t *b_q_weight, const void *b_scales,
+                               const uint32_t *b_zeros, uint8_t *qtile, uint32_t *sz,
+                               int size_n, int size_k, int group_size, void *stream);
+
 /* Inverse of the repack: tile layout -> GPTQ u32 [size_k/8, size_n].
  * No counterpart in the reference (its repacked layout is opaque); used to
  * prove the repack is a bijection. */

@@ -533,6 +533,48 @@ def test_moe_route_forward_sigmoid_groups(torch_gpu, T):
         assert Q.max_abs_rel(y.cpu().numpy(), y2.cpu().numpy()) < 1e-5
 
 
+@pytest.mark.parametrize("hidden,inter,gs", [(512, 384, 128), (256, 640, 32)])
+def test_stack_marlin_experts_bit_exact(torch_gpu, hidden, inter, gs):
+    """Resident Marlin payloads -> stacked tile layout on the GPU: the tiles are
+    the oracle's tile pack of the very integers, scales and zeros the Marlin
+    quantizer produced, and the fused MoE over them matches the oracle on the
+    Marlin-dequantized weights."""
+    from fastllm_py.kernels import moe_int4
+    from fastllm_py.moe import quantize_marlin_matrix_device
+
+    torch = torch_gpu
+    rng = np.random.default_rng(6100 + hidden + gs)
+    E, K = 3, 2
+    exps = _experts(rng, E, hidden, inter, 0.05)
+    pays = [{p: quantize_marlin_matrix_device(torch.from_numpy(w[p].astype(np.float32)).cuda(), gs)
+             for p in ("gate", "up", "down")} for w in exps]
+    st = moe_int4.stack_marlin_experts(pays, gs)
+    deq = {}
+    for proj in ("gate", "up", "down"):
+        ws = [w[proj].astype(np.float32) for w in exps]
+        qs, hats = [], []
+        for W in ws:
+            q, s, z = Q.quantize_int4_marlin(W, gs)
+            s16, zp = Q.marlin_scales_zeros(s, z)
+            hats.append(Q.marlin_dequant(q, s16, zp, gs))
+            qs.append(Q.moe_tile_pack(Q._pack_pairs(q), s.astype(np.float16), z.astype(np.float16)))
+        np.testing.assert_array_equal(st[f"{proj}.qtile"].cpu().numpy(),
+                                      np.stack([a for a, _ in qs]).reshape(st[f"{proj}.qtile"].shape))
+        np.testing.assert_array_equal(st[f"{proj}.sz"].cpu().numpy().view(np.uint32),
+                                      np.stack([b for _, b in qs]).reshape(st[f"{proj}.sz"].shape))
+        deq[proj] = np.stack(hats)
+    from fastllm_py.expert_router import route_topk_device
+
+    T = 2
+    x = (rng.standard_normal((T, hidden)) * 0.5).astype(np.float32)
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).cuda()
+    r = route_topk_device(logits, K)
+    y = moe_int4.moe_forward(torch.from_numpy(x).cuda(), st, E, hidden, inter, r, max_slots=E,
+                             max_entries=T * K)
+    ref = OM.moe_ref(x, deq, r["topk_ids"].cpu().numpy(), r["topk_w"].cpu().numpy())
+    assert Q.max_abs_rel(y.cpu().numpy(), ref) < 5e-3
+
+
 def test_fused_moe_edge_lists(torch_gpu):
     """ffn2 with a repeated expert (two slots, summed), zero weights (dropped)
     and all-zero routing without a shared expert (y == 0)."""
