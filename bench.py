@@ -285,6 +285,34 @@ def run_fp8(torch, lib, stream, M_list=(1, 8)):
     return res
 
 
+def run_fp8_prefill(torch, lib, stream, M=512):
+    """The config-3 shapes at prefill size (M=512, bf16): the FP8 MFMA GEMM,
+    with its MFMA utilisation against the dense bf16 peak."""
+    from fastllm_py import quantizer
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3100)
+    res = {}
+    for name, N, K in FP8_SHAPES:
+        W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+        qt = quantizer.quantize_fp8_block(W, 128)
+        del W
+        x = torch.randn((M, K), generator=gen, device="cuda").to(torch.bfloat16)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        f = lib.fastllm_fp8_b128x128_gemv
+
+        def go(h, q=qt.data, s=qt.scales, x=x, y=y, N=N, K=K):
+            if f(x.data_ptr(), q.data_ptr(), s.data_ptr(), None, y.data_ptr(), M, N, K, 1, h):
+                raise RuntimeError("fp8 gemm failed")
+        us = graph_time(torch, stream, [go] * 20, 5) / 20 * 1e3
+        tf = 2.0 * M * N * K / us / 1e6
+        res[f"{name}/M{M}"] = {"us_per_call": round(us, 3), "TFLOP/s": round(tf, 1),
+                               "mfma_util_bf16_dense": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+        del qt
+        torch.cuda.empty_cache()
+    return res
+
+
 # ------------------------------------------------------------------- MoE
 def run_moe(torch, lib, stream, T_list=(1, 16)):
     """Fused Qwen1.5-MoE-A2.7B INT4 layer: router from fp16 logits ~ N(0,1)
@@ -552,7 +580,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--only", default="int4,swiglu,layer,fp8,moe,gemm")
+    ap.add_argument("--only", default="int4,swiglu,layer,fp8,fp8p,moe,gemm")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy a 64 MiB buffer 5 times (a known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -617,6 +645,9 @@ def main():
     if "fp8" in only:
         breakdown["fp8_b128x128_bf16"] = run_fp8(torch, lib, stream)
         log(f"FP8: {breakdown['fp8_b128x128_bf16']}")
+    if "fp8p" in only:
+        breakdown["fp8_prefill_gemm_M512"] = run_fp8_prefill(torch, lib, stream)
+        log(f"FP8 prefill: {breakdown['fp8_prefill_gemm_M512']}")
     if "moe" in only:
         breakdown["moe_qwen15_a27b_int4"] = run_moe(torch, lib, stream)
         log(f"MoE: {breakdown['moe_qwen15_a27b_int4']}")

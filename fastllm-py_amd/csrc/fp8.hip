@@ -608,6 +608,164 @@ Fp8Cfg fp8_cfg(int M, int N, int K) {
 
 constexpr size_t kFp8LdsCap = 96 * 1024;
 
+// Prefill-shaped FP8 GEMM (M > kF8MinM, 128 x 128 block format, K % 128 ==
+// 0) on the matrix cores: the INT4 MFMA GEMM's structure with e4m3 weights.
+//   * Workgroup tile 64 (m) x 256 (n), eight waves side by side along n, a
+//     64 x 32 wave tile (4 m-tiles x 2 n-tiles of 16 x 16 fp32).
+//   * Every main-loop load goes global -> LDS (buffer_load ... lds) two
+//     128-k blocks ahead into a ring of three stages, one vmcnt wait and one
+//     barrier per block.  A stage holds the 64 x 128 activation tile
+//     fragment-major (the 1 KB of (m-tile, 32-k step j) holds lane l's MFMA A
+//     operand at 16 l) and the strip's 256 weight rows x 128 codes: n-tile s,
+//     half i, lane (c, g) at 2048 s + 1024 i + 16 (c + 16 g) holds codes
+//     [64 i + 16 g, + 16) of row c -- so MFMA lane (c, q) finds its 8 codes of
+//     step j at 16 (c + 16 (2 (j & 1) + q / 2)) + 8 (q & 1) of half j / 2, and
+//     a ds_read_b64 over the wave touches each bank once.
+//   * Codes become fp16/bf16 exactly (v_cvt_scalef32_pk_*_fp8, scale 1); each
+//     block's MFMAs accumulate into a fresh partial that the fp32 block scale
+//     then adds into the accumulator, as the GEMV does.
+//   * A trailing 64-wide block is a 128-k block whose second half is read as
+//     zeros (source offsets past the buffer end), activations and codes both.
+constexpr int kF8BM = 64, kF8BN = 256, kF8MinM = 64;
+constexpr int kF8Ahead = 2, kF8Stages = kF8Ahead + 1;
+constexpr int kF8StA = 0, kF8StB = 16384, kF8Stage = kF8StB + 32768;
+constexpr size_t kF8Lds = (size_t)kF8Stages * kF8Stage;
+
+template <bool BF16>
+__global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict__ A,
+                                                     const uint8_t* __restrict__ W,
+                                                     const float* __restrict__ Sc,
+                                                     const uint16_t* __restrict__ bias,
+                                                     uint16_t* __restrict__ C, int M, int N, int K,
+                                                     int nks) {
+    constexpr int D = kF8Ahead, NS = kF8Stages;
+    constexpr int LPB = 2 + 4;  // copies per block and wave: 2 A fragments, 2 tiles x 2 halves
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, kq = lane >> 4;
+    const int nkb = (K + 127) >> 7;  // a trailing 64-wide block counts as one
+    const int ntiles = (N + 15) >> 4;
+
+    const int nblk = (N + kF8BN - 1) / kF8BN, mblk = (M + kF8BM - 1) / kF8BM;
+    const int total = nblk * mblk;
+    int lin = blockIdx.x;
+    if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);  // XCD-grouped
+    const int nb_i = lin / mblk, mb_i = lin - nb_i * mblk;
+    const int m0 = mb_i * kF8BM;
+    const int nt_base = nb_i * 16;
+
+    const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)M * K * 2);
+    const __amdgpu_buffer_rsrc_t rW = buf_rsrc(W, (uint32_t)N * K);
+    // per-lane source offsets; a piece at k >= K (the second half of a
+    // trailing 64-wide block) points past the buffer, and the copy reads zeros
+    constexpr uint32_t kOut = 0x80000000u;
+    uint32_t ao[2], bo[2][2];
+    int ak[2], bk[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int f = wave * 2 + i;  // fragment f = 4 m-tile + step
+        int m = m0 + 16 * (f >> 2) + col;
+        m = m < M ? m : M - 1;
+        ak[i] = 32 * (f & 3) + 8 * kq;
+        ao[i] = 2u * ((uint32_t)m * K + ak[i]);
+        int n = (nt_base + wave * 2 + i) * 16 + col;
+        n = n < N ? n : N - 1;
+        bk[i] = 16 * kq;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) bo[i][h] = (uint32_t)n * K + 64 * h + 16 * kq;
+    }
+    auto issue = [&](int kb, int slot) {
+        kb = kb < nkb ? kb : nkb - 1;
+        unsigned char* st = smem + (size_t)slot * kF8Stage;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rA, (lptr_t)(st + kF8StA + (wave * 2 + i) * 1024), 16,
+                kb * 128 + ak[i] < K ? ao[i] + kb * 256 : kOut, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rW, (lptr_t)(st + kF8StB + (wave * 2 + i) * 2048 + h * 1024), 16,
+                    kb * 128 + 64 * h + bk[i] < K ? bo[i][h] + kb * 128 : kOut, 0, 0, 0);
+    };
+    // block-scale rows of this wave's two n-tiles (a 16-row tile lies in one band)
+    const float* srow[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        int nt = nt_base + wave * 2 + t;
+        nt = nt < ntiles ? nt : ntiles - 1;
+        srow[t] = Sc + (size_t)((nt * 16) >> 7) * nks;
+    }
+
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < D; ++d) issue(d, d);
+
+    const int boff = 16 * col + 8 * (kq & 1);
+    for (int kb0 = 0; kb0 < nkb; kb0 += NS) {
+#pragma unroll
+        for (int u = 0; u < NS; ++u) {
+            const int kb = kb0 + u;
+            const bool live = kb < nkb;
+            wait_vmcnt<(D - 1) * LPB>();
+            asm volatile("s_barrier" ::: "memory");
+            issue(kb + D, (u + D) % NS);
+            const unsigned char* st = smem + (size_t)u * kF8Stage;
+            f32x4 part[4][2];
+#pragma unroll
+            for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) part[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                u32x4 a[4];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+                    a[mt] = *reinterpret_cast<const u32x4*>(st + kF8StA + (mt * 4 + j) * 1024 + lane * 16);
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const uint2 w8 = *reinterpret_cast<const uint2*>(
+                        st + kF8StB + (wave * 2 + t) * 2048 + (j >> 1) * 1024 + 256 * (2 * (j & 1) + (kq >> 1)) +
+                        boff);
+                    const u32x4 b = fp8x8_to_16<BF16>(w8.x, w8.y);
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt) part[mt][t] = mfma16<BF16>(a[mt], b, part[mt][t]);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const float s = live ? srow[t][kb < nkb ? kb : nkb - 1] : 0.0f;
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[mt][t][e] = __builtin_fmaf(s, part[mt][t][e], acc[mt][t][e]);
+            }
+        }
+    }
+    wait_vmcnt<0>();  // no LDS copy may still be in flight when the workgroup ends
+
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int n = (nt_base + wave * 2 + t) * 16 + col;
+        if (n >= N) continue;
+        const float bv = bias ? act_to_f32<BF16>(bias[n]) : 0.0f;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = m0 + mt * 16 + 4 * kq + e;
+                if (m < M) C[(size_t)m * N + n] = f32_to_act<BF16>(acc[mt][t][e] + bv);
+            }
+    }
+}
+
 template <int T, int NB, bool INLINE, bool BF16>
 hipError_t launch_fp8(const uint16_t* A, const uint8_t* W, const float* Sc, const uint16_t* bias,
                       uint16_t* C, int M, int N, int K, int rs, int nks, int waves,
@@ -658,6 +816,14 @@ hipError_t fp8_gemm(const uint16_t* A, const uint8_t* W, const float* Sc, const 
     // M <= 8 there: the halved 8-row kernel (K <= 128 x 2 x 64)
     if (M <= 8 && K >= 512 && K <= 16384 && N < 8192 && N % 8 == 0)
         return fp8_q2<INLINE, BF16>(A, W, Sc, bias, C, M, N, K, rs, nks, st);
+    // prefill-shaped: the MFMA GEMM (128 x 128 format; K % 64 == 0)
+    if (!INLINE && M > kF8MinM && K % 64 == 0 && (size_t)N * K < (1ull << 31) &&
+        (size_t)M * K * 2 < (1ull << 31)) {
+        const int tiles = ((N + kF8BN - 1) / kF8BN) * ((M + kF8BM - 1) / kF8BM);
+        hipLaunchKernelGGL((fp8_gemm_mfma<BF16>), dim3(tiles), dim3(512), kF8Lds, st, A, W, Sc, bias, C, M,
+                           N, K, nks);
+        return hipGetLastError();
+    }
     // decode-shaped kernel, 16 activation rows per launch
     for (int m0 = 0; m0 < M; m0 += 16) {
         const int Mc = (M - m0) < 16 ? (M - m0) : 16;

@@ -158,3 +158,27 @@ def test_fp8_block_gemv_fp16_bias_ragged(torch_gpu, N, K, M):
     ref = Q.matmul_ref(x.float().cpu().numpy(), Q.dequantize_fp8_block(q_ref, s_ref, 128))
     ref = ref + b.float().cpu().numpy()[None]
     assert Q.max_abs_rel(out.float().cpu().numpy(), ref) < TOL
+
+
+# prefill-shaped (M > 64): the MFMA GEMM, ragged M and N, K ending in a 64-wide block,
+# both activation types, bias
+@pytest.mark.parametrize("M,N,K,bf16", [(128, 2048, 2048, True), (200, 1000, 1024, False),
+                                        (65, 4096, 512, True), (512, 10944, 2048, True),
+                                        (128, 2048, 10944, True), (96, 256, 320, False)])
+def test_fp8_block_gemm_prefill(torch_gpu, M, N, K, bf16):
+    from fastllm_py import quantizer
+    from fastllm_py.kernels import fp8
+
+    torch = torch_gpu
+    rng = np.random.default_rng(8100 + M + N + K)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    dt = torch.bfloat16 if bf16 else torch.float16
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda().to(dt)
+    b = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).cuda().to(dt)
+    qt = quantizer.quantize_fp8_block(torch.from_numpy(W).cuda(), 128)
+    out = fp8.fp8_gemv_block(x, qt.data, qt.scales, bias=b)
+    assert out.shape == (M, N) and out.dtype == dt
+    q_ref, s_ref = Q.quantize_fp8_block(W, 128)
+    ref = Q.matmul_ref(x.float().cpu().numpy(), Q.dequantize_fp8_block(q_ref, s_ref, 128))
+    ref = ref + b.float().cpu().numpy()[None]
+    assert Q.max_abs_rel(out.float().cpu().numpy(), ref) < TOL
