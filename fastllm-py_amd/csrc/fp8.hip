@@ -610,13 +610,15 @@ constexpr size_t kFp8LdsCap = 96 * 1024;
 
 // Prefill-shaped FP8 GEMM (M > kF8MinM, 128 x 128 block format, K % 128 ==
 // 0) on the matrix cores: the INT4 MFMA GEMM's structure with e4m3 weights.
-//   * Workgroup tile 64 (m) x 256 (n), eight waves side by side along n, a
-//     64 x 32 wave tile (4 m-tiles x 2 n-tiles of 16 x 16 fp32).
-//   * Every main-loop load goes global -> LDS (buffer_load ... lds) two
-//     128-k blocks ahead into a ring of three stages, one vmcnt wait and one
-//     barrier per block.  A stage holds the 64 x 128 activation tile
+//   * Workgroup tile 64 (m) x 128 (n), eight waves side by side along n, a
+//     64 x 16 wave tile (4 m-tiles x one n-tile of 16 x 16 fp32).  (64 x 256
+//     tiles in three 48 KB stages measured 40 / 162 / 82 us at M = 512 for
+//     2048 x 2048 / 2048 x 10944 / 10944 x 2048, against 26.7 / 120 / 79.)
+//   * Every main-loop load goes global -> LDS (buffer_load ... lds) three
+//     128-k blocks ahead into a ring of four 32 KB stages, one vmcnt wait and
+//     one barrier per block.  A stage holds the 64 x 128 activation tile
 //     fragment-major (the 1 KB of (m-tile, 32-k step j) holds lane l's MFMA A
-//     operand at 16 l) and the strip's 256 weight rows x 128 codes: n-tile s,
+//     operand at 16 l) and the strip's 128 weight rows x 128 codes: n-tile s,
 //     half i, lane (c, g) at 2048 s + 1024 i + 16 (c + 16 g) holds codes
 //     [64 i + 16 g, + 16) of row c -- so MFMA lane (c, q) finds its 8 codes of
 //     step j at 16 (c + 16 (2 (j & 1) + q / 2)) + 8 (q & 1) of half j / 2, and
@@ -626,9 +628,9 @@ constexpr size_t kFp8LdsCap = 96 * 1024;
 //     then adds into the accumulator, as the GEMV does.
 //   * A trailing 64-wide block is a 128-k block whose second half is read as
 //     zeros (source offsets past the buffer end), activations and codes both.
-constexpr int kF8BM = 64, kF8BN = 256, kF8MinM = 64;
-constexpr int kF8Ahead = 2, kF8Stages = kF8Ahead + 1;
-constexpr int kF8StA = 0, kF8StB = 16384, kF8Stage = kF8StB + 32768;
+constexpr int kF8BM = 64, kF8BN = 128, kF8MinM = 64;
+constexpr int kF8Ahead = 3, kF8Stages = kF8Ahead + 1;
+constexpr int kF8StA = 0, kF8StB = 16384, kF8Stage = kF8StB + 16384;
 constexpr size_t kF8Lds = (size_t)kF8Stages * kF8Stage;
 
 template <bool BF16>
@@ -639,7 +641,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
                                                      uint16_t* __restrict__ C, int M, int N, int K,
                                                      int nks) {
     constexpr int D = kF8Ahead, NS = kF8Stages;
-    constexpr int LPB = 2 + 4;  // copies per block and wave: 2 A fragments, 2 tiles x 2 halves
+    constexpr int LPB = 2 + 2;  // copies per block and wave: 2 A fragments, its tile's 2 halves
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -653,15 +655,15 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
     if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);  // XCD-grouped
     const int nb_i = lin / mblk, mb_i = lin - nb_i * mblk;
     const int m0 = mb_i * kF8BM;
-    const int nt_base = nb_i * 16;
+    const int nt_base = nb_i * 8;
 
     const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)M * K * 2);
     const __amdgpu_buffer_rsrc_t rW = buf_rsrc(W, (uint32_t)N * K);
     // per-lane source offsets; a piece at k >= K (the second half of a
     // trailing 64-wide block) points past the buffer, and the copy reads zeros
     constexpr uint32_t kOut = 0x80000000u;
-    uint32_t ao[2], bo[2][2];
-    int ak[2], bk[2];
+    uint32_t ao[2], bo[1][2];
+    int ak[2], bk[1];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const int f = wave * 2 + i;  // fragment f = 4 m-tile + step
@@ -669,11 +671,13 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
         m = m < M ? m : M - 1;
         ak[i] = 32 * (f & 3) + 8 * kq;
         ao[i] = 2u * ((uint32_t)m * K + ak[i]);
-        int n = (nt_base + wave * 2 + i) * 16 + col;
+    }
+    {
+        int n = (nt_base + wave) * 16 + col;
         n = n < N ? n : N - 1;
-        bk[i] = 16 * kq;
+        bk[0] = 16 * kq;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) bo[i][h] = (uint32_t)n * K + 64 * h + 16 * kq;
+        for (int h = 0; h < 2; ++h) bo[0][h] = (uint32_t)n * K + 64 * h + 16 * kq;
     }
     auto issue = [&](int kb, int slot) {
         kb = kb < nkb ? kb : nkb - 1;
@@ -684,27 +688,27 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
                 rA, (lptr_t)(st + kF8StA + (wave * 2 + i) * 1024), 16,
                 kb * 128 + ak[i] < K ? ao[i] + kb * 256 : kOut, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 1; ++i)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rW, (lptr_t)(st + kF8StB + (wave * 2 + i) * 2048 + h * 1024), 16,
+                    rW, (lptr_t)(st + kF8StB + (wave + i) * 2048 + h * 1024), 16,
                     kb * 128 + 64 * h + bk[i] < K ? bo[i][h] + kb * 128 : kOut, 0, 0, 0);
     };
     // block-scale rows of this wave's two n-tiles (a 16-row tile lies in one band)
-    const float* srow[2];
+    const float* srow[1];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        int nt = nt_base + wave * 2 + t;
+    for (int t = 0; t < 1; ++t) {
+        int nt = nt_base + wave + t;
         nt = nt < ntiles ? nt : ntiles - 1;
         srow[t] = Sc + (size_t)((nt * 16) >> 7) * nks;
     }
 
-    f32x4 acc[4][2];
+    f32x4 acc[4][1];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int t = 0; t < 2; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 1; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(d, d);
 
@@ -718,11 +722,11 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
             asm volatile("s_barrier" ::: "memory");
             issue(kb + D, (u + D) % NS);
             const unsigned char* st = smem + (size_t)u * kF8Stage;
-            f32x4 part[4][2];
+            f32x4 part[4][1];
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                for (int t = 0; t < 2; ++t) part[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int t = 0; t < 1; ++t) part[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 u32x4 a[4];
@@ -730,9 +734,9 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
                 for (int mt = 0; mt < 4; ++mt)
                     a[mt] = *reinterpret_cast<const u32x4*>(st + kF8StA + (mt * 4 + j) * 1024 + lane * 16);
 #pragma unroll
-                for (int t = 0; t < 2; ++t) {
+                for (int t = 0; t < 1; ++t) {
                     const uint2 w8 = *reinterpret_cast<const uint2*>(
-                        st + kF8StB + (wave * 2 + t) * 2048 + (j >> 1) * 1024 + 256 * (2 * (j & 1) + (kq >> 1)) +
+                        st + kF8StB + (wave + t) * 2048 + (j >> 1) * 1024 + 256 * (2 * (j & 1) + (kq >> 1)) +
                         boff);
                     const u32x4 b = fp8x8_to_16<BF16>(w8.x, w8.y);
 #pragma unroll
@@ -740,7 +744,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
                 }
             }
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
+            for (int t = 0; t < 1; ++t) {
                 const float s = live ? srow[t][kb < nkb ? kb : nkb - 1] : 0.0f;
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
@@ -752,8 +756,8 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
     wait_vmcnt<0>();  // no LDS copy may still be in flight when the workgroup ends
 
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        const int n = (nt_base + wave * 2 + t) * 16 + col;
+    for (int t = 0; t < 1; ++t) {
+        const int n = (nt_base + wave + t) * 16 + col;
         if (n >= N) continue;
         const float bv = bias ? act_to_f32<BF16>(bias[n]) : 0.0f;
 #pragma unroll
