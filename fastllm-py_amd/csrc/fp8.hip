@@ -611,12 +611,14 @@ constexpr size_t kFp8LdsCap = 96 * 1024;
 // Prefill-shaped FP8 GEMM (M > kF8MinM, 128 x 128 block format, K % 128 ==
 // 0) on the matrix cores: the INT4 MFMA GEMM's structure with e4m3 weights.
 //   * Workgroup tile 64 (m) x 128 (n), eight waves side by side along n, a
-//     64 x 16 wave tile (4 m-tiles x one n-tile of 16 x 16 fp32).  (64 x 256
-//     tiles in three 48 KB stages measured 40 / 162 / 82 us at M = 512 for
-//     2048 x 2048 / 2048 x 10944 / 10944 x 2048, against 26.7 / 120 / 79.)
-//   * Every main-loop load goes global -> LDS (buffer_load ... lds) three
-//     128-k blocks ahead into a ring of four 32 KB stages, one vmcnt wait and
-//     one barrier per block.  A stage holds the 64 x 128 activation tile
+//     64 x 16 wave tile (4 m-tiles x one n-tile of 16 x 16 fp32).
+//   * Every main-loop load goes global -> LDS (buffer_load ... lds) one
+//     128-k block ahead into two 32 KB stages (64 KB: two workgroups per CU),
+//     one vmcnt wait and one barrier per block.  At M = 512 for 2048 x 2048 /
+//     10944 x 2048 / 2048 x 10944 this measured 25.2 / 60.7 / 118.6 us,
+//     against 26.7 / 79.4 / 120.4 with four stages (one workgroup per CU)
+//     and 40 / 82 / 162 with 64 x 256 tiles in three 48 KB stages.
+//     A stage holds the 64 x 128 activation tile
 //     fragment-major (the 1 KB of (m-tile, 32-k step j) holds lane l's MFMA A
 //     operand at 16 l) and the strip's 128 weight rows x 128 codes: n-tile s,
 //     half i, lane (c, g) at 2048 s + 1024 i + 16 (c + 16 g) holds codes
@@ -629,7 +631,7 @@ constexpr size_t kFp8LdsCap = 96 * 1024;
 //   * A trailing 64-wide block is a 128-k block whose second half is read as
 //     zeros (source offsets past the buffer end), activations and codes both.
 constexpr int kF8BM = 64, kF8BN = 128, kF8MinM = 64;
-constexpr int kF8Ahead = 3, kF8Stages = kF8Ahead + 1;
+constexpr int kF8Ahead = 1, kF8Stages = kF8Ahead + 1;
 constexpr int kF8StA = 0, kF8StB = 16384, kF8Stage = kF8StB + 16384;
 constexpr size_t kF8Lds = (size_t)kF8Stages * kF8Stage;
 
