@@ -242,7 +242,14 @@ __global__ __launch_bounds__(1024) void int4_tile_mm(
 //         system, which serialises the compute tail behind the stream;
 //       AM 1: the M x K rows are staged once per workgroup in LDS (row stride
 //         K+8 halves) behind an LDS-only barrier;
-//       AM 2: MFMA A operands are read from global memory at use;
+//       AM 2 (M > 4, NB > 4, M x K too large for AM 1): a ring of three
+//         register slots -- the A operands of a wave's first three blocks
+//         are loaded ahead of its weights, and block i + 3's are issued once
+//         block i's MFMAs have read slot i % 3.  Loads complete in issue
+//         order, so the first three blocks wait only for their own weights,
+//         and by the time the later blocks' weights have arrived so have
+//         their activations (loaded at use, each block would wait a full L2
+//         round trip after all of the wave's weights);
 //       AM 3 (M > 4, NB <= 4): each lane loads its own MFMA A operands of all
 //         its blocks from global memory into registers (4 x 16 B per block),
 //         first of all, so they arrive ahead of the weights in issue order;
@@ -338,6 +345,18 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
     unsigned char* aslot = smem + (size_t)wave * NB * 1024;
     const int arow_m = col < M ? col : M - 1;
     f16x8 ar[NB][4];
+    constexpr int kRing = 3;  // AM 2 register slots
+    f16x8 rg[kRing][4];
+    if (AM == 2) {
+        const f16* ap = A + (size_t)arow_m * K + 8 * kq;
+#pragma unroll
+        for (int i = 0; i < (NB < kRing ? NB : kRing); ++i) {
+            int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+            kb = kb < nfull ? kb : nfull - 1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) rg[i][j] = *reinterpret_cast<const f16x8*>(ap + kb * 128 + 32 * j);
+        }
+    }
     if (AM == 3) {
         const f16* ap = A + (size_t)arow_m * K + 8 * kq;
 #pragma unroll
@@ -495,6 +514,8 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
                                                        2 * (32 * j + 8 * kq));
             else if (AM == 3)
                 a[j] = ar[i][j];
+            else if (AM == 2)
+                a[j] = rg[i % kRing][j];
             else
                 a[j] = *reinterpret_cast<const f16x8*>(arow + kb * 128 + 32 * j);
         }
@@ -522,6 +543,16 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
                     for (int e = 0; e < 4; ++e) acc[t][e] = __builtin_fmaf(s, part[e], acc[t][e]);
                 }
             }
+        }
+        if (AM == 2 && i + kRing < NB) {
+            // refill the slot block i has just consumed with block i + 3's rows
+            __builtin_amdgcn_sched_barrier(0);
+            const int ii = i + kRing;
+            int kn = wave + (ii < nb ? ii : (nb > 0 ? nb - 1 : 0)) * nwaves;
+            kn = kn < nfull ? kn : nfull - 1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                rg[i % kRing][j] = *reinterpret_cast<const f16x8*>(arow + kn * 128 + 32 * j);
         }
         // keep block i's work in its own scheduling region: blocks then wait
         // only for their own loads, in arrival order

@@ -36,13 +36,19 @@ __global__ __launch_bounds__(256) void add_rmsnorm_k(const void* __restrict__ xv
     };
     // a thread's values stay in registers when they fit (one global pass)
     const bool regs = dim <= kRegPer * nt;
-    float vr[kRegPer];
+    float vr[kRegPer], wr[kRegPer];
     float acc = 0.0f;
     if (regs) {
+        // every load unconditional (index clamped into the row; values past
+        // dim are never used), so all of them go out before the first wait --
+        // a guarded load becomes a branch with its own wait, one round trip
+        // per value.  w is loaded here too, ahead of the reduction.
 #pragma unroll
         for (int j = 0; j < kRegPer; ++j) {
             const int i = tid + j * nt;
-            vr[j] = i < dim ? ld(xv, base + i, XF) + ld(dv, base + i, DF) : 0.0f;
+            const int ic = i < dim ? i : dim - 1;
+            vr[j] = ld(xv, base + ic, XF) + ld(dv, base + ic, DF);
+            wr[j] = ld(wv, ic, WF);
         }
 #pragma unroll
         for (int j = 0; j < kRegPer; ++j) {
@@ -88,7 +94,7 @@ __global__ __launch_bounds__(256) void add_rmsnorm_k(const void* __restrict__ xv
         for (int j = 0; j < kRegPer; ++j) {
             const int i = tid + j * nt;
             if (i < dim) {
-                float y = vr[j] * inv * ld(wv, i, WF);
+                float y = vr[j] * inv * wr[j];
                 asm volatile("" : "+v"(y));
                 h[base + i] = bitcast<uint16_t>((f16)y);
             }
