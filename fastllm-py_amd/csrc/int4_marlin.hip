@@ -453,8 +453,21 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
         for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
         if (lane == 0) npart[wave] = ss;
         lds_barrier();
+        // the partials in wave order: four 16-byte reads (the launch gives
+        // npart 64 floats, so all 16 slots are in the allocation), slots of
+        // absent waves masked -- not one dependent LDS read per wave
+        float pw[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 f = reinterpret_cast<const float4*>(npart)[q];
+            pw[4 * q] = f.x;
+            pw[4 * q + 1] = f.y;
+            pw[4 * q + 2] = f.z;
+            pw[4 * q + 3] = f.w;
+        }
         float tot = 0.0f;
-        for (int w = 0; w < nwaves; ++w) tot += npart[w];
+#pragma unroll
+        for (int w = 0; w < 16; ++w) tot += w < nwaves ? pw[w] : 0.0f;
         const float inv = (float)(1.0 / sqrt((double)tot / (double)K + (double)nrm.eps));
         uint32_t hv[NB];
 #pragma unroll
