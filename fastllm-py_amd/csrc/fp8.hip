@@ -631,6 +631,12 @@ constexpr size_t kFp8LdsCap = 96 * 1024;
 //   * A trailing 64-wide block is a 128-k block whose second half is read as
 //     zeros (source offsets past the buffer end), activations and codes both.
 constexpr int kF8BM = 64, kF8BN = 128, kF8MinM = 64;
+// n-tiles per wave and waves per workgroup: one tile each for eight waves.
+// Two tiles for four waves (half the LDS reads of activations per block)
+// measured slower at M = 512: 26.7 / 65.0 / 132.4 us, with half the waves
+// per SIMD to hide the LDS and conversion latencies.
+constexpr int kF8NTW = 1, kF8Waves = 8 / kF8NTW;
+constexpr int kF8AF = 16 / kF8Waves;               // A fragments each wave copies per block
 constexpr int kF8Ahead = 1, kF8Stages = kF8Ahead + 1;
 constexpr int kF8StA = 0, kF8StB = 16384, kF8Stage = kF8StB + 16384;
 constexpr size_t kF8Lds = (size_t)kF8Stages * kF8Stage;
@@ -642,8 +648,8 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
                                                      const uint16_t* __restrict__ bias,
                                                      uint16_t* __restrict__ C, int M, int N, int K,
                                                      int nks) {
-    constexpr int D = kF8Ahead, NS = kF8Stages;
-    constexpr int LPB = 2 + 2;  // copies per block and wave: 2 A fragments, its tile's 2 halves
+    constexpr int D = kF8Ahead, NS = kF8Stages, NTW = kF8NTW, AF = kF8AF;
+    constexpr int LPB = AF + 2 * NTW;  // copies per block and wave: A fragments, 2 halves per tile
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -664,53 +670,54 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
     // per-lane source offsets; a piece at k >= K (the second half of a
     // trailing 64-wide block) points past the buffer, and the copy reads zeros
     constexpr uint32_t kOut = 0x80000000u;
-    uint32_t ao[2], bo[1][2];
-    int ak[2], bk[1];
+    uint32_t ao[AF], bo[NTW][2];
+    int ak[AF], bk[NTW];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int f = wave * 2 + i;  // fragment f = 4 m-tile + step
+    for (int i = 0; i < AF; ++i) {
+        const int f = wave * AF + i;  // fragment f = 4 m-tile + step
         int m = m0 + 16 * (f >> 2) + col;
         m = m < M ? m : M - 1;
         ak[i] = 32 * (f & 3) + 8 * kq;
         ao[i] = 2u * ((uint32_t)m * K + ak[i]);
     }
-    {
-        int n = (nt_base + wave) * 16 + col;
-        n = n < N ? n : N - 1;
-        bk[0] = 16 * kq;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) bo[0][h] = (uint32_t)n * K + 64 * h + 16 * kq;
+    for (int t = 0; t < NTW; ++t) {
+        int n = (nt_base + wave * NTW + t) * 16 + col;
+        n = n < N ? n : N - 1;
+        bk[t] = 16 * kq;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) bo[t][h] = (uint32_t)n * K + 64 * h + 16 * kq;
     }
     auto issue = [&](int kb, int slot) {
         kb = kb < nkb ? kb : nkb - 1;
         unsigned char* st = smem + (size_t)slot * kF8Stage;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < AF; ++i)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rA, (lptr_t)(st + kF8StA + (wave * 2 + i) * 1024), 16,
+                rA, (lptr_t)(st + kF8StA + (wave * AF + i) * 1024), 16,
                 kb * 128 + ak[i] < K ? ao[i] + kb * 256 : kOut, 0, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 1; ++i)
+        for (int i = 0; i < NTW; ++i)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rW, (lptr_t)(st + kF8StB + (wave + i) * 2048 + h * 1024), 16,
+                    rW, (lptr_t)(st + kF8StB + (wave * NTW + i) * 2048 + h * 1024), 16,
                     kb * 128 + 64 * h + bk[i] < K ? bo[i][h] + kb * 128 : kOut, 0, 0, 0);
     };
     // block-scale rows of this wave's two n-tiles (a 16-row tile lies in one band)
-    const float* srow[1];
+    const float* srow[NTW];
 #pragma unroll
-    for (int t = 0; t < 1; ++t) {
-        int nt = nt_base + wave + t;
+    for (int t = 0; t < NTW; ++t) {
+        int nt = nt_base + wave * NTW + t;
         nt = nt < ntiles ? nt : ntiles - 1;
         srow[t] = Sc + (size_t)((nt * 16) >> 7) * nks;
     }
 
-    f32x4 acc[4][1];
+    f32x4 acc[4][NTW];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-        for (int t = 0; t < 1; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < NTW; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(d, d);
 
@@ -724,11 +731,11 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
             asm volatile("s_barrier" ::: "memory");
             issue(kb + D, (u + D) % NS);
             const unsigned char* st = smem + (size_t)u * kF8Stage;
-            f32x4 part[4][1];
+            f32x4 part[4][NTW];
 #pragma unroll
             for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-                for (int t = 0; t < 1; ++t) part[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                for (int t = 0; t < NTW; ++t) part[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 u32x4 a[4];
@@ -736,9 +743,9 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
                 for (int mt = 0; mt < 4; ++mt)
                     a[mt] = *reinterpret_cast<const u32x4*>(st + kF8StA + (mt * 4 + j) * 1024 + lane * 16);
 #pragma unroll
-                for (int t = 0; t < 1; ++t) {
+                for (int t = 0; t < NTW; ++t) {
                     const uint2 w8 = *reinterpret_cast<const uint2*>(
-                        st + kF8StB + (wave + t) * 2048 + (j >> 1) * 1024 + 256 * (2 * (j & 1) + (kq >> 1)) +
+                        st + kF8StB + (wave * NTW + t) * 2048 + (j >> 1) * 1024 + 256 * (2 * (j & 1) + (kq >> 1)) +
                         boff);
                     const u32x4 b = fp8x8_to_16<BF16>(w8.x, w8.y);
 #pragma unroll
@@ -746,7 +753,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
                 }
             }
 #pragma unroll
-            for (int t = 0; t < 1; ++t) {
+            for (int t = 0; t < NTW; ++t) {
                 const float s = live ? srow[t][kb < nkb ? kb : nkb - 1] : 0.0f;
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
@@ -758,8 +765,8 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
     wait_vmcnt<0>();  // no LDS copy may still be in flight when the workgroup ends
 
 #pragma unroll
-    for (int t = 0; t < 1; ++t) {
-        const int n = (nt_base + wave + t) * 16 + col;
+    for (int t = 0; t < NTW; ++t) {
+        const int n = (nt_base + wave * NTW + t) * 16 + col;
         if (n >= N) continue;
         const float bv = bias ? act_to_f32<BF16>(bias[n]) : 0.0f;
 #pragma unroll
@@ -826,7 +833,7 @@ hipError_t fp8_gemm(const uint16_t* A, const uint8_t* W, const float* Sc, const 
     if (!INLINE && M > kF8MinM && K % 64 == 0 && (size_t)N * K < (1ull << 31) &&
         (size_t)M * K * 2 < (1ull << 31)) {
         const int tiles = ((N + kF8BN - 1) / kF8BN) * ((M + kF8BM - 1) / kF8BM);
-        hipLaunchKernelGGL((fp8_gemm_mfma<BF16>), dim3(tiles), dim3(512), kF8Lds, st, A, W, Sc, bias, C, M,
+        hipLaunchKernelGGL((fp8_gemm_mfma<BF16>), dim3(tiles), dim3(64 * kF8Waves), kF8Lds, st, A, W, Sc, bias, C, M,
                            N, K, nks);
         return hipGetLastError();
     }
