@@ -47,3 +47,12 @@ static inline int fl_current_device_cu_count() {
 static inline bool fl_aligned(const void* p, size_t a) {
     return ((uintptr_t)p % a) == 0;
 }
+
+// True when the byte ranges [a, a + na) and [b, b + nb) intersect.
+static inline bool fl_overlap(const void* a, size_t na, const void* b, size_t nb) {
+    const uintptr_t pa = (uintptr_t)a, pb = (uintptr_t)b;
+    return pa < pb + nb && pb < pa + na;
+}
+
+// LDS per workgroup on gfx950 (160 KB).
+constexpr size_t kMaxLds = 160 * 1024;

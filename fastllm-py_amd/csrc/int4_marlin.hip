@@ -1079,10 +1079,20 @@ bool int4_marlin_abi_gemm(const void* a, const uint32_t* q, const void* scales,
     const bool g32 = group_size == 32;
     const f16* A = static_cast<const f16*>(a);
     f16* Cp = static_cast<f16*>(c);
-    if (M > kGemmMfmaMinM && K % 128 == 0)
-        return report(launch_gemm_mfma(A, q, static_cast<const uint16_t*>(scales), zeros, Cp, M, N,
-                                       K, g32, stream),
-                      "FastllmCudaMarlinHalfInt4Gemm");
+    if (M > kGemmMfmaMinM && K % 128 == 0 && (size_t)N * K / 2 < (1ull << 31)) {
+        // the kernel addresses A through a 32-bit buffer range: launch rows in
+        // chunks (multiples of its 64-row tile) of fewer than 2^31 bytes
+        const size_t rows_cap = ((1ull << 31) - 1) / ((size_t)K * 2);
+        const int mchunk = rows_cap >= (size_t)M ? M : (int)(rows_cap / kGemmBM * kGemmBM);
+        for (int m0 = 0; m0 < M; m0 += mchunk) {
+            const int Mc = (M - m0) < mchunk ? (M - m0) : mchunk;
+            if (!report(launch_gemm_mfma(A + (size_t)m0 * K, q, static_cast<const uint16_t*>(scales),
+                                         zeros, Cp + (size_t)m0 * N, Mc, N, K, g32, stream),
+                        "FastllmCudaMarlinHalfInt4Gemm"))
+                return false;
+        }
+        return true;
+    }
     if (M > 16)
         return int4_gemm_large_m(A, q, static_cast<const f16*>(scales), zeros, Cp, M, N, K, g32,
                                  stream);
@@ -1107,6 +1117,13 @@ hipError_t launch_gemv_swiglu(const f16* A, const uint32_t* Wq, const uint16_t* 
     const size_t red = (size_t)waves * 2 * 256 * sizeof(float);
     const size_t own = (size_t)waves * NB * 1024;
     const dim3 grid(N / 32), block(64 * waves);
+    if (own + red > kMaxLds) return hipErrorInvalidValue;
+    if constexpr (NB > 4) {  // LDS activation copies only (register activations spill)
+        if (M > 4) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 0, true>), grid, block, own + red, stream, A, Wq, S,
+                           Z, H, M, N, K);
+        return hipGetLastError();
+    }
     if (M <= 4)
         hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 0, true>), grid, block, own + red, stream, A, Wq, S,
                            Z, H, M, N, K);
@@ -1122,16 +1139,26 @@ hipError_t dispatch_swiglu(const f16* A, const uint32_t* Wq, const uint16_t* S, 
     // the decode config of this shape, with NB <= 4 (register activations);
     // above M = 4 sixteen waves (NB = 2 at K = 4096): the NB = 4 register-A
     // instantiation of this kernel needs more than 128 VGPRs and spills
+    // Up to M = 4 (LDS activation copies) six blocks per wave fit the
+    // registers at 16 waves, so K <= 12288 (16 x 6 x 128); above M = 4 four
+    // blocks per wave (K <= 8192).  Larger K is refused (rc 1): the caller
+    // runs the plain GEMV and the standalone SwiGLU.
     const int nfull = K / 128 > 0 ? K / 128 : 1;
+    const int cap = (M <= 4 && !G32) ? 6 : 4;
     int waves = (N >= 16384 && M <= 4) ? 8 : 16;
     while (waves > 1 && nfull < waves) waves /= 2;
     while ((nfull + waves - 1) / waves > 4 && waves < 16) waves *= 2;
-    const int nb = (nfull + waves - 1) / waves;
+    int nb = (nfull + waves - 1) / waves;
+    if (nb > 4 && nb <= cap) nb = 6;
     switch (nb) {
         case 1: return launch_gemv_swiglu<1, G32>(A, Wq, S, Z, H, M, N, K, waves, stream);
         case 2: return launch_gemv_swiglu<2, G32>(A, Wq, S, Z, H, M, N, K, waves, stream);
         case 3: return launch_gemv_swiglu<3, G32>(A, Wq, S, Z, H, M, N, K, waves, stream);
         case 4: return launch_gemv_swiglu<4, G32>(A, Wq, S, Z, H, M, N, K, waves, stream);
+        case 6:
+            if constexpr (!G32)
+                if (M <= 4) return launch_gemv_swiglu<6, G32>(A, Wq, S, Z, H, M, N, K, waves, stream);
+            return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }
@@ -1168,10 +1195,17 @@ __global__ void marlin_to_moe_tile_k(const uint32_t* __restrict__ qw, const uint
     }
 }
 
+// LDS bytes of int4_gemv_norm: a 1 KB slot per block of every wave, the
+// cross-wave reduction area and the per-wave norm partials.
+constexpr size_t gemv_norm_lds(int T, int NB, int waves) {
+    return (size_t)waves * NB * 1024 + (size_t)waves * T * 1024 + 256;
+}
+
 template <int T, int NB, bool G32, bool SWI>
 hipError_t launch_gemv_norm(const NormArgs& nrm, const uint32_t* Wq, const uint16_t* S,
                             const uint32_t* Z, f16* C, int N, int K, int waves, hipStream_t st) {
-    const size_t lds = (size_t)waves * NB * 1024 + (size_t)waves * T * 1024 + 256;
+    const size_t lds = gemv_norm_lds(T, NB, waves);
+    if (lds > kMaxLds) return hipErrorInvalidValue;
     const dim3 grid(SWI ? N / 32 : N / (16 * T)), block(64 * waves);
     hipLaunchKernelGGL((int4_gemv_norm<T, NB, G32, SWI>), grid, block, lds, st, nrm, Wq, S, Z, C, N, K);
     return hipGetLastError();
@@ -1211,6 +1245,15 @@ hipError_t gemv_norm(const NormArgs& nrm, const uint32_t* Wq, const uint16_t* S,
     }
     int nb = nb_bucket((nfull + waves - 1) / waves);
     if (nb > cap) return hipErrorInvalidValue;
+    // two tiles per workgroup need 1 KB more reduction space per wave; where
+    // that overflows the LDS (16 waves of 8 blocks: K > 12288) the plain GEMV
+    // takes one tile, and the SwiGLU pair is refused (the caller runs the
+    // standalone norm and the unfused kernels instead)
+    if (tiles == 2 && gemv_norm_lds(2, nb, waves) > kMaxLds) {
+        if (swi) return hipErrorInvalidValue;
+        tiles = 1;
+    }
+    if (gemv_norm_lds(tiles, nb, waves) > kMaxLds) return hipErrorInvalidValue;
     if (swi) return dispatch_gemv_norm<2, G32, true>(nb, nrm, Wq, S, Z, C, N, K, waves, st);
     if (tiles == 2) return dispatch_gemv_norm<2, G32, false>(nb, nrm, Wq, S, Z, C, N, K, waves, st);
     return dispatch_gemv_norm<1, G32, false>(nb, nrm, Wq, S, Z, C, N, K, waves, st);
@@ -1301,6 +1344,7 @@ int fastllm_int4_gemm_swiglu(const void* a, const uint32_t* b_q_weight, const vo
         group_size == 32
             ? dispatch_swiglu<true>(A, b_q_weight, S, b_zeros, H, size_m, size_n, size_k, (hipStream_t)stream)
             : dispatch_swiglu<false>(A, b_q_weight, S, b_zeros, H, size_m, size_n, size_k, (hipStream_t)stream);
+    if (e == hipErrorInvalidValue) return 1;  // shape beyond the fused kernel (see dispatch_swiglu)
     return report(e, "fastllm_int4_gemm_swiglu") ? 0 : 2;
 }
 
@@ -1330,6 +1374,11 @@ int fastllm_int4_gemm_add_rmsnorm(const float* x, const void* delta, const void*
     if (group_size != 32 && group_size != 128) return 1;
     if (!fl_aligned(x, 16) || !fl_aligned(delta, 16) || !fl_aligned(norm_w, 16) || !fl_aligned(xnew, 16) ||
         !fl_aligned(b_q_weight, 16))
+        return 1;
+    // workgroup 0 stores xnew while later workgroups still read x and delta:
+    // an in-place update would feed them x + 2 delta
+    if (fl_overlap(xnew, (size_t)size_k * 4, x, (size_t)size_k * 4) ||
+        fl_overlap(xnew, (size_t)size_k * 4, delta, (size_t)size_k * 2))
         return 1;
     if (!fl_current_device_supported()) return 2;
     const NormArgs nrm{x, static_cast<const uint16_t*>(delta), static_cast<const uint16_t*>(norm_w), xnew,

@@ -111,14 +111,54 @@ FL_DEV void tile_block_mma(f32x4& acc, const u32x4 (&a)[4], u32x4 w, uint16_t s1
     }
 }
 
+// One 128-k block of one 16-row tile in quantize_int4_group's format
+// (quantizer.py:97-129): fp32 scale s and fp32 group minimum mn, w = q*s + mn.
+// Groups of 128 or more: s * sum(x*q) + mn * sum(x), both sums on the matrix
+// cores (the second against a B operand of ones), scaled in fp32.  Groups of
+// 32/64: w formed in fp16 by one fused multiply-add before the MFMA.
+template <bool G128>
+FL_DEV void a_block_mma(f32x4& acc, const u32x4 (&a)[4], u32x4 w, float s, float mn, float live) {
+    const uint32_t zc = rm_zero_consts(0);
+    f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (G128) {
+        f32x4 xsum = f32x4{0.f, 0.f, 0.f, 0.f};
+        const u32x4 ones = u32x4{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            part = mfma_f16(bitcast<f16x8>(a[j]), bitcast<f16x8>(rm_dequant(w[j], zc, kRmMagic)), part);
+            xsum = mfma_f16(bitcast<f16x8>(a[j]), bitcast<f16x8>(ones), xsum);
+        }
+        const float ss = s * live, mm = mn * live;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(mm, xsum[e], __builtin_fmaf(ss, part[e], acc[e]));
+    } else {
+        const f16 s16 = (f16)s, m16 = (f16)mn;
+        const f16x2 ss{s16, s16}, mm{m16, m16};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x4 q = rm_dequant(w[j], zc, kRmMagic);
+            u32x4 v;
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+                v[h] = bitcast<uint32_t>(__builtin_elementwise_fma(bitcast<f16x2>(q[h]), ss, mm));
+            part = mfma_f16(bitcast<f16x8>(a[j]), bitcast<f16x8>(v), part);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(live, part[e], acc[e]);
+    }
+}
+
 // ------------------------------------------------------ row-major INT4 GEMV
 // Y[M, N] = X[M, K] @ dequant(W)^T, M <= 16, X/Y fp32 or fp16 (XF32/YF32).
-// K % 128 == 0; group gs in {32, 64, 128}.
-template <int NB, bool G128, bool XF32, bool YF32>
+// K % 128 == 0.  AFMT false: moe_int4.py's format, fp16 scale and zero,
+// group gs in {32, 64, 128}.  AFMT true: quantize_int4_group's format
+// (same nibbles), fp32 scale and minimum, gs in {32, 64} or a multiple of
+// 128 (G128 then means "one group per 128-k block").
+template <int NB, bool G128, bool XF32, bool YF32, bool AFMT>
 __global__ __launch_bounds__(1024) void rm_gemv_nb(const void* __restrict__ Xv,
                                                    const uint8_t* __restrict__ Wq,
-                                                   const uint16_t* __restrict__ S,
-                                                   const uint16_t* __restrict__ Z, void* __restrict__ Yv,
+                                                   const void* __restrict__ Sv,
+                                                   const void* __restrict__ Zv, void* __restrict__ Yv,
                                                    int M, int N, int K, int gs) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int nwaves = blockDim.x >> 6;
@@ -160,14 +200,17 @@ __global__ __launch_bounds__(1024) void rm_gemv_nb(const void* __restrict__ Xv,
     const uint8_t* wrow = Wq + (size_t)nc * (K / 2);
     const int nb = wave < nfull ? (nfull - wave + nwaves - 1) / nwaves : 0;
 
+    using P = typename std::conditional<AFMT, float, uint16_t>::type;
+    const P* __restrict__ S = static_cast<const P*>(Sv);
+    const P* __restrict__ Z = static_cast<const P*>(Zv);
     u32x4 wv[NB];
-    uint16_t sv[NB], zv[NB];
+    P sv[NB], zv[NB];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
         kb = kb < nfull ? kb : nfull - 1;
         wv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow + kb * 64 + 16 * kq));
-        const int g = (kb * 128 + 32 * kq) / gs;
+        const int g = (kb * 128 + (G128 ? 0 : 32 * kq)) / gs;
         sv[i] = S[(size_t)nc * G + g];
         zv[i] = Z[(size_t)nc * G + g];
     }
@@ -184,7 +227,10 @@ __global__ __launch_bounds__(1024) void rm_gemv_nb(const void* __restrict__ Xv,
         u32x4 a[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const u32x4*>(arow + kb * 128 + 8 * j);
-        rm_block_mma<G128>(acc[0], a, wv[i], sv[i], zv[i], live ? 1.0f : 0.0f);
+        if constexpr (AFMT)
+            a_block_mma<G128>(acc[0], a, wv[i], sv[i], zv[i], live ? 1.0f : 0.0f);
+        else
+            rm_block_mma<G128>(acc[0], a, wv[i], sv[i], zv[i], live ? 1.0f : 0.0f);
         __builtin_amdgcn_sched_barrier(0);
     }
 
@@ -1518,26 +1564,66 @@ int finish(const char* what) {
     return 0;
 }
 
-template <int NB, bool G128, bool XF32, bool YF32>
-void launch_rm(const void* X, const uint8_t* W, const uint16_t* S, const uint16_t* Z, void* Y,
-               int M, int N, int K, int gs, int waves, hipStream_t st) {
+template <int NB, bool G128, bool XF32, bool YF32, bool AFMT>
+void launch_rm(const void* X, const uint8_t* W, const void* S, const void* Z, void* Y, int M,
+               int N, int K, int gs, int waves, hipStream_t st) {
     const size_t lds = (((size_t)M * (K + 8) * 2 + 15) & ~(size_t)15) + (size_t)waves * 1024;
-    hipLaunchKernelGGL((rm_gemv_nb<NB, G128, XF32, YF32>), dim3((N + 15) / 16), dim3(64 * waves),
-                       lds, st, X, W, S, Z, Y, M, N, K, gs);
+    hipLaunchKernelGGL((rm_gemv_nb<NB, G128, XF32, YF32, AFMT>), dim3((N + 15) / 16),
+                       dim3(64 * waves), lds, st, X, W, S, Z, Y, M, N, K, gs);
 }
 
-template <bool G128, bool XF32, bool YF32>
-void rm_dispatch(int nb, const void* X, const uint8_t* W, const uint16_t* S, const uint16_t* Z,
-                 void* Y, int M, int N, int K, int gs, int waves, hipStream_t st) {
+template <bool G128, bool XF32, bool YF32, bool AFMT>
+void rm_dispatch(int nb, const void* X, const uint8_t* W, const void* S, const void* Z, void* Y,
+                 int M, int N, int K, int gs, int waves, hipStream_t st) {
     switch (nb) {
-        case 1: launch_rm<1, G128, XF32, YF32>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
-        case 2: launch_rm<2, G128, XF32, YF32>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
-        case 3: launch_rm<3, G128, XF32, YF32>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
-        case 4: launch_rm<4, G128, XF32, YF32>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
-        case 5: launch_rm<5, G128, XF32, YF32>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
-        case 6: launch_rm<6, G128, XF32, YF32>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
-        default: launch_rm<8, G128, XF32, YF32>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
+        case 1: launch_rm<1, G128, XF32, YF32, AFMT>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
+        case 2: launch_rm<2, G128, XF32, YF32, AFMT>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
+        case 3: launch_rm<3, G128, XF32, YF32, AFMT>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
+        case 4: launch_rm<4, G128, XF32, YF32, AFMT>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
+        case 5: launch_rm<5, G128, XF32, YF32, AFMT>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
+        case 6: launch_rm<6, G128, XF32, YF32, AFMT>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
+        default: launch_rm<8, G128, XF32, YF32, AFMT>(X, W, S, Z, Y, M, N, K, gs, waves, st); break;
     }
+}
+
+// Shared body of the two row-major GEMV entries: M in chunks whose fp16 rows
+// fit the LDS staging area, one launch per chunk.
+template <bool AFMT>
+int rm_gemv_entry(const char* what, const void* x, int x_fp32, const uint8_t* qweight,
+                  const void* scales, const void* zeros, void* y, int y_fp32, int M, int out_f,
+                  int in_f, int group_size, bool g128, void* stream) {
+    const int nfull = in_f / 128;
+    int waves = 16;
+    while (waves > 1 && nfull < waves) waves /= 2;
+    while ((nfull + waves - 1) / waves > 8 && waves < 16) waves *= 2;
+    if ((nfull + waves - 1) / waves > 8) return 1;  // in_f > 16384
+    const int need = (nfull + waves - 1) / waves;
+    const int nb = need <= 6 ? need : 8;
+    hipStream_t st = (hipStream_t)stream;
+    const size_t xe = x_fp32 ? 4 : 2, ye = y_fp32 ? 4 : 2;
+    int mcap = (int)((96 * 1024) / ((size_t)(in_f + 8) * 2));
+    mcap = mcap > 16 ? 16 : (mcap < 1 ? 1 : mcap);
+    for (int m0 = 0; m0 < M; m0 += mcap) {
+        const int Mc = (M - m0) < mcap ? (M - m0) : mcap;
+        const void* xm = static_cast<const char*>(x) + (size_t)m0 * in_f * xe;
+        void* ym = static_cast<char*>(y) + (size_t)m0 * out_f * ye;
+#define RM_CASE(G, XF, YF)                                                                       \
+    if (g128 == G && (x_fp32 != 0) == XF && (y_fp32 != 0) == YF)                                 \
+        rm_dispatch<G, XF, YF, AFMT>(nb, xm, qweight, scales, zeros, ym, Mc, out_f, in_f,         \
+                                     group_size, waves, st);
+        RM_CASE(true, true, true)
+        RM_CASE(true, true, false)
+        RM_CASE(true, false, true)
+        RM_CASE(true, false, false)
+        RM_CASE(false, true, true)
+        RM_CASE(false, true, false)
+        RM_CASE(false, false, true)
+        RM_CASE(false, false, false)
+#undef RM_CASE
+        const int rc = finish(what);
+        if (rc) return rc;
+    }
+    return 0;
 }
 
 // Launch plan of the fused MoE for one problem shape (host side).
@@ -1663,40 +1749,20 @@ int fastllm_int4_rowmajor_gemv(const void* x, int x_fp32, const uint8_t* qweight
     if (in_f % 128 || (group_size != 32 && group_size != 64 && group_size != 128)) return 1;
     if (!fl_aligned(x, 16) || !fl_aligned(qweight, 16)) return 1;
     if (!fl_current_device_supported()) return 2;
-    const int nfull = in_f / 128;
-    int waves = 16;
-    while (waves > 1 && nfull < waves) waves /= 2;
-    while ((nfull + waves - 1) / waves > 8 && waves < 16) waves *= 2;
-    if ((nfull + waves - 1) / waves > 8) return 1;  // in_f > 16384
-    const int need = (nfull + waves - 1) / waves;
-    const int nb = need <= 6 ? need : 8;
-    const bool g128 = group_size == 128;
-    hipStream_t st = (hipStream_t)stream;
-    const size_t xe = x_fp32 ? 4 : 2, ye = y_fp32 ? 4 : 2;
-    int mcap = (int)((96 * 1024) / ((size_t)(in_f + 8) * 2));
-    mcap = mcap > 16 ? 16 : (mcap < 1 ? 1 : mcap);
-    for (int m0 = 0; m0 < M; m0 += mcap) {
-        const int Mc = (M - m0) < mcap ? (M - m0) : mcap;
-        const void* xm = static_cast<const char*>(x) + (size_t)m0 * in_f * xe;
-        void* ym = static_cast<char*>(y) + (size_t)m0 * out_f * ye;
-        const uint16_t* S = static_cast<const uint16_t*>(scales);
-        const uint16_t* Z = static_cast<const uint16_t*>(zeros);
-#define RM_CASE(G, XF, YF)                                                                       \
-    if (g128 == G && (x_fp32 != 0) == XF && (y_fp32 != 0) == YF)                                 \
-        rm_dispatch<G, XF, YF>(nb, xm, qweight, S, Z, ym, Mc, out_f, in_f, group_size, waves, st);
-        RM_CASE(true, true, true)
-        RM_CASE(true, true, false)
-        RM_CASE(true, false, true)
-        RM_CASE(true, false, false)
-        RM_CASE(false, true, true)
-        RM_CASE(false, true, false)
-        RM_CASE(false, false, true)
-        RM_CASE(false, false, false)
-#undef RM_CASE
-        const int rc = finish("fastllm_int4_rowmajor_gemv");
-        if (rc) return rc;
-    }
-    return 0;
+    return rm_gemv_entry<false>("fastllm_int4_rowmajor_gemv", x, x_fp32, qweight, scales, zeros, y,
+                                y_fp32, M, out_f, in_f, group_size, group_size == 128, stream);
+}
+
+int fastllm_int4_group_gemv(const void* x, int x_fp32, const uint8_t* data, const float* scales,
+                            const float* zeros, void* y, int y_fp32, int M, int out_f, int in_f,
+                            int group_size, void* stream) {
+    if (!x || !data || !scales || !zeros || !y || M <= 0 || out_f <= 0 || in_f <= 0) return 1;
+    if (in_f % 128 || group_size <= 0 || in_f % group_size) return 1;
+    if (group_size != 32 && group_size != 64 && group_size % 128) return 1;
+    if (!fl_aligned(x, 16) || !fl_aligned(data, 16)) return 1;
+    if (!fl_current_device_supported()) return 2;
+    return rm_gemv_entry<true>("fastllm_int4_group_gemv", x, x_fp32, data, scales, zeros, y, y_fp32,
+                               M, out_f, in_f, group_size, group_size % 128 == 0, stream);
 }
 
 int fastllm_gate_matvec(const float* x, const void* gate_w, const void* shared_gate_w,

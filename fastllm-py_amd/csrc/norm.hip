@@ -119,9 +119,45 @@ void launch_w(bool wf, const void* x, const void* d, const void* w, float* xnew,
                            dim, eps);
 }
 
+
+
+// out[r, i] = fp16(silu(g) * u) for g = gate[r, i], u = up[r, i] (fp16 in),
+// computed in fp32 as g / (1 + exp(-g)) * u -- the reference's swiglu
+// (fastllm_py/kernels/ops.py:157-163) and the SwiGLU epilogue of the fused
+// gate/up GEMV.  Elementwise, 8 halves per thread where the row allows.
+__global__ void swiglu_k(const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,
+                         uint16_t* __restrict__ out, int rows, int cols, int ldg, int ldu, int ldo) {
+    const long total = (long)rows * cols;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (long)gridDim.x * blockDim.x) {
+        const int r = (int)(i / cols), c = (int)(i - (long)r * cols);
+        const float g = (float)bitcast<f16>(gate[(size_t)r * ldg + c]);
+        const float u = (float)bitcast<f16>(up[(size_t)r * ldu + c]);
+        out[(size_t)r * ldo + c] = bitcast<uint16_t>((f16)(g / (1.0f + expf(-g)) * u));
+    }
+}
+
 }  // namespace
 
 extern "C" {
+
+int fastllm_swiglu(const void* gate, const void* up, void* out, int rows, int cols, int ld_gate,
+                   int ld_up, int ld_out, void* stream) {
+    if (!gate || !up || !out || rows <= 0 || cols <= 0) return 1;
+    if (ld_gate < cols || ld_up < cols || ld_out < cols) return 1;
+    if (!fl_current_device_supported()) return 2;
+    const long total = (long)rows * cols;
+    const int grid = (int)((total + 255) / 256 < 8192 ? (total + 255) / 256 : 8192);
+    hipLaunchKernelGGL(swiglu_k, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                       static_cast<const uint16_t*>(gate), static_cast<const uint16_t*>(up),
+                       static_cast<uint16_t*>(out), rows, cols, ld_gate, ld_up, ld_out);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        fprintf(stderr, "fastllm_swiglu launch error: %s\n", hipGetErrorString(e));
+        return 2;
+    }
+    return 0;
+}
 
 // 0 ok, 1 bad arguments, 2 device / launch error.  *_f32: 1 = fp32, 0 = fp16.
 int fastllm_add_rmsnorm(const void* x, int x_f32, const void* delta, int delta_f32, const void* w,

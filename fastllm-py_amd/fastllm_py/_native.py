@@ -30,6 +30,7 @@ SIGNATURES: dict[str, tuple] = {
     "fastllm_int4_gemm_config": (_B, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
     "fastllm_int4_gemm_swiglu": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "fastllm_add_rmsnorm": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _I, _I, _F, _P]),
+    "fastllm_swiglu": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "fastllm_marlin_to_moe_tile": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "fastllm_int4_gemm_add_rmsnorm": (_I, [_P, _P, _P, _F, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     # packers / unpackers
@@ -53,6 +54,7 @@ SIGNATURES: dict[str, tuple] = {
     "fastllm_fp8_b128x128_gemv": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     # row-major INT4 / router / fused MoE
     "fastllm_int4_rowmajor_gemv": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "fastllm_int4_group_gemv": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "fastllm_gate_matvec": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "fastllm_route_topk": (_I, [_P, _I, _I, _I, _I, _I, _F, _P, _I, _I, _P, _P, _P, _P, _P,
                                 _P, _P, _P, _P, _P, _P]),
@@ -156,6 +158,30 @@ def stream_handle(stream) -> int:
     if isinstance(stream, int):
         return stream
     return int(stream.cuda_stream)
+
+
+def check_out(buf, numel: int, dtypes, device, name: str = "out"):
+    """Validate a caller-supplied output buffer before its pointer goes to a
+    kernel: a contiguous device tensor of one of `dtypes`, on `device`, with
+    exactly `numel` elements.  Raises ValueError otherwise."""
+    t = torch()
+    if not isinstance(buf, t.Tensor):
+        raise ValueError(f"{name} must be a torch tensor")
+    if buf.dtype not in tuple(dtypes):
+        raise ValueError(f"{name} has dtype {buf.dtype}; expected one of {tuple(dtypes)}")
+    if not buf.is_cuda or (device is not None and buf.device != t.device(device)):
+        raise ValueError(f"{name} must live on {device}")
+    if not buf.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if buf.numel() != numel:
+        raise ValueError(f"{name} has {buf.numel()} elements; expected {numel}")
+
+
+def overlaps(a, b) -> bool:
+    """True when the device memory of tensors a and b intersects."""
+    pa, pb = a.data_ptr(), b.data_ptr()
+    na, nb = a.numel() * a.element_size(), b.numel() * b.element_size()
+    return pa < pb + nb and pb < pa + na
 
 
 def as_output(x, like_numpy: bool):

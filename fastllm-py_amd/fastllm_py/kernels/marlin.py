@@ -182,14 +182,23 @@ def gemm_swiglu(a_fp16, qweight, scales, zeros, size_n, size_k, out=None, stream
     a = a.reshape(-1, size_k).contiguous()
     size_m = a.shape[0]
     group_size = size_k // scales.shape[0]
+    if out is not None:
+        nat.check_out(out, size_m * (size_n // 2), (t.float16,), a.device)
     h = out if out is not None else t.empty((size_m, size_n // 2), dtype=t.float16, device=a.device)
     hs = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
     rc = nat.lib().fastllm_int4_gemm_swiglu(nat.ptr(a), nat.ptr(qweight), nat.ptr(scales),
                                             nat.ptr(zeros), nat.ptr(h), size_m, size_n, size_k,
                                             group_size, hs)
     if rc == 1:
-        raise ValueError(f"gemm_swiglu: unsupported shape M={size_m} N={size_n} K={size_k} "
-                         f"group={group_size}")
+        if size_m > 16 or size_n % 128 or size_k % 128 or group_size not in (32, 128):
+            raise ValueError(f"gemm_swiglu: unsupported shape M={size_m} N={size_n} K={size_k} "
+                             f"group={group_size}")
+        # K beyond the fused kernel's register/LDS budget: plain GEMV, then swiglu
+        gu = gemm_fast(a, qweight, scales, zeros, size_n, size_k, stream=hs,
+                       workspace=get_workspace(size_n))
+        inter = size_n // 2
+        from . import ops
+        return ops.swiglu(gu[:, :inter], gu[:, inter:], out=h, stream=hs)
     nat.check_rc(rc, "fastllm_int4_gemm_swiglu")
     return h
 
@@ -207,6 +216,13 @@ def gemm_add_rmsnorm(x, delta, norm_w, eps, qweight, scales, zeros, size_n, size
     dd = nat.to_device(delta, t.float16).reshape(1, size_k).contiguous()
     wd = nat.to_device(norm_w, t.float16).reshape(size_k).contiguous()
     n_out = size_n // 2 if swiglu else size_n
+    if out is not None:
+        nat.check_out(out, n_out, (t.float16,), xd.device, "out")
+    if xnew is not None:
+        nat.check_out(xnew, size_k, (t.float32,), xd.device, "xnew")
+        if nat.overlaps(xnew, xd) or nat.overlaps(xnew, dd):
+            raise ValueError("gemm_add_rmsnorm: xnew must not overlap x or delta (the kernel "
+                             "stores xnew while other workgroups still read them)")
     c = out if out is not None else t.empty((1, n_out), dtype=t.float16, device=xd.device)
     xn = xnew if xnew is not None else t.empty((1, size_k), dtype=t.float32, device=xd.device)
     group_size = size_k // scales.shape[0]
@@ -215,7 +231,20 @@ def gemm_add_rmsnorm(x, delta, norm_w, eps, qweight, scales, zeros, size_n, size
         nat.ptr(xd), nat.ptr(dd), nat.ptr(wd), float(eps), nat.ptr(xn), nat.ptr(qweight),
         nat.ptr(scales), nat.ptr(zeros), nat.ptr(c), size_n, size_k, group_size, int(bool(swiglu)), hs)
     if rc == 1:
-        raise ValueError(f"gemm_add_rmsnorm: unsupported shape N={size_n} K={size_k} group={group_size}")
+        if (size_k % 128 or size_n % 64 or (swiglu and size_n % 128)
+                or group_size not in (32, 128)):
+            raise ValueError(f"gemm_add_rmsnorm: unsupported shape N={size_n} K={size_k} "
+                             f"group={group_size}")
+        # the fused prologue does not fit this shape: standalone norm, then the projection
+        from . import ops
+        h = t.empty((1, size_k), dtype=t.float16, device=xd.device)
+        ops.add_rmsnorm(xd, dd, wd, eps, out=(xn, h), stream=hs)
+        if swiglu:
+            gemm_swiglu(h, qweight, scales, zeros, size_n, size_k, out=c, stream=hs)
+        else:
+            gemm_fast(h, qweight, scales, zeros, size_n, size_k, stream=hs,
+                      workspace=get_workspace(size_n), out=c)
+        return xn, c
     nat.check_rc(rc, "fastllm_int4_gemm_add_rmsnorm")
     return xn, c
 

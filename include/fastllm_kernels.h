@@ -89,6 +89,9 @@ bool fastllm_int4_gemm_config(const void *a, const uint32_t *b_q_weight,
  * [0, I) then up rows [I, 2 I) (I % 64 == 0, size_k % 128 == 0); writes
  * h[size_m, I] (fp16) = silu(g) * u from the fp16 g, u the plain GEMV would
  * store -- one launch instead of the GEMV and the swiglu kernel.
+ * Limits: size_k <= 8192 above size_m = 4 (and for group 32); size_k <= 12288
+ * up to size_m = 4 with group 128.  Beyond them it returns 1 and the caller
+ * runs the plain GEMV then fastllm_swiglu.
  * Returns 0, 1 for arguments the kernel cannot take, 2 for a device or
  * launch error.
  * Replaces: the gate_up GEMV + swiglu pair of the reference's decode MLP
@@ -112,6 +115,14 @@ int fastllm_add_rmsnorm(const void *x, int x_f32, const void *delta, int delta_f
                         const void *w, int w_f32, float *xnew, uint16_t *h, int rows,
                         int dim, float eps, void *stream);
 
+/* out[r, i] = fp16(silu(g) * u), g = gate[r * ld_gate + i],
+ * u = up[r * ld_up + i], computed in fp32 as g / (1 + exp(-g)) * u; fp16
+ * in and out, row strides in elements.  Returns 0, 1 for bad arguments,
+ * 2 for a device or launch error.
+ * Replaces: swiglu (fastllm_py/kernels/ops.py:144-163). */
+int fastllm_swiglu(const void *gate, const void *up, void *out, int rows, int cols,
+                   int ld_gate, int ld_up, int ld_out, void *stream);
+
 /* add_rmsnorm fused into the prologue of one decode row's Marlin GEMV (M = 1):
  * xnew = x + delta (fp32, stored), h = fp16(xnew * inv * norm_w) with
  * inv = 1/sqrt(sum(xnew^2)/size_k + eps), and c = h @ dequant(W)^T (fp16,
@@ -120,7 +131,11 @@ int fastllm_add_rmsnorm(const void *x, int x_f32, const void *delta, int delta_f
  * norm_w fp16, 16-byte aligned; size_k % 128 == 0.  h never leaves the chip:
  * every workgroup forms its own blocks of it while its weight loads are in
  * flight (the sum of squares is taken in a different order from the
- * standalone op, so h may differ from it in the last bit).  Returns 0, 1 for
+ * standalone op, so h may differ from it in the last bit).  xnew must not
+ * overlap x or delta: workgroup 0 stores it while other workgroups still read
+ * them (rc 1 otherwise).  Shapes whose per-wave LDS slots and reduction area
+ * exceed 160 KB (group 128, size_k > 12288 with swiglu) return 1; the caller
+ * then runs fastllm_add_rmsnorm and the unfused projection.  Returns 0, 1 for
  * arguments the kernel cannot take, 2 for a device or launch error.
  * Replaces: the add_rmsnorm launch before a projection plus that projection
  * (fastllm_py/graph_decode.py:818-826, 858-866); no single reference entry. */
@@ -302,6 +317,19 @@ int fastllm_int4_rowmajor_gemv(const void *x, int x_fp32, const uint8_t *qweight
                                const void *scales, const void *zeros, void *y,
                                int y_fp32, int M, int out_f, int in_f,
                                int group_size, void *stream);
+
+/* y[M, out_f] = x[M, in_f] @ dequant(W)^T for quantize_int4_group's format
+ * (fastllm_py/quantizer.py:97-129): data u8 [out_f, in_f/2], even column in
+ * the low nibble; scales and zeros (the group minimum) f32
+ * [out_f, in_f/group]; dequant(W) = q * scale + zero.  x fp32 (x_fp32 = 1) or
+ * fp16, y fp32 (y_fp32 = 1) or fp16.  in_f % 128 == 0, in_f <= 16384,
+ * group in {32, 64} or a multiple of 128 dividing in_f.  The reference has no
+ * GPU consumer of this format: its CPU path is dequantize_int4_group
+ * (quantizer.py:120-129) followed by a matmul. */
+int fastllm_int4_group_gemv(const void *x, int x_fp32, const uint8_t *data,
+                            const float *scales, const float *zeros, void *y,
+                            int y_fp32, int M, int out_f, int in_f,
+                            int group_size, void *stream);
 
 /* logits[T, E] = x[T, hidden] (f32) @ gate_w[E, hidden]^T (fp16), fp32
  * accumulate; with shared_gate_w (fp16 [hidden]) also shared_logit[T].

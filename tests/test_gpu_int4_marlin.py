@@ -72,15 +72,16 @@ SHAPES = [(1024, 512), (2048, 1408 // 64 * 64), (1408 // 64 * 64, 2048), (4096, 
           (192, 64)]
 
 
-@pytest.mark.parametrize("gs", [128, 32])
-@pytest.mark.parametrize("K,N", SHAPES)
+# (K, N, group) with K a multiple of the group (192 x 64 runs at group 32 only)
+SHAPE_CASES = [(K, N, gs) for K, N in SHAPES for gs in (128, 32) if K % gs == 0]
+
+
+@pytest.mark.parametrize("K,N,gs", SHAPE_CASES)
 @pytest.mark.parametrize("M", [1, 4, 8, 16])
 def test_gemm_parity(torch_gpu, M, K, N, gs):
     from fastllm_py.kernels import marlin
 
     torch = torch_gpu
-    if K % gs:
-        pytest.skip("K not a multiple of the group")
     rng = np.random.default_rng(1000 * M + K + N + gs)
     W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
     a = rng.standard_normal((M, K)).astype(np.float16)
@@ -92,6 +93,42 @@ def test_gemm_parity(torch_gpu, M, K, N, gs):
     ref = Q.matmul_ref(a.astype(np.float32), w_hat)
     err = Q.max_abs_rel(out.float().cpu().numpy(), ref)
     assert err < TOL, err
+
+
+# Config 2: the four Qwen3-8B decode linears (N x K) at their exact shapes,
+# each at every batch of the config (each (shape, M) has its own launch
+# configuration).  Seeds 2000 + i per shape i, W drawn before x.
+QWEN3_8B = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (24576, 4096),
+            "down": (4096, 12288)}
+_qwen_cache = {}
+
+
+def _qwen_payload(torch, name):
+    if name not in _qwen_cache:
+        N, K = QWEN3_8B[name]
+        rng = np.random.default_rng(2000 + list(QWEN3_8B).index(name))
+        W = (rng.standard_normal((N, K)) * 0.02).astype(np.float16).astype(np.float32)
+        pay, w_hat, _ = _prep(torch, W, 128)
+        _qwen_cache.clear()  # one shape's fp32 W_hat at a time (gate_up's is 400 MB)
+        _qwen_cache[name] = (pay, w_hat, rng)
+    return _qwen_cache[name]
+
+
+@pytest.mark.parametrize("M", [1, 4, 8, 16])
+@pytest.mark.parametrize("name", list(QWEN3_8B))  # closest decorator = outer loop
+def test_gemm_parity_qwen3_8b(torch_gpu, name, M):
+    from fastllm_py.kernels import marlin
+
+    torch = torch_gpu
+    pay, w_hat, rng = _qwen_payload(torch, name)
+    N, K = QWEN3_8B[name]
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    out = marlin.marlin_gemm_int4(torch.from_numpy(a).cuda(), pay["qweight"], pay["scales"],
+                                  pay["zeros"], marlin.make_workspace(N))
+    assert out.shape == (M, N)
+    ref = Q.matmul_ref(a.astype(np.float32), w_hat)
+    err = Q.max_abs_rel(out.float().cpu().numpy(), ref)
+    assert err < TOL, (name, M, err)
 
 
 @pytest.mark.parametrize("M", [17, 33, 64, 100, 130])

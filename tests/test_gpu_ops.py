@@ -105,6 +105,115 @@ def test_gemm_add_rmsnorm_rejects(torch_gpu):
     assert lib.fastllm_int4_gemm_add_rmsnorm(p, p, p, 1e-6, p, p, p, p, p, 64, 128, 64, 0, None) == 1  # group
 
 
+def test_gemm_add_rmsnorm_rejects_aliasing(torch_gpu):
+    """xnew overlapping x or delta is refused: workgroup 0 stores xnew while
+    other workgroups still read x and delta."""
+    from fastllm_py import _native as nat
+    from fastllm_py.kernels import marlin
+    from fastllm_py.moe import quantize_marlin_matrix_device
+
+    torch = torch_gpu
+    N, K = 256, 1024
+    W = torch.randn((N, K), generator=torch.Generator().manual_seed(3)).mul_(0.02).cuda()
+    pay = quantize_marlin_matrix_device(W, 128)
+    x = torch.randn((1, K), device="cuda")
+    d = torch.randn((1, K), device="cuda").half()
+    ln = torch.ones(K, device="cuda").half()
+    with pytest.raises(ValueError):
+        marlin.gemm_add_rmsnorm(x, d, ln, 1e-6, pay["qweight"], pay["scales"], pay["zeros"], N, K,
+                                xnew=x)
+    c = torch.empty((1, N), device="cuda").half()
+    lib = nat.lib()
+    args = [pay["qweight"].data_ptr(), pay["scales"].data_ptr(), pay["zeros"].data_ptr(),
+            c.data_ptr(), N, K, 128, 0, None]
+    assert lib.fastllm_int4_gemm_add_rmsnorm(x.data_ptr(), d.data_ptr(), ln.data_ptr(), 1e-6,
+                                             x.data_ptr(), *args) == 1
+    dd = torch.empty(4 * K, device="cuda").half()  # xnew (fp32, 4K bytes) covering delta
+    assert lib.fastllm_int4_gemm_add_rmsnorm(x.data_ptr(), dd[K:].data_ptr(), ln.data_ptr(), 1e-6,
+                                             dd.data_ptr(), *args) == 1
+    xn = torch.empty((1, K), device="cuda")
+    assert lib.fastllm_int4_gemm_add_rmsnorm(x.data_ptr(), d.data_ptr(), ln.data_ptr(), 1e-6,
+                                             xn.data_ptr(), *args) == 0
+    torch.cuda.synchronize()
+
+
+def _device_payload(torch, N, K, seed):
+    from fastllm_py.moe import quantize_marlin_matrix_device
+
+    g = torch.Generator().manual_seed(seed)
+    W = (torch.randn((N, K), generator=g) * 0.02).cuda()
+    return quantize_marlin_matrix_device(W, 128)
+
+
+@pytest.mark.parametrize("N,K,swiglu", [(16384, 13312, False), (256, 16384, True),
+                                        (256, 12288, True)])
+def test_gemm_add_rmsnorm_large_k(torch_gpu, N, K, swiglu):
+    """Shapes past the two-tile LDS budget: the plain GEMV drops to one tile
+    per workgroup (N >= 16384, K > 12288), the SwiGLU pair falls back to the
+    standalone norm + unfused kernels (K > 12288).  Checked against the
+    two-launch path (oracle-tested at the other shapes)."""
+    from fastllm_py.kernels import marlin, ops
+
+    torch = torch_gpu
+    pay = _device_payload(torch, N, K, 41 + K)
+    g = torch.Generator().manual_seed(K)
+    x = torch.randn((1, K), generator=g).cuda()
+    d = (torch.randn((1, K), generator=g) * 0.5).half().cuda()
+    ln = (1.0 + 0.1 * torch.randn(K, generator=g)).half().cuda()
+    xnew, c = marlin.gemm_add_rmsnorm(x, d, ln, 1e-6, pay["qweight"], pay["scales"], pay["zeros"],
+                                      N, K, swiglu=swiglu)
+    h = ops.add_rmsnorm(x, d, ln, 1e-6)[1]
+    if swiglu:
+        two = marlin.gemm_swiglu(h, pay["qweight"], pay["scales"], pay["zeros"], N, K)
+    else:
+        two = marlin.gemm_fast(h, pay["qweight"], pay["scales"], pay["zeros"], N, K)
+    torch.cuda.synchronize()
+    assert torch.equal(xnew, x + d.float())
+    assert Q.max_abs_rel(c.float().cpu().numpy(), two.float().cpu().numpy()) < 5e-3
+
+
+@pytest.mark.parametrize("M,K", [(1, 12288), (4, 12288), (8, 12288), (1, 16384), (16, 16384)])
+def test_gemm_swiglu_large_k(torch_gpu, M, K):
+    """SwiGLU GEMV past four blocks per wave: fused up to K = 12288 at M <= 4,
+    the GEMV + standalone swiglu beyond; both against the oracle."""
+    from fastllm_py.kernels import marlin
+    from fastllm_py.moe import quantize_marlin_matrix_device
+
+    torch = torch_gpu
+    N = 256
+    rng = np.random.default_rng(900 + M + K)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    pay = quantize_marlin_matrix_device(torch.from_numpy(W).cuda(), 128)
+    q, s_, z = Q.quantize_int4_marlin(W, 128)
+    s16, zp = Q.marlin_scales_zeros(s_, z)
+    w_hat = Q.marlin_dequant(q, s16, zp, 128)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    h = marlin.gemm_swiglu(torch.from_numpy(a).cuda(), pay["qweight"], pay["scales"], pay["zeros"],
+                           N, K)
+    gu = Q.matmul_ref(a.astype(np.float32), w_hat)
+    g, u = gu[:, :N // 2], gu[:, N // 2:]
+    ref = g / (1.0 + np.exp(-g)) * u
+    assert h.shape == (M, N // 2)
+    assert Q.max_abs_rel(h.float().cpu().numpy(), ref) < 1e-2
+
+
+def test_swiglu_op(torch_gpu):
+    """ops.swiglu on strided halves of a gate/up output vs numpy's fp32
+    formula (reference ops.py:157-163), then fp16."""
+    from fastllm_py.kernels import ops
+
+    torch = torch_gpu
+    rng = np.random.default_rng(5)
+    gu = (rng.standard_normal((3, 2 * 1000)) * 4).astype(np.float16)
+    d = torch.from_numpy(gu).cuda()
+    out = ops.swiglu(d[:, :1000], d[:, 1000:])
+    g, u = gu[:, :1000].astype(np.float32), gu[:, 1000:].astype(np.float32)
+    ref = ((g / (1.0 + np.exp(-g))) * u).astype(np.float16).astype(np.float32)
+    np.testing.assert_allclose(out.float().cpu().numpy(), ref, rtol=2e-3, atol=1e-4)
+    with pytest.raises(ValueError):
+        ops.swiglu(d[:, :1000], d[:, 1000:], out=torch.empty(5, device="cuda").half())
+
+
 def _layer(torch, rng, hidden, q_dim, n_qkv, inter):
     from fastllm_py.moe import quantize_marlin_matrix_device
 
