@@ -18,6 +18,9 @@
 #include "int4_common.cuh"
 #include "npmath.cuh"
 
+#include <atomic>
+#include <mutex>
+
 namespace {
 
 // 8 row-major nibbles (bytes b0..b3 of w; byte b = k 2b low, 2b+1 high) ->
@@ -1936,18 +1939,21 @@ int fastllm_moe_int4_fused(const float* x, int T, int hidden, int group_size, in
                           true);
 }
 
-int fastllm_moe_int4_routed(const float* logits, int top_k, int scoring, int norm,
-                            float routed_scaling, const float* e_score_bias, int n_group,
-                            int topk_group, const float* shared_logit, int* topk_ids,
-                            float* topk_w, float* rw, float* shared_coef, int* n_active,
-                            int* active, int* offsets, int* tok, float* tokw, const float* x,
-                            int T, int hidden, int group_size, int E, int inter,
-                            const uint8_t* gq, const uint32_t* gsz, const uint8_t* uq,
-                            const uint32_t* usz, const uint8_t* dq, const uint32_t* dsz,
-                            int shared_inter, const uint8_t* sgq, const uint32_t* sgsz,
-                            const uint8_t* suq, const uint32_t* susz, const uint8_t* sdq,
-                            const uint32_t* sdsz, void* workspace, size_t workspace_bytes, float* y,
-                            void* stream) {
+// Router + fused MoE of T <= 16 tokens (body of fastllm_moe_int4_routed and
+// of its static-scratch variant).  `scratch_of`, when given, supplies the
+// workspace once every argument has been validated (nullptr -> rc 2).
+static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm,
+                           float routed_scaling, const float* e_score_bias, int n_group,
+                           int topk_group, const float* shared_logit, int* topk_ids,
+                           float* topk_w, float* rw, float* shared_coef, int* n_active,
+                           int* active, int* offsets, int* tok, float* tokw, const float* x,
+                           int T, int hidden, int group_size, int E, int inter,
+                           const uint8_t* gq, const uint32_t* gsz, const uint8_t* uq,
+                           const uint32_t* usz, const uint8_t* dq, const uint32_t* dsz,
+                           int shared_inter, const uint8_t* sgq, const uint32_t* sgsz,
+                           const uint8_t* suq, const uint32_t* susz, const uint8_t* sdq,
+                           const uint32_t* sdsz, void* workspace, size_t workspace_bytes,
+                           float* y, void* stream, void* (*scratch_of)() = nullptr) {
     if (!logits || T <= 0 || T > 16 || E <= 0 || E > 256 || top_k <= 0 || top_k > 16 || top_k > E)
         return 1;
     if (!topk_ids || !topk_w || !n_active || !active || !offsets || !tok || !tokw) return 1;
@@ -1955,6 +1961,21 @@ int fastllm_moe_int4_routed(const float* logits, int top_k, int scoring, int nor
     if (n_group > 1 && (E % n_group || n_group > 64)) return 1;
     if (shared_inter > 0 && shared_logit && !shared_coef) return 1;
     const int max_entries = T * top_k, max_slots = E < max_entries ? E : max_entries;
+    if (scratch_of) {
+        MoePlan sp;
+        if (!moe_plan(T, hidden, inter, shared_inter > 0 ? shared_inter : 0, max_entries, sp))
+            return 1;
+        if (sp.bytes > workspace_bytes) {
+            fprintf(stderr,
+                    "fastllm_moe_int4_routed_noalloc: this shape needs %zu bytes of scratch; the "
+                    "static scratch holds %zu (use fastllm_moe_int4_routed with a workspace)\n",
+                    sp.bytes, workspace_bytes);
+            return 1;
+        }
+        if (!fl_current_device_supported()) return 2;
+        workspace = scratch_of();
+        if (!workspace) return 2;
+    }
     // the MoE arguments are checked before anything is launched
     const int rc = moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz,
                                   shared_inter, sgq, sgsz, suq, susz, sdq, sdsz, shared_coef,
@@ -1991,6 +2012,84 @@ int fastllm_moe_int4_routed(const float* logits, int top_k, int scoring, int nor
                           shared_logit ? shared_coef : nullptr, n_active, active, offsets, tok, tokw,
                           max_slots, max_entries, workspace, workspace_bytes, y, stream, true,
                           nullptr, p.xh_off != 0);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------- static scratch (no-alloc entry)
+// Workspace of fastllm_moe_int4_routed_noalloc: one copy per GPU, held until
+// the process ends.  In host code `scratch` only names the symbol; kernels
+// get the device address that hipGetSymbolAddress returns for the current
+// device (moe_scratch_ptr).  Every call on a GPU shares it, so calls that
+// overlap on one GPU (two streams, two threads) race on it.
+constexpr size_t kMoeScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kMoeScratchBytes];
+
+// Device address of `scratch` on the calling thread's current device,
+// resolved once per device with that device current (nullptr on failure).
+static void* moe_scratch_ptr() {
+    static std::atomic<void*> addr[64];
+    static std::mutex mu;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    void* p = addr[dev].load(std::memory_order_acquire);
+    if (p) return p;
+    std::lock_guard<std::mutex> lock(mu);
+    p = addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            fprintf(stderr, "fastllm_moe_int4_routed_noalloc: scratch address on device %d: %s\n",
+                    dev, hipGetErrorString(e));
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        addr[dev].store(p, std::memory_order_release);
+    }
+    return p;
+}
+
+extern "C" {
+
+int fastllm_moe_int4_routed(const float* logits, int top_k, int scoring, int norm,
+                            float routed_scaling, const float* e_score_bias, int n_group,
+                            int topk_group, const float* shared_logit, int* topk_ids,
+                            float* topk_w, float* rw, float* shared_coef, int* n_active,
+                            int* active, int* offsets, int* tok, float* tokw, const float* x,
+                            int T, int hidden, int group_size, int E, int inter,
+                            const uint8_t* gq, const uint32_t* gsz, const uint8_t* uq,
+                            const uint32_t* usz, const uint8_t* dq, const uint32_t* dsz,
+                            int shared_inter, const uint8_t* sgq, const uint32_t* sgsz,
+                            const uint8_t* suq, const uint32_t* susz, const uint8_t* sdq,
+                            const uint32_t* sdsz, void* workspace, size_t workspace_bytes, float* y,
+                            void* stream) {
+    return moe_routed_impl(logits, top_k, scoring, norm, routed_scaling, e_score_bias, n_group,
+                           topk_group, shared_logit, topk_ids, topk_w, rw, shared_coef, n_active,
+                           active, offsets, tok, tokw, x, T, hidden, group_size, E, inter, gq, gsz,
+                           uq, usz, dq, dsz, shared_inter, sgq, sgsz, suq, susz, sdq, sdsz,
+                           workspace, workspace_bytes, y, stream);
+}
+
+int fastllm_moe_int4_routed_noalloc(const float* logits, int top_k, int scoring, int norm,
+                                    float routed_scaling, const float* e_score_bias, int n_group,
+                                    int topk_group, const float* shared_logit, int* topk_ids,
+                                    float* topk_w, float* rw, float* shared_coef, int* n_active,
+                                    int* active, int* offsets, int* tok, float* tokw,
+                                    const float* x, int T, int hidden, int group_size, int E,
+                                    int inter, const uint8_t* gq, const uint32_t* gsz,
+                                    const uint8_t* uq, const uint32_t* usz, const uint8_t* dq,
+                                    const uint32_t* dsz, int shared_inter, const uint8_t* sgq,
+                                    const uint32_t* sgsz, const uint8_t* suq, const uint32_t* susz,
+                                    const uint8_t* sdq, const uint32_t* sdsz, float* y,
+                                    void* stream) {
+    return moe_routed_impl(logits, top_k, scoring, norm, routed_scaling, e_score_bias, n_group,
+                           topk_group, shared_logit, topk_ids, topk_w, rw, shared_coef, n_active,
+                           active, offsets, tok, tokw, x, T, hidden, group_size, E, inter, gq, gsz,
+                           uq, usz, dq, dsz, shared_inter, sgq, sgsz, suq, susz, sdq, sdsz, nullptr,
+                           kMoeScratchBytes, y, stream, moe_scratch_ptr);
 }
 
 }  // extern "C"

@@ -394,18 +394,93 @@ def moe_route_forward(x, logits, stacked, top_k, E, hidden, inter, *, norm_topk_
     if ws is None or ws.numel() * ws.element_size() < need or not ws.is_contiguous():
         ws = t.empty((need,), dtype=t.uint8, device=dev)
     y = out if out is not None else t.empty((T, hidden), dtype=t.float32, device=dev)
-    sp = _stacked_ptrs(shared) if shared is not None else [None] * 6
     h = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
-    rc = nat.lib().fastllm_moe_int4_routed(
-        nat.ptr(s), int(top_k), 1 if scoring == "sigmoid" else 0, 1 if norm_topk_prob else 0,
-        float(routed_scaling), nat.ptr(bias) if bias is not None else None, int(n_group or 0),
-        int(topk_group or 0), nat.ptr(sl) if sl is not None else None, nat.ptr(ids), nat.ptr(w),
-        nat.ptr(rw), nat.ptr(sc) if sc is not None else None, nat.ptr(na), nat.ptr(act),
-        nat.ptr(offs), nat.ptr(tok), nat.ptr(tokw), nat.ptr(x2), T, hidden, stacked["group"], E,
-        inter, *_stacked_ptrs(stacked), sint, *sp, nat.ptr(ws), ws.numel() * ws.element_size(),
-        nat.ptr(y), h)
+    args = _routed_args(s, top_k, scoring, norm_topk_prob, routed_scaling, bias, n_group,
+                        topk_group, sl, o, x2, T, hidden, stacked, E, inter, shared, sint)
+    rc = nat.lib().fastllm_moe_int4_routed(*args, nat.ptr(ws), ws.numel() * ws.element_size(),
+                                           nat.ptr(y), h)
     nat.check_rc(rc, "fastllm_moe_int4_routed")
     return y
+
+
+def _routed_args(s, top_k, scoring, norm_topk_prob, routed_scaling, bias, n_group, topk_group,
+                 sl, o, x2, T, hidden, stacked, E, inter, shared, sint):
+    """Arguments of the routed MoE entries up to the workspace."""
+    sp = _stacked_ptrs(shared) if shared is not None else [None] * 6
+    sc = o.get("shared_coef") if sl is not None else None
+    return [nat.ptr(s), int(top_k), 1 if scoring == "sigmoid" else 0, 1 if norm_topk_prob else 0,
+            float(routed_scaling), nat.ptr(bias) if bias is not None else None, int(n_group or 0),
+            int(topk_group or 0), nat.ptr(sl) if sl is not None else None,
+            nat.ptr(o["topk_ids"]), nat.ptr(o["topk_w"]), nat.ptr(o["rw"]),
+            nat.ptr(sc) if sc is not None else None, nat.ptr(o["n_active"]),
+            nat.ptr(o["active"]), nat.ptr(o["offsets"]), nat.ptr(o["tok"]), nat.ptr(o["tokw"]),
+            nat.ptr(x2), T, hidden, stacked["group"], E, inter, *_stacked_ptrs(stacked), sint, *sp]
+
+
+# sizes (elements, dtype name) of the router outputs of T tokens, top_k of E
+def _route_buffer_shapes(T, E, top_k):
+    return {"topk_ids": ((T, top_k), "int32"), "topk_w": ((T, top_k), "float32"),
+            "rw": ((T, E), "float32"), "n_active": ((1,), "int32"), "active": ((E,), "int32"),
+            "offsets": ((E + 1,), "int32"), "tok": ((T * top_k,), "int32"),
+            "tokw": ((T * top_k,), "float32"), "shared_coef": ((T,), "float32")}
+
+
+def alloc_route_buffers(T: int, E: int, top_k: int, device="cuda") -> dict:
+    """Persistent router-output buffers for ``moe_route_forward`` /
+    ``moe_route_forward_noalloc`` (allocated once, outside any loop that must
+    not allocate)."""
+    t = nat.torch()
+    return {k: t.empty(shape, dtype=getattr(t, dt), device=device)
+            for k, (shape, dt) in _route_buffer_shapes(T, E, top_k).items()}
+
+
+def moe_route_forward_noalloc(x, logits, stacked, top_k, E, hidden, inter, *, route, out,
+                              norm_topk_prob=False, scoring="softmax", routed_scaling=1.0,
+                              e_score_bias=None, n_group=0, topk_group=0, shared=None,
+                              shared_inter=0, shared_logit=None, stream=None):
+    """``moe_route_forward`` through fastllm_moe_int4_routed_noalloc: the
+    workspace is the library's static per-GPU scratch (16 MiB), so nothing is
+    allocated, by this wrapper either.  Every buffer must be supplied: x
+    (T, hidden) and logits (T, E) contiguous fp32 device tensors, ``route``
+    from ``alloc_route_buffers``, ``out`` (T, hidden) fp32.  Calls that
+    overlap on one GPU share the scratch and race.  Raises ValueError for
+    missing or wrongly typed buffers and for shapes whose workspace exceeds
+    the scratch."""
+    t = nat.torch()
+    for name, v in (("x", x), ("logits", logits), ("out", out)):
+        if not isinstance(v, t.Tensor) or v.dtype != t.float32 or not v.is_cuda \
+                or not v.is_contiguous():
+            raise ValueError(f"moe_route_forward_noalloc: {name} must be a contiguous fp32 "
+                             f"device tensor")
+    T = x.numel() // hidden
+    if T > 16 or x.numel() != T * hidden or logits.numel() != T * E or out.numel() != T * hidden:
+        raise ValueError("moe_route_forward_noalloc: x (T, hidden), logits (T, E) and out "
+                         "(T, hidden) with T <= 16")
+    for k, (shape, dt) in _route_buffer_shapes(T, E, top_k).items():
+        if k == "shared_coef" and shared_logit is None:
+            continue
+        buf = route.get(k)
+        n = 1
+        for d in shape:
+            n *= d
+        if buf is None or buf.dtype != getattr(t, dt) or not buf.is_contiguous() \
+                or buf.numel() < n:
+            raise ValueError(f"moe_route_forward_noalloc: route[{k!r}] must hold {n} {dt}")
+    bias = None
+    if scoring == "sigmoid" and e_score_bias is not None:
+        bias = e_score_bias
+    sint = int(shared_inter or 0) if shared is not None else 0
+    h = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
+    args = _routed_args(logits, top_k, scoring, norm_topk_prob, routed_scaling, bias, n_group,
+                        topk_group, shared_logit, route, x, T, hidden, stacked, E, inter, shared,
+                        sint)
+    rc = nat.lib().fastllm_moe_int4_routed_noalloc(*args, nat.ptr(out), h)
+    if rc == 1:
+        raise ValueError(f"moe_route_forward_noalloc: arguments or shape refused (T={T} "
+                         f"hidden={hidden} inter={inter} shared_inter={sint}; a workspace above "
+                         f"the 16 MiB static scratch takes moe_route_forward)")
+    nat.check_rc(rc, "fastllm_moe_int4_routed_noalloc")
+    return out
 
 
 def fused_moe_weighted(x, stacked, rw, E, hidden, inter, out=None, inter_buf=None,

@@ -458,6 +458,38 @@ int fastllm_moe_int4_routed(const float *logits, int top_k, int scoring,
                             void *workspace, size_t workspace_bytes, float *y,
                             void *stream);
 
+/* fastllm_moe_int4_routed without the workspace argument: the workspace is a
+ * static device array of the library, FASTLLM_MOE_SCRATCH_BYTES (16 MiB) per
+ * GPU, held until the process ends, so the call allocates nothing (no
+ * hipMalloc/hipFree, no allocating library routine).  Shapes whose workspace
+ * (fastllm_moe_int4_workspace_bytes) exceeds it return 1 with a message on
+ * stderr.  Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (different streams or threads) race and must not be issued.
+ * The first call on each device resolves the array's address on that device
+ * (hipGetSymbolAddress); make it outside graph capture.  Other arguments,
+ * outputs and return codes as fastllm_moe_int4_routed.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). */
+#define FASTLLM_MOE_SCRATCH_BYTES ((size_t)16 << 20)
+int fastllm_moe_int4_routed_noalloc(const float *logits, int top_k, int scoring,
+                                    int norm, float routed_scaling,
+                                    const float *e_score_bias, int n_group,
+                                    int topk_group, const float *shared_logit,
+                                    int *topk_ids, float *topk_w, float *rw,
+                                    float *shared_coef, int *n_active,
+                                    int *active, int *offsets, int *tok,
+                                    float *tokw, const float *x, int T,
+                                    int hidden, int group_size, int E,
+                                    int inter, const uint8_t *gq,
+                                    const uint32_t *gsz, const uint8_t *uq,
+                                    const uint32_t *usz, const uint8_t *dq,
+                                    const uint32_t *dsz, int shared_inter,
+                                    const uint8_t *sgq, const uint32_t *sgsz,
+                                    const uint8_t *suq, const uint32_t *susz,
+                                    const uint8_t *sdq, const uint32_t *sdsz,
+                                    float *y, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
