@@ -12,9 +12,21 @@ Also measured (same JSON line, "breakdown"): M in {1,4,8,16}; FP8-E4M3
 (configs[2]); the fused Qwen1.5-MoE-A2.7B INT4 MoE layer at 1 and 16 tokens
 (configs[3]) in us/layer and against its routed-weight-bytes roofline.
 
+Also: config 1 (the INT4 GEMV on quantize_int4_group's format, 3072x1024),
+the row-major INT4 GEMV (dgemv) at the Qwen3-8B shapes, and the prefill
+GEMMs of config 5.
+
 Every figure is timed with HIP events around HIP-graph replays on the launch
-stream; each graph holds ~100 launches over weight copies whose total
-exceeds 2x the 256 MB Infinity Cache, so weights stream from HBM.
+stream.  Each graph cycles through enough weight copies (and, for the MoE,
+router logits) that the bytes touched between two reads of the same weight
+exceed 2.2x the 256 MB Infinity Cache, so weights stream from HBM; each leg
+records its `cycle_bytes`.  `--warmup W` untimed replays precede each timed
+region.
+
+CPU baselines (BASELINE.md's plan): the numpy oracle on the host, 3 warm-up
+runs then the median of 20; figure (i) dequantize-then-fp32-matmul per call
+(the reference's CPU semantics), figure (ii) the fp32 matmul on
+pre-dequantized weights (the BLAS floor); CPU model and BLAS build recorded.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -59,10 +71,15 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def graph_time(torch, stream, launches, reps, warmup=1):
+WARMUP = [5]  # untimed replays before each timed region (--warmup)
+
+
+def graph_time(torch, stream, launches, reps, warmup=None):
     """Capture the enqueue callbacks in one HIP graph on `stream`, replay it
-    `warmup` times, then time `reps` replays with HIP events on that stream.
-    Returns ms per replay."""
+    `warmup` (default --warmup) times, then time `reps` replays with HIP
+    events on that stream.  Returns ms per replay."""
+    if warmup is None:
+        warmup = WARMUP[0]
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         h = torch.cuda.current_stream().cuda_stream
@@ -86,6 +103,11 @@ def copies_for(nbytes):
     return max(2, -(-ROTATE_BYTES // max(1, nbytes)))
 
 
+def cycle(nbytes):
+    """Bytes touched between two reads of the same weight, and that over the MALL."""
+    return {"cycle_bytes": int(nbytes), "cycle_over_mall": round(nbytes / MALL_BYTES, 2)}
+
+
 # ------------------------------------------------------------------ INT4
 def build_int4_layers(torch):
     from fastllm_py.moe import quantize_marlin_matrix_device
@@ -97,8 +119,8 @@ def build_int4_layers(torch):
         W = torch.randn((N, K), generator=gen, device="cuda", dtype=torch.float32) * 0.02
         base[name] = quantize_marlin_matrix_device(W, GS)
         del W
-    nbytes = sum(marlin_bytes(0, N, K) for _, N, K in QWEN3_8B)
-    n = copies_for(nbytes)
+    # enough copies that even the smallest matrix (o) cycles through > 2.2x MALL
+    n = max(copies_for(marlin_bytes(0, N, K)) for _, N, K in QWEN3_8B)
     layers = [base] + [{k: {f: v.clone() for f, v in p.items()} for k, p in base.items()}
                        for _ in range(n - 1)]
     torch.cuda.synchronize()
@@ -136,7 +158,9 @@ def run_int4(torch, lib, layers, M, steps, stream):
     for name, N, K in QWEN3_8B:
         seq1 = [launcher(layers[c], name, N, K) for _ in range(r1) for c in range(L)]
         per[name] = graph_time(torch, stream, seq1, max(2, reps // 4)) / (r1 * L) * 1e3
-    return ms_step, per, reps * per_graph
+    cyc = {name: cycle(L * marlin_bytes(0, N, K)) for name, N, K in QWEN3_8B}
+    cyc["layer"] = cycle(L * sum(marlin_bytes(0, N, K) for _, N, K in QWEN3_8B))
+    return ms_step, per, reps * per_graph, cyc
 
 
 def run_swiglu(torch, lib, layers, stream, M_list=(1, 8)):
@@ -174,6 +198,7 @@ def run_swiglu(torch, lib, layers, stream, M_list=(1, 8)):
         tg = graph_time(torch, stream, [gemv(layers[c]["gate_up"]) for _ in range(r1)
                                         for c in range(L)], 4) / (r1 * L) * 1e3
         res[f"M{M}"] = {"fused_us": round(tf, 3), "gemv_alone_us": round(tg, 3)}
+    res.update(cycle(len(layers) * marlin_bytes(0, N, K)))
     return res
 
 
@@ -243,6 +268,86 @@ def run_layer_chain(torch, lib, layers, stream):
         res[name] = {"us_per_layer": round(us, 3), "launches_per_layer": nl,
                      "weight_GB/s": round(nb / us / 1e3, 1),
                      "pct_of_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS * 100, 2)}
+    res.update(cycle(n * nb))
+    return res
+
+
+def run_int4_group(torch, lib, stream, M_list=(1,), N=3072, K=1024, gs=128):
+    """Config 1: the INT4 GEMV on quantize_int4_group's format (u8 nibbles,
+    fp32 scale and minimum per 128-group), 3072x1024, fp16 x -> fp32 y,
+    rotated over copies (1.77 MB each) past 2.2x MALL."""
+    from fastllm_py import quantizer
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0)
+    W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+    qt = quantizer.quantize_int4_group(W, gs)
+    del W
+    wb = N * K // 2 + 2 * N * (K // gs) * 4
+    n = copies_for(wb)
+    cps = [(qt.data, qt.scales, qt.zeros)] + [(qt.data.clone(), qt.scales.clone(),
+                                               qt.zeros.clone()) for _ in range(n - 1)]
+    res = {}
+    for M in M_list:
+        x = torch.randn((M, K), generator=gen, device="cuda").to(torch.float16)
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+
+        def mk(d, sc, z, x=x, y=y, M=M):
+            def go(h):
+                if lib.fastllm_int4_group_gemv(x.data_ptr(), 0, d.data_ptr(), sc.data_ptr(),
+                                               z.data_ptr(), y.data_ptr(), 1, M, N, K, gs, h):
+                    raise RuntimeError("int4 group gemv failed")
+            return go
+        seq = [mk(*c) for c in cps]
+        us = graph_time(torch, stream, seq, 3) / len(seq) * 1e3
+        nb = wb + M * K * 2 + M * N * 4
+        res[f"M{M}"] = {"us_per_call": round(us, 3), "bytes": nb, "GB/s": round(nb / us / 1e3, 1),
+                        "pct_of_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS * 100, 2)}
+    res.update(cycle(n * wb))
+    del cps
+    torch.cuda.empty_cache()
+    return res
+
+
+def rowmajor_bytes(M, N, K, gs=GS):
+    return N * K // 2 + 2 * N * (K // gs) * 2 + M * K * 2 + M * N * 2
+
+
+def run_rowmajor(torch, lib, stream, M=1):
+    """The row-major INT4 GEMV (the reference's dgemv format: u8 nibbles, fp16
+    scale and zero per group) at the Qwen3-8B shapes, fp16 in and out, each
+    matrix rotated over copies past 2.2x MALL; per call and summed per layer."""
+    from fastllm_py.kernels import moe_int4
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2100)
+    res, total_us, total_b = {}, 0.0, 0
+    for name, N, K in QWEN3_8B:
+        W = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+        qw, sc, ze, _ = moe_int4._quantize_int4_rowmajor_batched(W, GS)
+        del W
+        n = copies_for(rowmajor_bytes(0, N, K))
+        cps = [(qw, sc, ze)] + [(qw.clone(), sc.clone(), ze.clone()) for _ in range(n - 1)]
+        x = torch.randn((M, K), generator=gen, device="cuda").to(torch.float16)
+        y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+
+        def mk(q, s_, z, x=x, y=y, N=N, K=K):
+            def go(h):
+                if lib.fastllm_int4_rowmajor_gemv(x.data_ptr(), 0, q.data_ptr(), s_.data_ptr(),
+                                                  z.data_ptr(), y.data_ptr(), 0, M, N, K, GS, h):
+                    raise RuntimeError("row-major gemv failed")
+            return go
+        seq = [mk(*c) for c in cps]
+        us = graph_time(torch, stream, seq, 3) / len(seq) * 1e3
+        nb = rowmajor_bytes(M, N, K)
+        res[name] = {"us_per_call": round(us, 3), "GB/s": round(nb / us / 1e3, 1),
+                     **cycle(n * rowmajor_bytes(0, N, K))}
+        total_us += us
+        total_b += nb
+        del cps, qw, sc, ze
+        torch.cuda.empty_cache()
+    res["layer"] = {"M": M, "us": round(total_us, 3), "GB/s": round(total_b / total_us / 1e3, 1),
+                    "pct_of_hbm_peak": round(total_b / total_us / 1e3 / HBM_PEAK_GBS * 100, 2)}
     return res
 
 
@@ -274,7 +379,7 @@ def run_fp8(torch, lib, stream, M_list=(1, 8)):
             us = graph_time(torch, stream, seq, 4) / len(seq) * 1e3
             nb = fp8_block_bytes(M, N, K)
             res[f"{name}/M{M}"] = {"us_per_call": round(us, 3), "GB/s": round(nb / us / 1e3, 1),
-                                   "bytes": nb}
+                                   "bytes": nb, **cycle(n * fp8_block_bytes(0, N, K))}
         del cps, qt
         torch.cuda.empty_cache()
     for M in M_list:
@@ -300,15 +405,21 @@ def run_fp8_prefill(torch, lib, stream, M=512):
         x = torch.randn((M, K), generator=gen, device="cuda").to(torch.bfloat16)
         y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
         f = lib.fastllm_fp8_b128x128_gemv
+        n = copies_for(N * K)
+        cps = [(qt.data, qt.scales)] + [(qt.data.clone(), qt.scales.clone()) for _ in range(n - 1)]
 
-        def go(h, q=qt.data, s=qt.scales, x=x, y=y, N=N, K=K):
-            if f(x.data_ptr(), q.data_ptr(), s.data_ptr(), None, y.data_ptr(), M, N, K, 1, h):
-                raise RuntimeError("fp8 gemm failed")
-        us = graph_time(torch, stream, [go] * 20, 5) / 20 * 1e3
+        def mk(q, s, x=x, y=y, N=N, K=K):
+            def go(h):
+                if f(x.data_ptr(), q.data_ptr(), s.data_ptr(), None, y.data_ptr(), M, N, K, 1, h):
+                    raise RuntimeError("fp8 gemm failed")
+            return go
+        seq = [mk(q, s) for q, s in cps]
+        us = graph_time(torch, stream, seq, 3) / len(seq) * 1e3
         tf = 2.0 * M * N * K / us / 1e6
         res[f"{name}/M{M}"] = {"us_per_call": round(us, 3), "TFLOP/s": round(tf, 1),
-                               "mfma_util_bf16_dense": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
-        del qt
+                               "mfma_util_bf16_dense": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                               **cycle(n * fp8_block_bytes(0, N, K))}
+        del qt, cps
         torch.cuda.empty_cache()
     return res
 
@@ -340,35 +451,45 @@ def run_moe(torch, lib, stream, T_list=(1, 16)):
         return st, sh
     expert_bytes = 3 * inter * hidden // 2 + 3 * inter * hidden // 128 * 4
     shared_bytes = 3 * sinter * hidden // 2 + 3 * sinter * hidden // 128 * 4
-    nl = copies_for(E * expert_bytes + shared_bytes)
+    # layer copies: one token's routed set + the shared expert, over 2.2x MALL
+    nl = copies_for(K * expert_bytes + shared_bytes)
     layers = [layer() for _ in range(nl)]
     res = {}
     for T in T_list:
-        logits = torch.randn((T, E), generator=gen, device="cuda").half().float()
-        x = torch.randn((T, hidden), generator=gen, device="cuda").half().float()
-        slog = torch.randn((T,), generator=gen, device="cuda")
+        # every launch of the cycle routes its own logits (tokens differ per
+        # layer and step), so consecutive launches touch different experts
+        rounds = max(1, -(-48 // nl))
+        n_ent = rounds * nl
+        logits = torch.randn((n_ent, T, E), generator=gen, device="cuda").half().float()
+        xs = torch.randn((n_ent, T, hidden), generator=gen, device="cuda").half().float()
+        slog = torch.randn((n_ent, T), generator=gen, device="cuda")
         bufs = {}
-        route_topk_device(logits, K, shared_logit=slog, out=bufs)
-        torch.cuda.synchronize()
-        distinct = len(np.unique(bufs["topk_ids"].cpu().numpy()))
+        touched, per_layer = set(), []
+        for i in range(n_ent):
+            route_topk_device(logits[i], K, shared_logit=slog[i], out=bufs)
+            ids = np.unique(bufs["topk_ids"].cpu().numpy())
+            per_layer.append(len(ids) * expert_bytes + shared_bytes)
+            touched.update((i % nl, int(e)) for e in ids)
         y = torch.empty((T, hidden), device="cuda")
         ws = torch.empty((moe_int4.moe_workspace_bytes(T, hidden, inter, sinter, T * K),),
                          dtype=torch.uint8, device="cuda")
 
-        def mk(st, sh, logits=logits, x=x, slog=slog, bufs=bufs, y=y, ws=ws):
+        def mk(i, st, sh, bufs=bufs, y=y, ws=ws, T=T):
             def go(h):
-                moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, shared=sh,
-                                           shared_inter=sinter, shared_logit=slog, route=bufs,
+                moe_int4.moe_route_forward(xs[i], logits[i], st, K, E, hidden, inter, shared=sh,
+                                           shared_inter=sinter, shared_logit=slog[i], route=bufs,
                                            out=y, workspace=ws, stream=h)
             return go
-        rounds = max(1, -(-48 // nl))
-        seq = [mk(st, sh) for _ in range(rounds) for st, sh in layers]
+        seq = [mk(i, *layers[i % nl]) for i in range(n_ent)]
         us = graph_time(torch, stream, seq, 4) / len(seq) * 1e3
-        routed = distinct * expert_bytes + shared_bytes
-        res[f"T{T}"] = {"us_per_layer": round(us, 3), "distinct_experts": distinct,
-                        "routed_weight_bytes": routed,
+        routed = float(np.mean(per_layer))
+        res[f"T{T}"] = {"us_per_layer": round(us, 3),
+                        "distinct_experts_mean": round((routed - shared_bytes) / expert_bytes, 2),
+                        "routed_weight_bytes_mean": int(routed),
                         "roofline_us": round(routed / HBM_PEAK_GBS / 1e3, 3),
-                        "frac_of_roofline": round(routed / HBM_PEAK_GBS / 1e3 / us, 4)}
+                        "frac_of_roofline": round(routed / HBM_PEAK_GBS / 1e3 / us, 4),
+                        "launch_cycle": f"{n_ent} layers: {nl} weight copies x {rounds} logits sets",
+                        **cycle(len(touched) * expert_bytes + nl * shared_bytes)}
     del layers
     torch.cuda.empty_cache()
     return res
@@ -411,7 +532,8 @@ def run_gemm_prefill(torch, lib, stream, M=512, N=8192, K=2048):
     torch.cuda.empty_cache()
     return {"shape": f"M{M} N{N} K{K}", "us_per_call": round(us, 3), "TFLOP/s": round(tflops, 1),
             "mfma_util_fp16_dense": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-            "weight_GB/s": round(marlin_bytes(M, N, K) / us / 1e3, 1)}
+            "weight_GB/s": round(marlin_bytes(M, N, K) / us / 1e3, 1),
+            **cycle(n * marlin_bytes(0, N, K))}
 
 
 def run_moe_prefill(torch, lib, stream, T=512):
@@ -464,14 +586,67 @@ def run_moe_prefill(torch, lib, stream, T=512):
     return {"T": T, "us_per_layer": round(us, 3), "distinct_experts": distinct,
             "routed_weight_bytes": routed, "weight_GB/s": round(routed / us / 1e3, 1),
             "pct_of_hbm_peak": round(routed / us / 1e3 / HBM_PEAK_GBS * 100, 2),
-            "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1)}
+            "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1), **cycle(nl * routed)}
 
 
 # ------------------------------------------------------------- CPU baseline
-def cpu_baseline_int4(budget_s=15.0):
-    """The reference's CPU semantics through the numpy oracle: per call,
-    dequantize the packed Marlin-format weight to fp32, then the fp32 GEMV.
-    Sample: the four Qwen3-8B GEMVs at M=1 (one layer) repeated until ~budget_s."""
+def host_info():
+    """CPU model, core count and the numpy BLAS build the baselines ran on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    blas, threads = "unknown", None
+    try:
+        import threadpoolctl
+
+        for lib_ in threadpoolctl.threadpool_info():
+            if lib_.get("user_api") == "blas":
+                threads = lib_.get("num_threads")
+                blas = (f"{lib_.get('internal_api')} {lib_.get('version')} "
+                        f"({lib_.get('architecture')}, {threads} threads)")
+                break
+    except Exception:  # threadpoolctl missing: report the build only
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "numpy": np.__version__,
+            "blas": blas, "blas_threads": threads}
+
+
+def time_median(fn, warmups=3, runs=20):
+    """3 warm-ups, then the median of `runs` timed calls (seconds)."""
+    for _ in range(warmups):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def _figures(name, nbytes, fn_i, fn_ii, info, sample, scale=1.0):
+    """Figure (i) dequantize-then-matmul and (ii) the matmul on pre-dequantized
+    fp32 weights, each 3 warm-ups + median of 20, times `scale` (a sample of
+    the unit's work scaled to the whole unit)."""
+    t1 = time_median(fn_i) * scale
+    t2 = time_median(fn_ii) * scale
+    return {"value": round(nbytes / t1 / 1e9, 4), "unit": "GB/s", "us": round(t1 * 1e6, 1),
+            "blas_floor": {"us": round(t2 * 1e6, 1), "GB/s": round(nbytes / t2 / 1e9, 3)},
+            "cores": info["blas_threads"] or os.cpu_count(), "kind": "port",
+            "sample": f"{name}; {sample}; numpy oracle, 3 warm-ups + median of 20; "
+                      f"(i) dequantize-then-fp32 matmul per call (elementwise numpy on 1 thread, "
+                      f"BLAS on {info['blas_threads']}), blas_floor = (ii) fp32 matmul on "
+                      f"pre-dequantized weights; {info['cpu_model']}, {info['blas']}"}
+
+
+def cpu_baseline_int4(info):
+    """Config 2 at M=1 (one Qwen3-8B layer, 4 GEMVs) on the Marlin-format
+    weights: the headline's CPU baseline."""
     from oracle import quant as Q
 
     rng = np.random.default_rng(3000)
@@ -484,32 +659,39 @@ def cpu_baseline_int4(budget_s=15.0):
         del W
     x = {K: rng.standard_normal((1, K)).astype(np.float16).astype(np.float32)
          for K in {k for _, _, k in QWEN3_8B}}
-    nbytes = sum(marlin_bytes(1, N, K) for _, N, K in QWEN3_8B)
-    reps, t_total = 0, 0.0
-    while t_total < budget_s and reps < 50:
-        t0 = time.perf_counter()
+    hats = [Q.marlin_dequant(q, s16, zp, GS) for _, _, q, s16, zp in layer]
+
+    def fi():
         for N, K, q, s16, zp in layer:
-            w_hat = Q.marlin_dequant(q, s16, zp, GS)
-            _ = Q.matmul_ref(x[K], w_hat)
-        t_total += time.perf_counter() - t0
-        reps += 1
-    us_per_layer = t_total / reps * 1e6
-    return {
-        "value": round(nbytes / (us_per_layer * 1e-6) / 1e9, 3),
-        "unit": "GB/s",
-        "us_per_layer": round(us_per_layer, 1),
-        "cores": os.cpu_count(),
-        "kind": "port",
-        "sample": f"numpy oracle: dequantize-then-fp32-GEMV of one Qwen3-8B layer (4 GEMVs, M=1), "
-                  f"{reps} reps in {t_total:.1f}s; numpy elementwise on 1 thread, BLAS on all "
-                  f"{os.cpu_count()} host threads",
-    }
+            Q.matmul_ref(x[K], Q.marlin_dequant(q, s16, zp, GS))
+
+    def fii():
+        for (N, K, *_), w in zip(layer, hats):
+            Q.matmul_ref(x[K], w)
+    nbytes = sum(marlin_bytes(1, N, K) for _, N, K in QWEN3_8B)
+    r = _figures("config 2: one Qwen3-8B layer (qkv, o, gate_up, down) at M=1, Marlin format",
+                 nbytes, fi, fii, info, "unit = one layer")
+    r["us_per_layer"] = r.pop("us")
+    return r
 
 
-def cpu_baseline_fp8(budget_s=6.0):
-    """Config 3 at M=1 on the host through the numpy oracle: per call,
-    dequantize the 128x128-block e4m3 weight to fp32, then the fp32 GEMV
-    (the three shapes, summed)."""
+def cpu_baseline_int4_group(info, N=3072, K=1024, gs=128):
+    """Config 1 on the host: dequantize_int4_group then the fp32 GEMV."""
+    from oracle import quant as Q
+
+    rng = np.random.default_rng(0)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((1, K)).astype(np.float16).astype(np.float32)
+    p, sc, z = Q.quantize_int4_group(W, gs)
+    w = Q.dequantize_int4_group(p, sc, z, gs)
+    nbytes = N * K // 2 + 2 * N * (K // gs) * 4 + K * 2 + N * 4
+    return _figures("config 1: 3072x1024 int4_group GEMV at M=1", nbytes,
+                    lambda: Q.matmul_ref(x, Q.dequantize_int4_group(p, sc, z, gs)),
+                    lambda: Q.matmul_ref(x, w), info, "unit = one call")
+
+
+def cpu_baseline_fp8(info):
+    """Config 3 at M=1 on the host: the three 128x128-block e4m3 shapes, summed."""
     from oracle import quant as Q
 
     rng = np.random.default_rng(3100)
@@ -517,60 +699,103 @@ def cpu_baseline_fp8(budget_s=6.0):
     for _, N, K in FP8_SHAPES:
         W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
         q, sc = Q.quantize_fp8_block(W, 128)
-        mats.append((q, sc, rng.standard_normal((1, K)).astype(np.float32)))
+        mats.append((q, sc, rng.standard_normal((1, K)).astype(np.float32),
+                     Q.dequantize_fp8_block(q, sc, 128)))
         del W
-    reps, t_total = 0, 0.0
-    while t_total < budget_s and reps < 30:
-        t0 = time.perf_counter()
-        for q, sc, x in mats:
-            _ = Q.matmul_ref(x, Q.dequantize_fp8_block(q, sc, 128))
-        t_total += time.perf_counter() - t0
-        reps += 1
-    return {"us_per_sum_M1": round(t_total / reps * 1e6, 1), "cores": os.cpu_count(), "kind": "port",
-            "sample": f"numpy oracle: dequantize-then-fp32-GEMV of the 3 config-3 shapes at M=1, "
-                      f"{reps} reps in {t_total:.1f}s"}
+    nbytes = sum(fp8_block_bytes(1, N, K) for _, N, K in FP8_SHAPES)
+
+    def fi():
+        for q, sc, x, _ in mats:
+            Q.matmul_ref(x, Q.dequantize_fp8_block(q, sc, 128))
+
+    def fii():
+        for _, _, x, w in mats:
+            Q.matmul_ref(x, w)
+    return _figures("config 3: the 3 FP8 128x128-block shapes at M=1, summed", nbytes, fi, fii,
+                    info, "unit = the sum of the three calls")
 
 
-def cpu_baseline_moe(budget_s=6.0):
-    """Config 4 at T=1 on the host through the numpy oracle, the reference's
-    CPU semantics (fastllm_py/moe.py:161-175): route_topk, then per routed
-    expert and for the shared expert dequantize the row-major INT4 weights to
-    fp32 and run the FFN; only the touched experts are dequantized.  The four
-    routed experts are built once and stand for whichever the router picks
-    (the cost does not depend on which)."""
-    from oracle import moe as OM
+def _moe_expert(rng, hidden, n_inter, n_exp=1):
     from oracle import quant as Q
+
+    d = {}
+    for p, shp in (("gate", (n_inter, hidden)), ("up", (n_inter, hidden)),
+                   ("down", (hidden, n_inter))):
+        w = (rng.standard_normal((n_exp,) + shp) * 0.02).astype(np.float16).astype(np.float32)
+        d.update(zip((f"{p}.qweight", f"{p}.scales", f"{p}.zeros"),
+                     Q.quantize_int4_rowmajor(w, 128)))
+    return d
+
+
+def cpu_baseline_moe(info):
+    """Config 4 at T=1 on the host, the reference's CPU semantics
+    (fastllm_py/moe.py:161-175): route_topk, then per routed expert and for
+    the shared expert dequantize the row-major INT4 weights to fp32 and run
+    the FFN.  The four routed experts are built once and stand for whichever
+    the router picks (the cost does not depend on which)."""
+    from oracle import moe as OM
     from oracle import router as R
 
     E, hidden, inter, sinter, K = 60, 2048, 1408, 5632, 4
     rng = np.random.default_rng(3200)
-
-    def expert(n_inter):
-        return {f"{p}.{k}": v for p, shp in (("gate", (n_inter, hidden)), ("up", (n_inter, hidden)),
-                                             ("down", (hidden, n_inter)))
-                for k, v in zip(("qweight", "scales", "zeros"),
-                                Q.quantize_int4_rowmajor((rng.standard_normal(shp) * 0.02)
-                                                         .astype(np.float32)[None], 128))}
-    routed = [expert(inter) for _ in range(K)]
-    shared = expert(sinter)
+    routed = [_moe_expert(rng, hidden, inter) for _ in range(K)]
+    shared = _moe_expert(rng, hidden, sinter)
     x = rng.standard_normal((1, hidden)).astype(np.float16).astype(np.float32)
     logits = rng.standard_normal((1, E)).astype(np.float16).astype(np.float32)
-    reps, t_total = 0, 0.0
-    while t_total < budget_s and reps < 30:
-        t0 = time.perf_counter()
+    deq = [OM.dequant_stacked(d, 128) for d in routed + [shared]]
+
+    def run(dequantize):
         _, idx, w = R.route_topk(logits, K, return_arrays=True)
         y = np.zeros((1, hidden), np.float32)
-        for j in range(K):
-            d = OM.dequant_stacked(routed[j], 128)
-            y += w[0, j] * OM.expert_ffn(x, d["gate"][0], d["up"][0], d["down"][0])
-        d = OM.dequant_stacked(shared, 128)
-        y += OM.expert_ffn(x, d["gate"][0], d["up"][0], d["down"][0])
-        t_total += time.perf_counter() - t0
-        reps += 1
-    return {"us_per_layer_T1": round(t_total / reps * 1e6, 1), "cores": os.cpu_count(),
-            "kind": "port",
-            "sample": f"numpy oracle: route_topk + dequantize-then-fp32 FFN of 4 routed experts and "
-                      f"the shared one at T=1, {reps} reps in {t_total:.1f}s"}
+        for j, d in enumerate(routed + [shared]):
+            dd = OM.dequant_stacked(d, 128) if dequantize else deq[j]
+            c = w[0, j] if j < K else 1.0
+            y += c * OM.expert_ffn(x, dd["gate"][0], dd["up"][0], dd["down"][0])
+        return y
+    expert_bytes = 3 * inter * hidden // 2 + 3 * inter * hidden // 128 * 4
+    shared_bytes = 3 * sinter * hidden // 2 + 3 * sinter * hidden // 128 * 4
+    r = _figures("config 4: Qwen1.5-MoE layer at T=1 (route_topk + 4 routed experts + shared)",
+                 K * expert_bytes + shared_bytes, lambda: run(True), lambda: run(False), info,
+                 "unit = one layer")
+    r["us_per_layer_T1"] = r.pop("us")
+    return r
+
+
+def cpu_baseline_moe_prefill(info, T=512, n_sample=16):
+    """Config 5's grouped MoE layer on the host (Qwen3-30B-A3B, T=512, top-8
+    of 128 with renormalisation): route_topk over all 512 tokens, then the
+    expert-grouped FFN (fastllm_py/moe.py:135-175) of `n_sample` experts with
+    their routed tokens, scaled by 128 / n_sample to the whole layer."""
+    from oracle import moe as OM
+    from oracle import router as R
+
+    E, hidden, inter, K = 128, 2048, 768, 8
+    rng = np.random.default_rng(3300)
+    logits = rng.standard_normal((T, E)).astype(np.float16).astype(np.float32)
+    x = rng.standard_normal((T, hidden)).astype(np.float16).astype(np.float32)
+    _, idx, w = R.route_topk(logits, K, norm_topk_prob=True, return_arrays=True)
+    experts = [_moe_expert(rng, hidden, inter) for _ in range(n_sample)]
+    deq = [OM.dequant_stacked(d, 128) for d in experts]
+    rows = [np.nonzero(idx == e) for e in range(n_sample)]
+
+    def run(dequantize):
+        R.route_topk(logits, K, norm_topk_prob=True, return_arrays=True)
+        y = np.zeros((T, hidden), np.float32)
+        for e in range(n_sample):
+            t_i, k_i = rows[e]
+            if len(t_i) == 0:
+                continue
+            d = OM.dequant_stacked(experts[e], 128) if dequantize else deq[e]
+            y[t_i] += w[t_i, k_i][:, None] * OM.expert_ffn(x[t_i], d["gate"][0], d["up"][0],
+                                                           d["down"][0])
+        return y
+    expert_bytes = 3 * inter * hidden // 2 + 3 * inter * hidden // 128 * 4
+    r = _figures(f"config 5: Qwen3-30B-A3B grouped MoE layer, T={T}", E * expert_bytes,
+                 lambda: run(True), lambda: run(False), info,
+                 f"unit = one layer, sampled as routing + {n_sample} of the 128 experts "
+                 f"scaled x{E // n_sample}", scale=E / n_sample)
+    r["us_per_layer"] = r.pop("us")
+    return r
 
 
 def main():
@@ -580,7 +805,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--only", default="int4,swiglu,layer,fp8,fp8p,moe,gemm")
+    ap.add_argument("--only", default="int4,swiglu,layer,group,rm,fp8,fp8p,moe,gemm")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy a 64 MiB buffer 5 times (a known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -590,6 +815,7 @@ def main():
               f"got --gpus {args.gpus}", file=sys.stderr)
         sys.exit(2)
 
+    WARMUP[0] = max(1, args.warmup)
     import torch
 
     from fastllm_py import _native as nat
@@ -613,8 +839,9 @@ def main():
     log(f"INT4: {len(layers)} Qwen3-8B layer copies")
     per_m = {}
     steps_run = args.steps
+    cyc = {}
     for M in ms_list:
-        ms_step, per, done = run_int4(torch, lib, layers, M, args.steps, stream)
+        ms_step, per, done, cyc = run_int4(torch, lib, layers, M, args.steps, stream)
         if M == ms_list[0]:
             steps_run = done
         nbytes = sum(marlin_bytes(M, N, K) for _, N, K in QWEN3_8B)
@@ -629,6 +856,7 @@ def main():
                  "us_per_layer": round(v["ms_per_layer"] * 1e3, 3),
                  "us_per_call": {k: round(u, 3) for k, u in v["us_per_call"].items()}}
         for m, v in per_m.items()}
+    breakdown["int4_qwen3_8b"]["cycle"] = cyc
     if "swiglu" in only:
         breakdown["int4_gate_up_swiglu"] = run_swiglu(torch, lib, layers, stream)
     if "layer" in only:
@@ -637,6 +865,12 @@ def main():
     del layers
     torch.cuda.empty_cache()
 
+    if "group" in only:
+        breakdown["int4_group_config1"] = run_int4_group(torch, lib, stream, M_list=(1, 16))
+        log(f"config 1: {breakdown['int4_group_config1']}")
+    if "rm" in only:
+        breakdown["int4_rowmajor_dgemv_qwen3_8b_M1"] = run_rowmajor(torch, lib, stream)
+        log(f"row-major: {breakdown['int4_rowmajor_dgemv_qwen3_8b_M1']}")
     if "gemm" in only:
         breakdown["int4_gemm_prefill"] = run_gemm_prefill(torch, lib, stream)
         log(f"GEMM: {breakdown['int4_gemm_prefill']}")
@@ -668,14 +902,19 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        log("timing CPU baseline (numpy oracle) ...")
-        cpu = cpu_baseline_int4()
-        if "fp8_b128x128_bf16" in breakdown:
-            breakdown["fp8_b128x128_bf16"]["cpu_baseline"] = cpu_baseline_fp8()
-        if "moe_qwen15_a27b_int4" in breakdown:
-            breakdown["moe_qwen15_a27b_int4"]["cpu_baseline"] = cpu_baseline_moe()
-        log(f"CPU baselines: fp8 {breakdown.get('fp8_b128x128_bf16', {}).get('cpu_baseline')} "
-            f"moe {breakdown.get('moe_qwen15_a27b_int4', {}).get('cpu_baseline')}")
+        info = host_info()
+        log(f"timing CPU baselines (numpy oracle) on {info}")
+        cpu = cpu_baseline_int4(info)
+        cpu["host"] = info
+        log(f"CPU config 2: {cpu}")
+        legs = (("int4_group_config1", cpu_baseline_int4_group),
+                ("fp8_b128x128_bf16", cpu_baseline_fp8),
+                ("moe_qwen15_a27b_int4", cpu_baseline_moe),
+                ("moe_prefill_qwen3_30b_a3b_int4", cpu_baseline_moe_prefill))
+        for key, fn in legs:
+            if key in breakdown:
+                breakdown[key]["cpu_baseline"] = fn(info)
+                log(f"CPU {key}: {breakdown[key]['cpu_baseline']}")
 
     out = {
         "metric": "INT4/FP8 GEMV HBM GB/s (% of peak) at Qwen3-8B shapes; fused-MoE us/layer",
