@@ -130,12 +130,20 @@ def is_tensor(x) -> bool:
     return isinstance(x, t.Tensor)
 
 
+def is_device_array(x) -> bool:
+    """A non-torch device array (e.g. CuPy) exposing __cuda_array_interface__."""
+    return hasattr(x, "__cuda_array_interface__") and not isinstance(x, torch().Tensor)
+
+
 def to_device(x, dtype=None):
-    """numpy/torch -> contiguous CUDA tensor (optionally cast)."""
+    """numpy / torch / device array (e.g. CuPy, zero-copy through
+    __cuda_array_interface__) -> contiguous CUDA tensor (optionally cast)."""
     t = torch()
     require_device()
     if isinstance(x, np.ndarray):
         x = t.from_numpy(np.ascontiguousarray(x))
+    elif is_device_array(x):
+        x = t.as_tensor(x, device="cuda")
     elif not isinstance(x, t.Tensor):
         x = t.as_tensor(np.asarray(x))
     if dtype is not None and x.dtype != dtype:
@@ -146,7 +154,10 @@ def to_device(x, dtype=None):
 
 
 def ptr(x) -> int:
-    return int(x.data_ptr())
+    """Device address of a torch tensor or of a __cuda_array_interface__ array."""
+    if hasattr(x, "data_ptr"):
+        return int(x.data_ptr())
+    return int(x.__cuda_array_interface__["data"][0])
 
 
 def current_stream_handle() -> int:
@@ -185,6 +196,13 @@ def overlaps(a, b) -> bool:
     pa, pb = a.data_ptr(), b.data_ptr()
     na, nb = a.numel() * a.element_size(), b.numel() * b.element_size()
     return pa < pb + nb and pb < pa + na
+
+
+def host_out(x, xp) -> bool:
+    """The reference's xp convention: numpy (host) results exactly when the
+    caller asks for xp=numpy with a host input; any other xp (CuPy, torch)
+    or a device input gives device results."""
+    return xp is np and not (isinstance(x, torch().Tensor) or is_device_array(x))
 
 
 def as_output(x, like_numpy: bool):

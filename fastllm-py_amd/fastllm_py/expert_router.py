@@ -24,9 +24,14 @@ from . import _native as nat
 
 @dataclass
 class ExpertTask:
+    """One expert's share of a batch: ``token_idx`` (int32, ascending) are
+    the batch rows routed to expert ``expert_id`` and ``weights`` (float32)
+    their combine weights, in the same order.  Field names and order are the
+    reference's, which its MoE layer reads."""
+
     expert_id: int
-    token_idx: np.ndarray  # (n,) int32 -- rows of x this expert processes
-    weights: np.ndarray    # (n,) float32 -- routing weights
+    token_idx: np.ndarray
+    weights: np.ndarray
 
 
 def route_topk_device(scores, top_k: int, *, norm_topk_prob: bool = False,

@@ -45,7 +45,8 @@ def quantize(weight_fp16, is_bf16: bool = False):
     w = nat.to_device(weight_fp16)
     k, m = w.shape
     if m % 128 != 0:
-        raise ValueError(f"in-features m ({m}) must be a multiple of 128")
+        raise ValueError(f"quantize: the inline format packs 128-wide blocks; m={m} is not a "
+                         f"multiple of 128")
     want = t.bfloat16 if is_bf16 else t.float16
     if w.dtype != want:
         w = w.to(want)
@@ -53,7 +54,8 @@ def quantize(weight_fp16, is_bf16: bool = False):
     out = t.empty((k, per_row), dtype=t.uint8, device=w.device)
     rc = lib.fastllm_fp8_block128_quantize(nat.ptr(w), nat.ptr(out), k, m, 1 if is_bf16 else 0)
     if rc != 0:
-        raise RuntimeError(f"fastllm_fp8_block128_quantize failed (rc={rc})")
+        raise RuntimeError(f"quantize: the library refused the call (rc={rc}: 1 = arguments, "
+                           f"2/3 = device or launch)")
     return out
 
 
@@ -63,7 +65,8 @@ def fp8_gemv(x_fp16, weight_fp8_block128, scales=None, out=None, k=None):
     t = nat.torch()
     lib = _load()
     if scales is not None:
-        raise ValueError("FP8_E4M3_BLOCK_128 stores scales inline; pass scales=None")
+        raise ValueError("fp8_gemv: the inline format carries its own block scales, so "
+                         "`scales` must stay None")
     x = nat.to_device(x_fp16, t.float16)
     n, m = x.shape
     per_row = packed_row_bytes(m)
@@ -71,18 +74,21 @@ def fp8_gemv(x_fp16, weight_fp8_block128, scales=None, out=None, k=None):
     if w.dim() == 2:
         k = w.shape[0]
         if w.shape[1] != per_row:
-            raise ValueError(f"weight row bytes {w.shape[1]} != expected perRow {per_row}")
+            raise ValueError(f"fp8_gemv: weight rows hold {w.shape[1]} bytes; m={m} needs "
+                             f"{per_row}")
     else:
         if k is None:
-            raise ValueError("k must be given when weight is 1-D")
+            raise ValueError("fp8_gemv: a flat weight needs its row count k")
         if w.numel() != k * per_row:
-            raise ValueError("flat weight size does not match k*perRow")
+            raise ValueError(f"fp8_gemv: flat weight has {w.numel()} bytes, k={k} rows need "
+                             f"{k * per_row}")
     if out is None:
         out = t.empty((n, k), dtype=t.float16, device=x.device)
     rc = lib.fastllm_fp8_block128_gemv_fp16(nat.ptr(x), nat.ptr(w), nat.ptr(out), None, n, m, k,
                                             per_row)
     if rc != 0:
-        raise RuntimeError(f"fastllm_fp8_block128_gemv_fp16 failed (rc={rc})")
+        raise RuntimeError(f"fp8_gemv: the library refused the call (rc={rc}: 1 = arguments, "
+                           f"2/3 = device or launch)")
     return out
 
 

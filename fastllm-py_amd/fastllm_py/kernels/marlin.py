@@ -54,7 +54,7 @@ def pack_gptq_qweight(q_int4, xp=np):
     t = nat.torch()
     size_n, size_k = q_int4.shape
     assert size_k % 8 == 0, "size_k must be a multiple of 8"
-    numpy_in = isinstance(q_int4, np.ndarray)
+    numpy_in = nat.host_out(q_int4, xp)
     if numpy_in:
         q = nat.to_device(np.asarray(q_int4).astype(np.uint32))
     else:
@@ -76,7 +76,7 @@ def build_marlin_scales_zeros(scale, zero_int, group_size, xp=np):
     t = nat.torch()
     size_n, num_groups = scale.shape
     assert size_n % 64 == 0, "size_n must be a multiple of 64"
-    numpy_in = isinstance(scale, np.ndarray)
+    numpy_in = nat.host_out(scale, xp)
     s = nat.to_device(np.asarray(scale).astype(np.float32) if numpy_in else scale, t.float32)
     if isinstance(zero_int, np.ndarray):
         z = nat.to_device(np.asarray(zero_int).astype(np.int64).astype(np.int32))
@@ -116,7 +116,8 @@ def marlin_repack(std_qweight, size_k, size_n):
     ok = lib.FastllmCudaGptqMarlinRepack(nat.ptr(std), nat.ptr(out), int(size_k), int(size_n))
     t.cuda.synchronize()
     if not ok:
-        raise RuntimeError("FastllmCudaGptqMarlinRepack failed (check size_k/size_n tiling)")
+        raise RuntimeError(f"marlin_repack: the library refused size_k={size_k}, "
+                           f"size_n={size_n} (both must be multiples of 64)")
     return out
 
 
@@ -132,7 +133,8 @@ def marlin_unrepack(tile_qweight, size_k, size_n):
     return out
 
 
-_workspaces: dict = {}  # (device_id, size_n) -> zeroed int32 workspace
+# one zeroed workspace per (device ordinal, size_n), created on first use
+_workspaces: dict = {}
 
 
 def get_workspace(size_n: int):
@@ -269,11 +271,14 @@ def marlin_gemm_int4(a_fp16, packed_weights, scales, zeros, workspace=None, size
     group_size = size_k // num_groups
 
     if size_n % 64 != 0 or size_k % 64 != 0:
-        raise ValueError(f"size_n({size_n}) and size_k({size_k}) must be multiples of 64")
+        raise ValueError(f"marlin_gemm_int4: the tile layout needs size_n and size_k in "
+                         f"multiples of 64 (got {size_n}, {size_k})")
     if group_size not in (32, 128):
-        raise ValueError(f"group_size must be 32 or 128, got {group_size}")
+        raise ValueError(f"marlin_gemm_int4: groups of 32 or 128 only (size_k / groups = "
+                         f"{group_size})")
     if size_k % group_size != 0:
-        raise ValueError("size_k must be a multiple of group_size")
+        raise ValueError(f"marlin_gemm_int4: size_k={size_k} is not a whole number of "
+                         f"{group_size}-groups")
 
     scales = nat.to_device(scales, t.float16)
     zeros = nat.to_device(zeros)
@@ -287,6 +292,6 @@ def marlin_gemm_int4(a_fp16, packed_weights, scales, zeros, workspace=None, size
     if sync:
         t.cuda.synchronize()
     if not ok:
-        raise RuntimeError("FastllmCudaMarlinHalfInt4Gemm returned false "
-                           "(unsupported device or shape)")
+        raise RuntimeError("marlin_gemm_int4: the library refused the call (not a gfx950 "
+                           "device, or a shape its kernels do not take)")
     return c

@@ -45,7 +45,7 @@ def _rowmajor_device(W, group_size):
 def quantize_int4_rowmajor(w, group_size: int = 128, xp=np) -> dict:
     """RTN group INT4, row-major (moe_int4.py:24-40).  numpy in -> numpy arrays
     out (computed on the GPU); torch in -> device tensors."""
-    numpy_in = isinstance(w, np.ndarray) or xp is np and not nat.is_tensor(w)
+    numpy_in = nat.host_out(w, xp)
     qw, sc, ze = _rowmajor_device(np.asarray(w) if numpy_in else w, group_size)
     out_f, in_f = qw.shape[0], qw.shape[1] * 2
     return {"qweight": nat.as_output(qw, numpy_in), "scales": nat.as_output(sc, numpy_in),
@@ -55,7 +55,7 @@ def quantize_int4_rowmajor(w, group_size: int = 128, xp=np) -> dict:
 def dequantize_int4_rowmajor(payload, xp=np):
     """(q - zero) * scale -> fp32 (moe_int4.py:43-54)."""
     t = nat.torch()
-    numpy_in = isinstance(payload["qweight"], np.ndarray)
+    numpy_in = nat.host_out(payload["qweight"], xp)
     qw = nat.to_device(payload["qweight"], t.uint8)
     sc = nat.to_device(payload["scales"], t.float16)
     ze = nat.to_device(payload["zeros"], t.float16)

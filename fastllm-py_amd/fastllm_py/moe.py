@@ -61,3 +61,26 @@ def build_marlin_expert_payload(w_fp16: dict, group_size: int = 128) -> dict:
         for k, v in quantize_marlin_matrix(w, group_size).items():
             payload[f"{proj}.{k}"] = v
     return payload
+
+
+def _expert_ffn_marlin(x_fp16, w, stream=None):
+    """One expert's FFN on its Marlin payload for the rows routed to it
+    (moe.py:62-81): gate and up GEMMs, swiglu, down GEMM.  ``w`` is the flat
+    payload of ``build_marlin_expert_payload`` on the device ("gate.qweight",
+    "gate.scales", ..., "down.zeros"); x (n, hidden) fp16.  Every step runs
+    in this library on ``stream`` (None: the current stream), with no
+    per-call validation, as the reference's hot loop expects.  Returns
+    (n, hidden) fp16."""
+    from .kernels import ops
+
+    if stream is None:  # one stream for all four launches
+        stream = nat.current_stream_handle()
+    hidden = x_fp16.shape[1]
+    inter = w["gate.scales"].shape[1]
+    g = marlin.gemm_fast(x_fp16, w["gate.qweight"], w["gate.scales"], w["gate.zeros"], inter,
+                         hidden, stream=stream)
+    u = marlin.gemm_fast(x_fp16, w["up.qweight"], w["up.scales"], w["up.zeros"], inter, hidden,
+                         stream=stream)
+    act = ops.swiglu(g, u, stream=stream)
+    return marlin.gemm_fast(act, w["down.qweight"], w["down.scales"], w["down.zeros"], hidden,
+                            inter, stream=stream)

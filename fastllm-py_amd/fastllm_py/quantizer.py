@@ -18,12 +18,20 @@ FP8_E4M3_MAX = 448.0
 
 @dataclass
 class QuantizedTensor:
-    kind: str  # "fp8_e4m3_block" | "int4_group"
-    data: object  # uint8 array (numpy or torch)
-    scales: object  # float array
-    shape: tuple[int, int]  # original (out_features, in_features)
+    """A packed weight.  Fields keep the reference's names and order (its
+    loaders construct and read them positionally): ``kind`` names the format,
+    "fp8_e4m3_block" or "int4_group"; ``data`` holds the packed codes as
+    uint8 (numpy or a device tensor); ``scales`` the float32 scale per block
+    or group; ``shape`` the unpacked (out_features, in_features);
+    ``block_size`` the block edge or group length; ``zeros`` the int4 group
+    minimum (None for fp8)."""
+
+    kind: str
+    data: object
+    scales: object
+    shape: tuple[int, int]
     block_size: int
-    zeros: object = None  # int4 only
+    zeros: object = None
 
 
 def _f32_device(x):
@@ -37,7 +45,7 @@ def _fp8_e4m3_encode(x, xp=np):
     """float array -> uint8 e4m3fn bytes, the reference encoder
     (quantizer.py:26-51, including its subnormal clip-to-7)."""
     t = nat.torch()
-    numpy_in = isinstance(x, np.ndarray) or np.isscalar(x)
+    numpy_in = nat.host_out(x, xp)
     xd = _f32_device(np.asarray(x) if numpy_in else x)
     out = t.empty(xd.shape, dtype=t.uint8, device=xd.device)
     rc = nat.lib().fastllm_fp8_e4m3_encode(nat.ptr(xd), nat.ptr(out), xd.numel(),
@@ -49,7 +57,7 @@ def _fp8_e4m3_encode(x, xp=np):
 def _fp8_e4m3_decode(b, xp=np):
     """uint8 e4m3fn -> float32, exact (quantizer.py:54-62)."""
     t = nat.torch()
-    numpy_in = isinstance(b, np.ndarray)
+    numpy_in = nat.host_out(b, xp)
     bd = nat.to_device(np.asarray(b).astype(np.uint8) if numpy_in else b, t.uint8)
     out = t.empty(bd.shape, dtype=t.float32, device=bd.device)
     rc = nat.lib().fastllm_fp8_e4m3_decode(nat.ptr(bd), nat.ptr(out), bd.numel(),
@@ -64,7 +72,7 @@ def quantize_fp8_block(w, block_size: int = 128, xp=np) -> QuantizedTensor:
     w: (out_features, in_features). scales: (ceil(out/bs), ceil(in/bs)) fp32;
     data cropped to (out, in) uint8."""
     t = nat.torch()
-    numpy_in = isinstance(w, np.ndarray)
+    numpy_in = nat.host_out(w, xp)
     wd = _f32_device(w)
     out_f, in_f = wd.shape
     bs = int(block_size)
@@ -81,7 +89,7 @@ def quantize_fp8_block(w, block_size: int = 128, xp=np) -> QuantizedTensor:
 def dequantize_fp8_block(qt: QuantizedTensor, xp=np):
     """decode(q) * block scale (quantizer.py:88-94)."""
     t = nat.torch()
-    numpy_in = isinstance(qt.data, np.ndarray)
+    numpy_in = nat.host_out(qt.data, xp)
     out_f, in_f = qt.shape
     q = nat.to_device(qt.data, t.uint8)
     s = _f32_device(qt.scales)
@@ -97,7 +105,7 @@ def quantize_int4_group(w, group_size: int = 128, xp=np) -> QuantizedTensor:
     (quantizer.py:97-117).  data (out, in/2) uint8, even column in the low
     nibble; scales and zeros (= group minimum) (out, in/group) float32."""
     t = nat.torch()
-    numpy_in = isinstance(w, np.ndarray)
+    numpy_in = nat.host_out(w, xp)
     wd = _f32_device(w)
     out_f, in_f = wd.shape
     assert in_f % group_size == 0 and in_f % 2 == 0
@@ -116,7 +124,7 @@ def quantize_int4_group(w, group_size: int = 128, xp=np) -> QuantizedTensor:
 def dequantize_int4_group(qt: QuantizedTensor, xp=np):
     """q * scale + zero (quantizer.py:120-129)."""
     t = nat.torch()
-    numpy_in = isinstance(qt.data, np.ndarray)
+    numpy_in = nat.host_out(qt.data, xp)
     out_f, in_f = qt.shape
     p = nat.to_device(qt.data, t.uint8)
     s = _f32_device(qt.scales)

@@ -25,6 +25,21 @@ def _experts(rng, E, hidden, inter, scale=0.1):
             for _ in range(E)]
 
 
+def _stacked(experts, gs):
+    """The product's stacked experts, and the oracle's own row-major
+    quantization (quantize_int4_rowmajor restated in oracle/quant.py) of the
+    same fp16 weights -- what the oracle dequantizes.  The product's tile
+    pack of those bytes is pinned separately (test_moe_tile_pack_bit_exact)."""
+    from fastllm_py.kernels import moe_int4
+
+    st = moe_int4.build_stacked_experts(experts, gs)
+    orc = {}
+    for proj in ("gate", "up", "down"):
+        p, s_, z = Q.quantize_int4_rowmajor(np.stack([e[proj] for e in experts]), gs)
+        orc.update({f"{proj}.qweight": p, f"{proj}.scales": s_, f"{proj}.zeros": z})
+    return st, orc
+
+
 def _np_stacked(st):
     """Tile-layout stacked experts -> row-major numpy arrays for the oracle."""
     from fastllm_py.kernels import moe_int4
@@ -287,13 +302,13 @@ def test_fused_moe_matches_reference(torch_gpu, E, K, hidden, inter, gs):
     x = (rng.standard_normal(hidden) * 0.5).astype(np.float32)
     eidx = rng.choice(E, size=K, replace=False).astype(np.int32)
     rw = (rng.random(K) + 0.1).astype(np.float32)
-    stacked = moe_int4.build_stacked_experts(experts, gs)
+    stacked, stacked_o = _stacked(experts, gs)
     xd = torch.from_numpy(x).cuda()
     y = moe_int4.fused_moe_ffn(xd, stacked, torch.from_numpy(eidx).cuda(),
                                torch.from_numpy(rw).cuda(), hidden, inter).cpu().numpy()
     y2 = moe_int4.fused_moe_ffn2(xd, stacked, torch.from_numpy(eidx).cuda(),
                                  torch.from_numpy(rw).cuda(), hidden, inter).cpu().numpy()
-    deq = OM.dequant_stacked(_np_stacked(stacked), gs)
+    deq = OM.dequant_stacked(stacked_o, gs)
     ref = OM.moe_ref(x[None], deq, eidx[None], rw[None])[0]
     assert Q.max_abs_rel(y, ref) < 5e-3
     assert Q.max_abs_rel(y2, y) < 1e-6  # same kernels; fp32 atomics may reorder the sum
@@ -306,7 +321,7 @@ def test_fused_moe_weighted_matches_index_version(torch_gpu):
     torch = torch_gpu
     rng = np.random.default_rng(4)
     E, K, hidden, inter, gs = 60, 4, 512, 1408, 128
-    stacked = moe_int4.build_stacked_experts(_experts(rng, E, hidden, inter), gs)
+    stacked, stacked_o = _stacked(_experts(rng, E, hidden, inter), gs)
     x = torch.from_numpy((rng.standard_normal(hidden) * 0.3).astype(np.float32)).cuda()
     eidx = np.sort(rng.choice(E, K, replace=False)).astype(np.int32)
     w = (rng.random(K) + 0.1).astype(np.float32)
@@ -327,8 +342,8 @@ def _qwen15_layer(torch, rng, E=60, hidden=2048, inter=1408, sinter=5632):
 
     experts = _experts(rng, E, hidden, inter, 0.02)
     shared = _experts(rng, 1, hidden, sinter, 0.02)
-    st = moe_int4.build_stacked_experts(experts, 128)
-    sh = moe_int4.build_stacked_experts(shared, 128)
+    st, st_o = _stacked(experts, 128)
+    sh, sh_o = _stacked(shared, 128)
     sgw = (rng.standard_normal((1, hidden)) * 0.02).astype(np.float16)
     gw = (rng.standard_normal((E, hidden)) * 0.02).astype(np.float16)
     return st, sh, sgw, gw
@@ -358,8 +373,8 @@ def test_moe_layer_config4(torch_gpu, T):
                              max_entries=4 * T, shared=sh, shared_inter=sinter,
                              shared_coef=r["shared_coef"])
     coef = 1.0 / (1.0 + np.exp(-sl.reshape(-1).cpu().numpy()))
-    ref = OM.moe_ref(x, OM.dequant_stacked(_np_stacked(st), 128), g["idx_canonical"],
-                     g["w_canonical"], OM.dequant_stacked(_np_stacked(sh), 128), coef)
+    ref = OM.moe_ref(x, OM.dequant_stacked(st_o, 128), g["idx_canonical"],
+                     g["w_canonical"], OM.dequant_stacked(sh_o, 128), coef)
     assert Q.max_abs_rel(y.cpu().numpy(), ref) < 1e-2
     assert Q.max_abs_rel(y.cpu().numpy(), ref) < 5e-3
 
@@ -373,8 +388,8 @@ def test_moe_branch_graph_capture(torch_gpu):
     torch = torch_gpu
     rng = np.random.default_rng(5)
     E, K, hidden, inter, sinter = 60, 4, 512, 512, 1024
-    st = moe_int4.build_stacked_experts(_experts(rng, E, hidden, inter), 128)
-    sh = moe_int4.build_stacked_experts(_experts(rng, 1, hidden, sinter), 128)
+    st, st_o = _stacked(_experts(rng, E, hidden, inter), 128)
+    sh, sh_o = _stacked(_experts(rng, 1, hidden, sinter), 128)
     gw = torch.from_numpy((rng.standard_normal((E, hidden)) * 0.1).astype(np.float16)).cuda()
     sgw = torch.from_numpy((rng.standard_normal((1, hidden)) * 0.1).astype(np.float16)).cuda()
     x = torch.from_numpy((rng.standard_normal((1, hidden)) * 0.5).astype(np.float32)).cuda()
@@ -415,8 +430,8 @@ def test_fused_moe_shapes(torch_gpu, T, E, K, hidden, inter, sinter, gs):
 
     torch = torch_gpu
     rng = np.random.default_rng(T * 7 + hidden)
-    st = moe_int4.build_stacked_experts(_experts(rng, E, hidden, inter, 0.05), gs)
-    sh = moe_int4.build_stacked_experts(_experts(rng, 1, hidden, sinter, 0.05), gs) if sinter else None
+    st, st_o = _stacked(_experts(rng, E, hidden, inter, 0.05), gs)
+    sh, sh_o = _stacked(_experts(rng, 1, hidden, sinter, 0.05), gs) if sinter else (None, None)
     x = (rng.standard_normal((T, hidden)) * 0.5).astype(np.float32)
     logits = rng.standard_normal((T, E)).astype(np.float32)
     sl = rng.standard_normal(T).astype(np.float32)
@@ -430,8 +445,8 @@ def test_fused_moe_shapes(torch_gpu, T, E, K, hidden, inter, sinter, gs):
     assert Q.max_abs_rel(y2.cpu().numpy(), y.cpu().numpy()) < 1e-6
     ids, w = r["topk_ids"].cpu().numpy(), r["topk_w"].cpu().numpy()
     coef = 1.0 / (1.0 + np.exp(-sl)) if sinter else None
-    ref = OM.moe_ref(x, OM.dequant_stacked(_np_stacked(st), gs), ids, w,
-                     OM.dequant_stacked(_np_stacked(sh), gs) if sh else None, coef)
+    ref = OM.moe_ref(x, OM.dequant_stacked(st_o, gs), ids, w,
+                     OM.dequant_stacked(sh_o, gs) if sh else None, coef)
     assert Q.max_abs_rel(y.cpu().numpy(), ref) < 5e-3
 
 
@@ -455,8 +470,8 @@ def test_moe_route_forward(torch_gpu, T, E, K, hidden, inter, sinter, gs, norm):
 
     torch = torch_gpu
     rng = np.random.default_rng(9000 + T * 13 + E + hidden)
-    st = moe_int4.build_stacked_experts(_experts(rng, E, hidden, inter, 0.05), gs)
-    sh = moe_int4.build_stacked_experts(_experts(rng, 1, hidden, sinter, 0.05), gs) if sinter else None
+    st, st_o = _stacked(_experts(rng, E, hidden, inter, 0.05), gs)
+    sh, sh_o = _stacked(_experts(rng, 1, hidden, sinter, 0.05), gs) if sinter else (None, None)
     x = torch.from_numpy((rng.standard_normal((T, hidden)) * 0.5).astype(np.float32)).cuda()
     logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float16).astype(np.float32)).cuda()
     sl = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).cuda() if sinter else None
@@ -466,8 +481,8 @@ def test_moe_route_forward(torch_gpu, T, E, K, hidden, inter, sinter, gs, norm):
                               shared_coef=ref_r.get("shared_coef"))
     ids, w = ref_r["topk_ids"].cpu().numpy(), ref_r["topk_w"].cpu().numpy()
     coef = 1.0 / (1.0 + np.exp(-sl.cpu().numpy())) if sinter else None
-    ref = OM.moe_ref(x.cpu().numpy(), OM.dequant_stacked(_np_stacked(st), gs), ids, w,
-                     OM.dequant_stacked(_np_stacked(sh), gs) if sh else None, coef)
+    ref = OM.moe_ref(x.cpu().numpy(), OM.dequant_stacked(st_o, gs), ids, w,
+                     OM.dequant_stacked(sh_o, gs) if sh else None, coef)
     s2 = torch.cuda.Stream()
     for call in range(4):
         stream = s2 if call == 3 else None
@@ -508,8 +523,8 @@ def test_moe_route_forward_sigmoid_groups(torch_gpu, T):
     kw = dict(norm_topk_prob=True, scoring="sigmoid", routed_scaling=2.5,
               e_score_bias=torch.from_numpy((rng.standard_normal(E) * 0.1).astype(np.float32)).cuda(),
               n_group=8, topk_group=3)
-    st = moe_int4.build_stacked_experts(_experts(rng, E, hidden, inter, 0.05), gs)
-    sh = moe_int4.build_stacked_experts(_experts(rng, 1, hidden, sinter, 0.05), gs)
+    st, st_o = _stacked(_experts(rng, E, hidden, inter, 0.05), gs)
+    sh, sh_o = _stacked(_experts(rng, 1, hidden, sinter, 0.05), gs)
     x = torch.from_numpy((rng.standard_normal((T, hidden)) * 0.5).astype(np.float32)).cuda()
     logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float32)).cuda()
     sl = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).cuda()
@@ -583,8 +598,8 @@ def test_fused_moe_edge_lists(torch_gpu):
     torch = torch_gpu
     rng = np.random.default_rng(12)
     E, hidden, inter = 6, 256, 384
-    st = moe_int4.build_stacked_experts(_experts(rng, E, hidden, inter), 128)
-    deq = OM.dequant_stacked(_np_stacked(st), 128)
+    st, st_o = _stacked(_experts(rng, E, hidden, inter), 128)
+    deq = OM.dequant_stacked(st_o, 128)
     x = (rng.standard_normal(hidden) * 0.5).astype(np.float32)
     xd = torch.from_numpy(x).cuda()
     eidx = np.array([3, 1, 3, 5], np.int32)
@@ -612,8 +627,8 @@ def test_fused_moe_prefill(torch_gpu, T, E, K, hidden, inter, sinter, gs, norm):
 
     torch = torch_gpu
     rng = np.random.default_rng(T * 13 + hidden + E)
-    st = moe_int4.build_stacked_experts(_experts(rng, E, hidden, inter, 0.05), gs)
-    sh = moe_int4.build_stacked_experts(_experts(rng, 1, hidden, sinter, 0.05), gs) if sinter else None
+    st, st_o = _stacked(_experts(rng, E, hidden, inter, 0.05), gs)
+    sh, sh_o = _stacked(_experts(rng, 1, hidden, sinter, 0.05), gs) if sinter else (None, None)
     x = (rng.standard_normal((T, hidden)) * 0.5).astype(np.float32)
     logits = rng.standard_normal((T, E)).astype(np.float16).astype(np.float32)
     sl = rng.standard_normal(T).astype(np.float32)
@@ -626,8 +641,8 @@ def test_fused_moe_prefill(torch_gpu, T, E, K, hidden, inter, sinter, gs, norm):
     assert Q.max_abs_rel(y2.cpu().numpy(), y.cpu().numpy()) < 1e-6
     ids, w = r["topk_ids"].cpu().numpy(), r["topk_w"].cpu().numpy()
     coef = 1.0 / (1.0 + np.exp(-sl)) if sinter else None
-    ref = OM.moe_ref_grouped(x, OM.dequant_stacked(_np_stacked(st), gs), ids, w,
-                             OM.dequant_stacked(_np_stacked(sh), gs) if sh else None, coef)
+    ref = OM.moe_ref_grouped(x, OM.dequant_stacked(st_o, gs), ids, w,
+                             OM.dequant_stacked(sh_o, gs) if sh else None, coef)
     assert Q.max_abs_rel(y.cpu().numpy(), ref) < 5e-3
 
 
@@ -644,7 +659,7 @@ def test_moe_prefill_config5(torch_gpu):
     T, E, K, hidden, inter = 512, 128, 8, 2048, 768
     rng = np.random.default_rng(5512)
     experts = _experts(rng, E, hidden, inter, 0.02)
-    st = moe_int4.build_stacked_experts(experts, 128)
+    st, st_o = _stacked(experts, 128)
     del experts
     x = rng.standard_normal((T, hidden)).astype(np.float16).astype(np.float32)
     r = route_topk_device(g["logits"], K, norm_topk_prob=True)
@@ -654,5 +669,5 @@ def test_moe_prefill_config5(torch_gpu):
     np.testing.assert_array_equal(w.view(np.uint32), g["w_canonical"].view(np.uint32))
     y = moe_int4.moe_forward(torch.from_numpy(x).cuda(), st, E, hidden, inter, r,
                              max_slots=E, max_entries=T * K)
-    ref = OM.moe_ref_grouped(x, OM.dequant_stacked(_np_stacked(st), 128), ids, w)
+    ref = OM.moe_ref_grouped(x, OM.dequant_stacked(st_o, 128), ids, w)
     assert Q.max_abs_rel(y.cpu().numpy(), ref) < 5e-3
