@@ -473,6 +473,124 @@ FL_DEV float np_sum_wave128(const float* a, int n, int lane, float v0, float v1)
     return res;
 }
 
+// ---- numpy's argpartition tie order (float32 rows of <= 256 elements)
+// numpy 2.x sends a single-kth float32 argpartition on an AVX512_SKX host to
+// x86-simd-sort, which fully sorts rows of <= 256 elements with a bitonic
+// key/index network on 8-lane registers: pad to maxN = max(8, next power of
+// two) with +inf keys and index 0; sort each 8-lane register (6 steps); merge
+// registers in groups of 2, 4, .. maxN/8 (register i against register n-1-i
+// read lane-reversed, half-cleaners across registers, then each register's
+// 3-step in-lane merge).  A step keeps the max where the lane's mask bit is
+// set, else the min, and a lane whose result equals its own key keeps its own
+// index, so equal keys never trade places and ties end where the wiring puts
+// them.  The selection of argpartition(keys, k-1)[:k] is the first k
+// positions.  Here position x = 64 c + lane sits in slot c of the lane;
+// partners come through ds_bpermute (the partner slot is uniform per slot
+// and step).  Used only for rows with a tied maximum in some top-k round.
+FL_DEV float bperm_f(float v, int src_lane) {
+    return bitcast<float>(__builtin_amdgcn_ds_bpermute(src_lane << 2, bitcast<int>(v)));
+}
+
+// One network step.  part(c, &pc, &pl, &mx): partner slot pc (uniform) and
+// lane pl of this lane's slot-c position, mx = keep the max.
+template <typename Part>
+FL_DEV void net_step(float (&kf)[4], int (&ix)[4], int nsl, Part part) {
+    float nk[4];
+    int ni[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        nk[c] = kf[c];
+        ni[c] = ix[c];
+        if (c < nsl) {
+            int pc, pl;
+            bool mx;
+            part(c, pc, pl, mx);
+            const float sk = pc == 0 ? kf[0] : pc == 1 ? kf[1] : pc == 2 ? kf[2] : kf[3];
+            const int si = pc == 0 ? ix[0] : pc == 1 ? ix[1] : pc == 2 ? ix[2] : ix[3];
+            const float ok = bperm_f(sk, pl);
+            const int oi = __builtin_amdgcn_ds_bpermute(pl << 2, si);
+            const float r = mx ? fmaxf(kf[c], ok) : fminf(kf[c], ok);
+            nk[c] = r;
+            ni[c] = r == kf[c] ? ix[c] : oi;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        kf[c] = nk[c];
+        ix[c] = ni[c];
+    }
+}
+
+// In-register step: partner lane l -> perm(l) inside each 8-lane register,
+// max where `mask` has bit l.
+template <typename Perm>
+FL_DEV void net_lane_step(float (&kf)[4], int (&ix)[4], int nsl, int lane, Perm perm, int mask) {
+    const int l = lane & 7;
+    const int pl = (lane & ~7) | perm(l);
+    const bool mx = (mask >> l) & 1;
+    net_step(kf, ix, nsl, [&](int c, int& pc, int& plo, bool& m) {
+        pc = c;
+        plo = pl;
+        m = mx;
+    });
+}
+
+// Full network over maxN (8..256) positions held as described above.
+FL_DEV void net_argsort(float (&kf)[4], int (&ix)[4], int maxN, int lane) {
+    const int nsl = (maxN + 63) >> 6;
+    const int nv = maxN >> 3;
+    auto sort8 = [&]() {
+        net_lane_step(kf, ix, nsl, lane, [](int l) { return l ^ 1; }, 0xAA);
+        net_lane_step(kf, ix, nsl, lane, [](int l) { return (l & 4) | (3 - (l & 3)); }, 0xCC);
+        net_lane_step(kf, ix, nsl, lane, [](int l) { return l ^ 1; }, 0xAA);
+        net_lane_step(kf, ix, nsl, lane, [](int l) { return 7 - l; }, 0xF0);
+        net_lane_step(kf, ix, nsl, lane, [](int l) { return l ^ 2; }, 0xCC);
+        net_lane_step(kf, ix, nsl, lane, [](int l) { return l ^ 1; }, 0xAA);
+    };
+    sort8();
+    const int l = lane & 7;
+    for (int n = 2; n <= nv; n <<= 1) {
+        // register R against register g + n - 1 - (R - g), lanes reversed
+        net_step(kf, ix, nsl, [&](int c, int& pc, int& pl, bool& mx) {
+            const int R = 8 * c + (lane >> 3);
+            const int g = R & ~(n - 1), a = R - g;
+            const int R2 = g + n - 1 - a;
+            mx = a >= (n >> 1);
+            pc = R2 >> 3;
+            pl = ((R2 & 7) << 3) | (7 - l);
+        });
+        for (int m = n >> 1; m >= 2; m >>= 1) {
+            const int d = m >> 1;
+            net_step(kf, ix, nsl, [&](int c, int& pc, int& pl, bool& mx) {
+                const int R = 8 * c + (lane >> 3);
+                const bool hi = (R % m) >= d;
+                const int R2 = hi ? R - d : R + d;
+                mx = hi;
+                pc = R2 >> 3;
+                pl = ((R2 & 7) << 3) | l;
+            });
+        }
+        net_lane_step(kf, ix, nsl, lane, [](int q) { return q ^ 4; }, 0xF0);
+        net_lane_step(kf, ix, nsl, lane, [](int q) { return q ^ 2; }, 0xCC);
+        net_lane_step(kf, ix, nsl, lane, [](int q) { return q ^ 1; }, 0xAA);
+    }
+}
+
+// Keys -v (numpy's -select) of n values (lane + 64 c), padded to the
+// network's size, sorted; returns maxN.
+FL_DEV int net_load_sort(const float (&v)[4], int n, int lane, float (&kf)[4], int (&ix)[4]) {
+    int maxN = 8;
+    while (maxN < n) maxN <<= 1;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const int x = lane + 64 * c;
+        kf[c] = x < n ? -v[c] : __builtin_inff();
+        ix[c] = x < n ? x : 0;
+    }
+    net_argsort(kf, ix, maxN, lane);
+    return maxN;
+}
+
 // Route token t with one wave.  `exw` is the wave's 256-float LDS row.
 // Lane i < K ends with the i-th selection (expert `my_id`, final weight
 // `my_w`), which it also stores to sids/sws[tl*K + i] and, when `store`, to
@@ -561,13 +679,23 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
             }
             gscore = gsz >= 2 ? (0.0f + b2) + b1 : 0.0f + b1;
         }
-        // keep topk_group groups: rank = #groups strictly better (ties -> lower index)
-        int rank = 0;
+        // keep topk_group groups: rank = #groups strictly better; tied
+        // group scores take numpy's argpartition order (the network)
+        int rank = 0, same = 0;
         for (int g2 = 0; g2 < a.n_group; ++g2) {
             const float o = __shfl(gscore, g2, 64);
             rank += (o > gscore || (o == gscore && g2 < lane)) ? 1 : 0;
+            same += (o == gscore && g2 != lane) ? 1 : 0;
         }
-        const int keep = (lane < a.n_group && rank < a.topk_group) ? 1 : 0;
+        int keep = (lane < a.n_group && rank < a.topk_group) ? 1 : 0;
+        if (__ballot(lane < a.n_group && same > 0)) {
+            float gv[4] = {gscore, 0.f, 0.f, 0.f}, kf[4];
+            int ix[4];
+            net_load_sort(gv, a.n_group, lane, kf, ix);
+            unsigned long long km = 0ull;
+            for (int j = 0; j < a.topk_group; ++j) km |= 1ull << __builtin_amdgcn_readlane(ix[0], j);
+            keep = (lane < a.n_group && ((km >> lane) & 1ull)) ? 1 : 0;
+        }
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int e = lane + 64 * c;
@@ -586,14 +714,16 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
     }
     my_id = 0;
     my_w = 0.f;
+    bool tie = false;  // some round's maximum held by more than one expert
     for (int i = 0; i < K; ++i) {
         const uint32_t m = wave_umax(umax4(key[0], key[1], key[2], key[3]));
-        int e = 0;
+        int e = 0, holders = 0;
         float w = 0.f;
 #pragma unroll
         for (int c = 3; c >= 0; --c) {  // the lowest slot c holding m wins
             if (c < nc) {
                 const unsigned long long bm = __ballot(key[c] == m);
+                holders += __builtin_popcountll(bm);
                 if (bm) {
                     const int l = __builtin_ctzll(bm);
                     e = 64 * c + l;
@@ -601,6 +731,7 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
                 }
             }
         }
+        tie |= holders > 1;
 #pragma unroll
         for (int c = 0; c < 4; ++c)
             if (lane + 64 * c == e) key[c] = 0u;
@@ -608,6 +739,26 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
             my_id = e;
             my_w = w;
         }
+    }
+    if (tie) {
+        // numpy's argpartition(-select)[:K]: the set at a tied k-th value and
+        // the order of tied picks (which the weight sum follows) come from
+        // its network
+        float kf[4];
+        int ix[4];
+        float sv[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sv[c] = sel[c];
+        net_load_sort(sv, E, lane, kf, ix);
+        my_id = ix[0];
+        float w = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float pc = bperm_f(p[c], my_id & 63);
+            if (c < nc && (my_id >> 6) == c) w = pc;
+        }
+        my_w = lane < K ? w : 0.f;
+        if (lane >= K) my_id = 0;
     }
     if (a.norm) {
         // numpy row sum of the k weights (selection order), + 1e-20: below 8

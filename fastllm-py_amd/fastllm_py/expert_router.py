@@ -7,8 +7,9 @@ renormalisation and routed scaling; returns one ``ExpertTask`` per activated
 expert, experts ascending, tokens ascending within an expert.  Scores run in
 the HIP router (csrc/moe_int4.hip), which evaluates numpy's float32 exp and
 pairwise sums exactly, so probabilities and weights are bit-identical to the
-reference's numpy.  Ties at the k-th selection value go to the lowest expert
-index (numpy's argpartition leaves that choice to its partition algorithm).
+reference's numpy.  Where experts tie, the selection and its order are those
+of np.argpartition as numpy 2.x runs it on an AVX512_SKX host (x86-simd-sort's
+bitonic key/index network, simulated in the router for tied rows).
 
 ``route_topk_device`` returns the device tensors the fused MoE kernels and
 graph-captured decode consume.

@@ -344,7 +344,9 @@ int fastllm_gate_matvec(const float *x, const void *gate_w,
  * float32 exp/sum arithmetic: scoring 0 = softmax, 1 = sigmoid (+ optional
  * e_score_bias[E] on the selection value); n_group/topk_group = DeepSeek
  * group-limited selection; norm = renormalise over the k weights (+1e-20);
- * times routed_scaling.  Ties at the k-th value go to the lower expert index.
+ * times routed_scaling.  Selection and order follow np.argpartition as numpy
+ * 2.x runs it for float32 rows of <= 256 on an AVX512_SKX host (its bitonic
+ * key/index network decides ties).
  * Outputs: topk_ids/topk_w [T, top_k] (descending selection), optional dense
  * rw [T, E]; optional shared_coef[T] = sigmoid(shared_logit); optional
  * expert-major MoE lists (all or none): n_active[1], active[E] ascending,

@@ -7,16 +7,19 @@ so the oracle gives the same probabilities on any host, whichever SIMD path
 that host's numpy dispatches.
 
 Selection: the reference calls np.argpartition, whose choice among values
-tied at the k-th position (and whose output order) is an implementation detail
-of numpy's partition.  ``route_topk`` here calls np.argpartition exactly like
-the reference; ``route_topk_canonical`` breaks ties by lowest expert index and
-lists a token's experts by descending selection value — the GPU router's
-documented rule.  The two agree on every token without a tie at the k-th
-value (``boundary_ties`` reports those tokens), and their weights agree bit for
-bit except that norm_topk_prob sums the k weights in a different order.
+tied at the k-th position (and whose output order) is left to numpy's
+selection algorithm.  ``route_topk`` here takes it from
+``oracle/argpartition.py``, the restatement of that algorithm as numpy 2.2.6
+runs it on an AVX512_SKX host (x86-simd-sort's key/index network), pinned
+against the installed np.argpartition in tests/test_oracle_argpartition.py,
+so the oracle selects the same experts as the reference on any host.
+``route_topk_canonical`` breaks ties by lowest expert index instead (a
+reference point for the tests: the two agree on every token without a tie,
+which ``boundary_ties`` reports).
 
-Pins: the reference's known answers (tests/test_router.py:36-64) and brute
-force (sort-based selection) on tie-free inputs.
+Pins: the reference's known answers (tests/test_router.py:36-64), brute
+force (sort-based selection) on tie-free inputs, and np.argpartition itself
+on tie-heavy rows.
 """
 from __future__ import annotations
 
@@ -25,6 +28,8 @@ import os
 from dataclasses import dataclass
 
 import numpy as np
+
+from .argpartition import argpartition_rows
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _lib = None
@@ -93,7 +98,7 @@ def _group_mask(select, n_group, topk_group, canonical):
         order = np.lexsort((np.broadcast_to(np.arange(n_group), group_score.shape), -group_score), axis=-1)
         keep = order[:, :topk_group]
     else:
-        keep = np.argpartition(-group_score, topk_group - 1, axis=-1)[:, :topk_group]
+        keep = argpartition_rows(-group_score, topk_group - 1)[:, :topk_group]
     masked = np.ones((T, n_group), dtype=bool)
     np.put_along_axis(masked, keep, False, axis=-1)
     return np.where(np.repeat(masked, gsz, axis=1), np.float32(-np.inf), select)
@@ -121,11 +126,12 @@ def _finish(probs, topk_idx, top_k, norm_topk_prob, routed_scaling):
 
 def route_topk(scores, top_k, *, norm_topk_prob=False, scoring="softmax", routed_scaling=1.0,
                e_score_bias=None, n_group=0, topk_group=0, return_arrays=False):
-    """fastllm_py/expert_router.py:22-71 with np.argpartition selection."""
+    """fastllm_py/expert_router.py:22-71, with np.argpartition's selection
+    (fastllm_py/expert_router.py:50,55) restated for rows of <= 256 experts."""
     probs, select = _scores(scores, scoring, e_score_bias)
     if n_group and n_group > 1 and 0 < topk_group < n_group:
         select = _group_mask(select, n_group, topk_group, canonical=False)
-    topk_idx = np.argpartition(-select, top_k - 1, axis=-1)[:, :top_k]
+    topk_idx = argpartition_rows(-select, top_k - 1)[:, :top_k]
     out = _finish(probs, topk_idx, top_k, norm_topk_prob, routed_scaling)
     return out if return_arrays else out[0]
 

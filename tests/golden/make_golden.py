@@ -27,14 +27,33 @@ def routing():
         "deepseek_t32": dict(seed=6000, T=32, E=64, k=8, norm=True, scoring="sigmoid",
                              n_group=8, topk_group=4, scale=2.5),
     }
+    # tie-heavy rows: fp16 logits (and biases) from a few distinct values, so
+    # many tokens hold experts tied at the k-th selection value
+    ties = {
+        "ties_e60_k4": dict(seed=7001, T=96, E=60, k=4, norm=False, scoring="softmax", levels=6),
+        "ties_e128_k8": dict(seed=7002, T=96, E=128, k=8, norm=True, scoring="softmax", levels=8),
+        "ties_e256_k16": dict(seed=7003, T=48, E=256, k=16, norm=True, scoring="softmax",
+                              levels=12),
+        "ties_groups": dict(seed=7004, T=64, E=64, k=8, norm=True, scoring="sigmoid", n_group=8,
+                            topk_group=4, scale=2.5, levels=4),
+    }
+    cases.update(ties)
     for name, c in cases.items():
         rng = np.random.default_rng(c["seed"])
-        logits = rng.standard_normal((c["T"], c["E"])).astype(np.float16)
-        bias = (rng.standard_normal(c["E"]) * 0.1).astype(np.float32) if c["scoring"] == "sigmoid" else None
+        if "levels" in c:
+            vals = rng.standard_normal(c["levels"]).astype(np.float16)
+            logits = vals[rng.integers(0, c["levels"], size=(c["T"], c["E"]))]
+            bias = (vals[rng.integers(0, c["levels"], size=c["E"])].astype(np.float32) * 0.1
+                    if c["scoring"] == "sigmoid" else None)
+        else:
+            logits = rng.standard_normal((c["T"], c["E"])).astype(np.float16)
+            bias = (rng.standard_normal(c["E"]) * 0.1).astype(np.float32) if c["scoring"] == "sigmoid" else None
         kw = dict(norm_topk_prob=c["norm"], scoring=c["scoring"], routed_scaling=c.get("scale", 1.0),
                   e_score_bias=bias, n_group=c.get("n_group", 0), topk_group=c.get("topk_group", 0))
         s32 = logits.astype(np.float32)
         _, ia, wa = R.route_topk(s32, c["k"], return_arrays=True, **kw)
+        # the restated selection is numpy's own on this host
+        assert np.array_equal(ia, _np_select(s32, c["k"], kw)), name
         _, ic, wc = R.route_topk_canonical(s32, c["k"], return_arrays=True, **kw)
         ties = R.boundary_ties(s32, c["k"], scoring=c["scoring"], e_score_bias=bias,
                                n_group=c.get("n_group", 0), topk_group=c.get("topk_group", 0))
@@ -46,6 +65,22 @@ def routing():
                             w_argpartition=wa, idx_canonical=ic.astype(np.int32), w_canonical=wc,
                             boundary_ties=ties)
         print(name, "ties:", int(ties.sum()))
+
+
+def _np_select(s32, k, kw):
+    """The reference's selection with the installed np.argpartition
+    (fastllm_py/expert_router.py:36-55, same float32 arithmetic as the oracle)."""
+    probs, select = R._scores(s32, kw["scoring"], kw["e_score_bias"])
+    ng, tg = kw["n_group"], kw["topk_group"]
+    if ng and ng > 1 and 0 < tg < ng:
+        T, E = select.shape
+        gs = select.reshape(T, ng, E // ng)
+        group_score = np.sort(gs, axis=-1)[:, :, -min(2, E // ng):].sum(-1)
+        keep = np.argpartition(-group_score, tg - 1, axis=-1)[:, :tg]
+        masked = np.ones((T, ng), dtype=bool)
+        np.put_along_axis(masked, keep, False, axis=-1)
+        select = np.where(np.repeat(masked, E // ng, axis=1), np.float32(-np.inf), select)
+    return np.argpartition(-select, k - 1, axis=-1)[:, :k]
 
 
 def packers():
