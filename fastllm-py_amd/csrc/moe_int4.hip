@@ -1240,16 +1240,26 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
         for (int i = threadIdx.x; i < a.T * a.hidden / 4; i += blockDim.x)
             reinterpret_cast<f32x4*>(a.y)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // Order of the grid (the hardware dispatches workgroups in index order):
+    // with the lists given, shared-expert workgroups first -- they depend on
+    // nothing and stream while the routed ones read their lists (T = 16:
+    // 60.8 -> 57.6 us per layer); with the routing fused (one token), the
+    // routed workgroups first, so their routing overlaps the shared stream
+    // (shared first measured 17.1 against 16.0 us)
     const int groups_r = a.routed.inter / (16 * TR);
+    const int n_r = a.max_slots * groups_r;
+    const int n_sh = a.has_shared ? a.shared.inter / (16 * TR) : 0;
     int slot, grp, e = 0, M = 0, row0 = 0;
     float fw = 0.f;  // fused routing: the slot's combine weight
     const MoeExperts* ex;
     const int b = blockIdx.x;
-    if (b < a.max_slots * groups_r) {
-        slot = b / groups_r;
-        grp = b - slot * groups_r;
+    const bool routed = a.fuse_route ? b < n_r : b >= n_sh;
+    if (routed) {
+        const int br = a.fuse_route ? b : b - n_sh;
+        slot = br / groups_r;
+        grp = br - slot * groups_r;
         if (a.fuse_route) {
-            fused_route_slot(a.ra, slot, b == 0, e, fw);
+            fused_route_slot(a.ra, slot, br == 0, e, fw);
             e = clampi(e, 0, a.E - 1);
             row0 = slot;
             M = 1;
@@ -1258,9 +1268,8 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
         }
         ex = &a.routed;
     } else {
-        if (!a.has_shared) return;
         slot = -1;
-        grp = b - a.max_slots * groups_r;
+        grp = a.fuse_route ? b - n_r : b;
         row0 = a.max_entries;
         M = a.T;
         ex = &a.shared;
@@ -1394,10 +1403,13 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, kq = lane >> 4;
-    const int y_slot = blockIdx.y;
+    // shared-expert pieces first (rows y < pieces) with the lists given, as
+    // in the gate/up grid; last with the routing fused
+    const int npc = a.has_shared ? a.pieces : 0;
+    const int yb = (int)blockIdx.y;
+    const bool is_shared = a.fuse_route ? yb >= a.max_slots : yb < npc;
+    const int y_slot = a.fuse_route ? yb : (is_shared ? a.max_slots + yb : yb - npc);
     const int o0 = blockIdx.x * W;
-    const bool is_shared = y_slot >= a.max_slots;
-    if (is_shared && (!a.has_shared || y_slot - a.max_slots >= a.pieces)) return;
 
     int e = 0, row0 = 0, M = 0, kb0, nfull;
     const MoeExperts* ex;
@@ -1848,7 +1860,7 @@ void launch_gate_up(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
 
 template <bool G128, int NB>
 void launch_down(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
-    const dim3 grid(a.hidden / (16 * down_tiles(NB)), a.max_slots + p.pieces);
+    const dim3 grid(a.hidden / (16 * down_tiles(NB)), a.max_slots + (a.has_shared ? p.pieces : 0));
     hipLaunchKernelGGL((moe_down_k<G128, NB, down_tiles(NB)>), grid, dim3(64 * p.waves_d), p.lds_d,
                        st, a);
 }

@@ -389,7 +389,7 @@ def _qwen15_layer(torch, rng, E=60, hidden=2048, inter=1408, sinter=5632):
     sh, sh_o = _stacked(shared, 128)
     sgw = (rng.standard_normal((1, hidden)) * 0.02).astype(np.float16)
     gw = (rng.standard_normal((E, hidden)) * 0.02).astype(np.float16)
-    return st, sh, sgw, gw
+    return st, sh, sgw, gw, st_o, sh_o
 
 
 @pytest.mark.parametrize("T", [1, 16])
@@ -403,7 +403,7 @@ def test_moe_layer_config4(torch_gpu, T):
     torch = torch_gpu
     g = np.load(os.path.join(GOLDEN, f"route_qwen15moe_t{T}.npz"))
     rng = np.random.default_rng(4100 + T)
-    st, sh, sgw, _ = _qwen15_layer(torch, rng)
+    st, sh, sgw, _, st_o, sh_o = _qwen15_layer(torch, rng)
     hidden, inter, sinter, E = 2048, 1408, 5632, 60
     x = rng.standard_normal((T, hidden)).astype(np.float16).astype(np.float32)
     xd = torch.from_numpy(x).cuda()
