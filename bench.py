@@ -134,15 +134,21 @@ def run_int4(torch, lib, layers, M, steps, stream):
           for K in {k for _, _, k in QWEN3_8B}}
     outs = {name: torch.empty((M, N), dtype=torch.float16, device="cuda")
             for name, N, _ in QWEN3_8B}
-    fn = lib.FastllmCudaMarlinHalfInt4GemmStream
+    # the Python layer's entry (marlin.gemm_fast): above four rows the GEMV
+    # splits K, its partials in a zeroed workspace per call site (one per
+    # shape here: launches on one stream never overlap)
+    wsb = {name: lib.fastllm_int4_gemm_ws_bytes(M, N, K, GS) for name, N, K in QWEN3_8B}
+    wss = {name: torch.zeros(max(b, 1), dtype=torch.uint8, device="cuda") for name, b in wsb.items()}
+    fn = lib.fastllm_int4_gemm_ws
 
     def launcher(layer, name, N, K):
         p = layer[name]
         args = (xs[K].data_ptr(), p["qweight"].data_ptr(), p["scales"].data_ptr(),
-                p["zeros"].data_ptr(), outs[name].data_ptr(), M, N, K, GS, None)
+                p["zeros"].data_ptr(), outs[name].data_ptr(), M, N, K, GS,
+                wss[name].data_ptr(), wsb[name], None)
 
         def go(h):
-            if not fn(*args, h):
+            if fn(*args, h) != 0:
                 raise RuntimeError(f"INT4 GEMM rejected M={M} N={N} K={K}")
         return go
 

@@ -278,11 +278,25 @@ struct NormArgs {
     float eps;
 };
 
+// Split-K (gridDim.y > 1, plain GEMV with register activations only): split
+// s of S covers full blocks [s * nb_s, (s + 1) * nb_s); each split stores its
+// fp32 partial of the strip with agent-scope atomic stores (coherent across
+// XCDs without cache flushes) into ws[(s * M + m) * N + n], waits for them to
+// complete, then bumps the strip's counter; the split that finds S - 1 sums the S partials in split
+// order (deterministic), writes C and resets the counter to 0.  Nothing
+// waits on another workgroup.  The counters start at zero (the caller's
+// workspace is zero-filled once) and are left at zero.
+struct SplitArgs {
+    float* ws = nullptr;
+    int* cnt = nullptr;
+};
+
 template <int T, int NB, bool G32, int AM, bool SWI>
 __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const uint32_t* __restrict__ Wq,
                                                const uint16_t* __restrict__ S, const uint32_t* __restrict__ Z,
                                                f16* __restrict__ C, int M, int N, int K,
-                                               const NormArgs& nrm = NormArgs{}) {
+                                               const NormArgs& nrm = NormArgs{},
+                                               const SplitArgs& sp = SplitArgs{}) {
     constexpr int SPB = G32 ? 4 : 1;  // scale groups per 128-k block
     extern __shared__ __align__(16) unsigned char smem[];
     const int nwaves = blockDim.x >> 6;
@@ -292,10 +306,18 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
     // contiguous range of strips and neighbours share its L2 (scale / zero
     // lines cover 64 columns, the activations every strip)
     const int strip = xcd_block();
-    const int nfull = K >> 7;
+    const int nsplit = gridDim.y;
+    const int nfull = (K >> 7) / nsplit;  // full 128-k blocks of this split
     const int col = lane & 15;
     const int kq = lane >> 4;
     const int zwords = N >> 3;
+    if (nsplit > 1) {  // this split's k-range: shift every block-indexed base
+        const int kbo = blockIdx.y * nfull;
+        A += (size_t)kbo * 128;
+        Wq += (size_t)kbo * 256;
+        S += (size_t)kbo * SPB * N;
+        Z += (size_t)kbo * SPB * zwords;
+    }
     constexpr bool ALDS = AM == 1;
     const int lda = K + 8;
     f16* As = reinterpret_cast<f16*>(smem);
@@ -399,9 +421,17 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
         }
     }
 
+    // the activation copies above stay ahead of every load below: the wait
+    // that hands a wave its copies counts the loads issued after them
+    __builtin_amdgcn_sched_barrier(0);
+
     // One straight-line issue of every load this wave will need (block
     // indices clamped into range: no guard, so nothing derived from the loaded
-    // values can be hoisted up here by the compiler).
+    // values can be hoisted up here by the compiler).  The tiles of one strip
+    // lie in one 64-column chunk unless SWI, so they share each zero word:
+    // it is loaded once (zv[i][0]) -- the load count the copy wait relies on
+    // is then the count the compiler emits, with nothing left to merge.
+    constexpr bool ZSHARE = !SWI && T > 1;
     u32x4 wv[NB][T];
     uint32_t sv[NB][T][SPB], zv[NB][T][SPB];
 #pragma unroll
@@ -416,17 +446,17 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
             for (int g = 0; g < SPB; ++g) {
                 const size_t grp = (size_t)kb * SPB + g;
                 sv[i][t][g] = S[grp * N + spos[t]];
-                zv[i][t][g] = Z[grp * zwords + zw[t]];
+                zv[i][t][g] = (ZSHARE && t > 0) ? zv[i][0][g] : Z[grp * zwords + zw[t]];
             }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
 
     if (AM == 0 || AM == 4) {
-        // this wave's activation copies, issued before its weight loads, are
-        // done once at most the weight loads are outstanding (no barrier:
-        // only this wave reads its slot)
-        constexpr int WL = NB * T * (1 + 2 * SPB);
+        // this wave's activation copies, issued before its weight, scale and
+        // zero loads, are done once at most those loads are outstanding (no
+        // barrier: only this wave reads its slot)
+        constexpr int WL = NB * (T * (1 + SPB) + (ZSHARE ? 1 : T) * SPB);
         wait_vmcnt<(WL < 63 ? WL : 63)>();
     }
     if (AM == 4) {
@@ -616,21 +646,56 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
         }
         return;
     }
+    if (nsplit == 1) {
+        for (int idx = threadIdx.x; idx < T * 256; idx += blockDim.x) {
+            const int l = (idx & 255) >> 2, e = idx & 3, t = idx >> 8;
+            const int m = 4 * (l >> 4) + e;
+            if (m >= M) continue;
+            float v = 0.f;
+            for (int w = 0; w < nwaves; ++w) v += red[(w * T + t) * 256 + (idx & 255)];
+            C[(size_t)m * N + (strip * T + t) * 16 + (l & 15)] = (f16)v;
+        }
+        return;
+    }
     for (int idx = threadIdx.x; idx < T * 256; idx += blockDim.x) {
         const int l = (idx & 255) >> 2, e = idx & 3, t = idx >> 8;
         const int m = 4 * (l >> 4) + e;
         if (m >= M) continue;
         float v = 0.f;
         for (int w = 0; w < nwaves; ++w) v += red[(w * T + t) * 256 + (idx & 255)];
-        C[(size_t)m * N + (strip * T + t) * 16 + (l & 15)] = (f16)v;
+        __hip_atomic_store(sp.ws + ((size_t)blockIdx.y * M + m) * N + (strip * T + t) * 16 + (l & 15), v,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // this wave's partial stores are complete (agent-coherent stores: no
+    // cache write-back needed; an agent-scope release fence would write back
+    // the XCD's whole L2 from every wave, measured 2-50x slower)
+    wait_vmcnt<0>();
+    __syncthreads();
+    int* last = reinterpret_cast<int*>(red);
+    if (threadIdx.x == 0)
+        last[0] = __hip_atomic_fetch_add(sp.cnt + strip, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                  nsplit - 1;
+    __syncthreads();
+    if (!last[0]) return;
+    for (int idx = threadIdx.x; idx < T * 256; idx += blockDim.x) {
+        const int l = (idx & 255) >> 2, e = idx & 3, t = idx >> 8;
+        const int m = 4 * (l >> 4) + e;
+        if (m >= M) continue;
+        const size_t n = (size_t)(strip * T + t) * 16 + (l & 15);
+        float v = 0.f;
+        for (int q = 0; q < nsplit; ++q)
+            v += __hip_atomic_load(sp.ws + ((size_t)q * M + m) * N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        C[(size_t)m * N + n] = (f16)v;
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(sp.cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int T, int NB, bool G32, int AM, bool SWI = false>
 __global__ __launch_bounds__(1024) void int4_gemv_nb(
     const f16* __restrict__ A, const uint32_t* __restrict__ Wq, const uint16_t* __restrict__ S,
-    const uint32_t* __restrict__ Z, f16* __restrict__ C, int M, int N, int K) {
-    int4_gemv_body<T, NB, G32, AM, SWI>(A, Wq, S, Z, C, M, N, K);
+    const uint32_t* __restrict__ Z, f16* __restrict__ C, int M, int N, int K,
+    SplitArgs sp = SplitArgs{}) {
+    int4_gemv_body<T, NB, G32, AM, SWI>(A, Wq, S, Z, C, M, N, K, NormArgs{}, sp);
 }
 
 // One decode row (M = 1) with add_rmsnorm in the prologue (AM 4): the GEMV of
@@ -885,47 +950,61 @@ hipError_t launch_gemm_mfma(const f16* A, const uint32_t* Wq, const uint16_t* S,
 }
 
 struct GemvCfg {
-    int tiles;  // n-tiles (16 columns) per workgroup: 1 or 2
-    int waves;  // waves per workgroup, 1..16
-    int nb;     // max full 128-k blocks per wave (register budget): 1,2,4,6,8
+    int tiles;      // n-tiles (16 columns) per workgroup: 1, 2 or 4
+    int waves;      // waves per workgroup, 1..16
+    int nb;         // max full 128-k blocks per wave (register budget): 1,2,4,6,8
+    int split = 1;  // k-splits (gridDim.y), each over (K/128)/split blocks
 };
+
+// Workspace of a split-K launch: the strip counters at offset 0 (room for
+// N / 16 of them, whatever the tiles, so calls of any M and split on one
+// workspace find theirs at zero), then the fp32 partials [split][M][N] from a
+// 256-byte boundary.
+constexpr size_t splitk_part_off(int N) { return ((size_t)(N / 16) * 4 + 255) & ~(size_t)255; }
+constexpr size_t splitk_ws_bytes(int M, int N, int split) {
+    return splitk_part_off(N) + (size_t)split * M * N * 4;
+}
 
 constexpr size_t kGemvLdsCap = 96 * 1024;  // activations staged in LDS up to this size
 
+// A split-K launch (split > 1) uses register activations (AM 0 copies for
+// M <= 4, AM 3 / AM 2 above): the whole-row LDS staging of AM 1 would read
+// past the shifted activation base.
 template <int T, int NB, bool G32>
 hipError_t launch_gemv_nb(const f16* A, const uint32_t* Wq, const uint16_t* S, const uint32_t* Z,
-                          f16* C, int M, int N, int K, int waves, hipStream_t stream) {
+                          f16* C, int M, int N, int K, int waves, int split, SplitArgs sp,
+                          hipStream_t stream) {
     const size_t red = (size_t)waves * T * 256 * sizeof(float);
-    const dim3 grid(N / (16 * T)), block(64 * waves);
+    const dim3 grid(N / (16 * T), split), block(64 * waves);
     const size_t own = (size_t)waves * NB * 1024;
     const size_t shared = (((size_t)M * (K + 8) * 2 + 15) & ~(size_t)15);
     if (M <= 4 && own + red <= 160 * 1024)
         hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 0>), grid, block, own + red, stream, A, Wq, S, Z,
-                           C, M, N, K);
+                           C, M, N, K, sp);
     else if (NB <= 4)
         hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 3>), grid, block, red, stream, A, Wq, S, Z, C, M,
-                           N, K);
-    else if (shared <= kGemvLdsCap)
+                           N, K, sp);
+    else if (shared <= kGemvLdsCap && split == 1)
         hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 1>), grid, block, shared + red, stream, A, Wq, S,
-                           Z, C, M, N, K);
+                           Z, C, M, N, K, sp);
     else
         hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 2>), grid, block, red, stream, A, Wq, S, Z, C, M,
-                           N, K);
+                           N, K, sp);
     return hipGetLastError();
 }
 
 template <int T, bool G32>
 hipError_t dispatch_nb(int nb, const f16* A, const uint32_t* Wq, const uint16_t* S,
-                       const uint32_t* Z, f16* C, int M, int N, int K, int waves,
-                       hipStream_t stream) {
+                       const uint32_t* Z, f16* C, int M, int N, int K, int waves, int split,
+                       SplitArgs sp, hipStream_t stream) {
     switch (nb) {
-        case 1: return launch_gemv_nb<T, 1, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
-        case 2: return launch_gemv_nb<T, 2, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
-        case 3: return launch_gemv_nb<T, 3, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
-        case 4: return launch_gemv_nb<T, 4, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
-        case 5: return launch_gemv_nb<T, 5, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
-        case 6: return launch_gemv_nb<T, 6, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
-        default: return launch_gemv_nb<T, 8, G32>(A, Wq, S, Z, C, M, N, K, waves, stream);
+        case 1: return launch_gemv_nb<T, 1, G32>(A, Wq, S, Z, C, M, N, K, waves, split, sp, stream);
+        case 2: return launch_gemv_nb<T, 2, G32>(A, Wq, S, Z, C, M, N, K, waves, split, sp, stream);
+        case 3: return launch_gemv_nb<T, 3, G32>(A, Wq, S, Z, C, M, N, K, waves, split, sp, stream);
+        case 4: return launch_gemv_nb<T, 4, G32>(A, Wq, S, Z, C, M, N, K, waves, split, sp, stream);
+        case 5: return launch_gemv_nb<T, 5, G32>(A, Wq, S, Z, C, M, N, K, waves, split, sp, stream);
+        case 6: return launch_gemv_nb<T, 6, G32>(A, Wq, S, Z, C, M, N, K, waves, split, sp, stream);
+        default: return launch_gemv_nb<T, 8, G32>(A, Wq, S, Z, C, M, N, K, waves, split, sp, stream);
     }
 }
 
@@ -934,25 +1013,28 @@ hipError_t dispatch_nb(int nb, const f16* A, const uint32_t* Wq, const uint16_t*
 // bytes, 128 KB at M = 16, K = 4096).  Register activations (AM 3) only.
 template <int NB, bool G32>
 hipError_t launch_gemv_t4(const f16* A, const uint32_t* Wq, const uint16_t* S, const uint32_t* Z,
-                          f16* C, int M, int N, int K, int waves, hipStream_t stream) {
+                          f16* C, int M, int N, int K, int waves, int split, SplitArgs sp,
+                          hipStream_t stream) {
     const size_t red = (size_t)waves * 4 * 256 * sizeof(float);
-    hipLaunchKernelGGL((int4_gemv_nb<4, NB, G32, 3>), dim3(N / 64), dim3(64 * waves), red, stream, A, Wq,
-                       S, Z, C, M, N, K);
+    hipLaunchKernelGGL((int4_gemv_nb<4, NB, G32, 3>), dim3(N / 64, split), dim3(64 * waves), red, stream, A,
+                       Wq, S, Z, C, M, N, K, sp);
     return hipGetLastError();
 }
 
 template <bool G32>
 hipError_t dispatch_gemv(const GemvCfg& c, const f16* A, const uint32_t* Wq, const uint16_t* S,
-                         const uint32_t* Z, f16* C, int M, int N, int K, hipStream_t stream) {
+                         const uint32_t* Z, f16* C, int M, int N, int K, hipStream_t stream,
+                         SplitArgs sp = SplitArgs{}) {
     if (c.tiles == 4) {
         switch (c.nb) {
-            case 1: return launch_gemv_t4<1, G32>(A, Wq, S, Z, C, M, N, K, c.waves, stream);
-            case 2: return launch_gemv_t4<2, G32>(A, Wq, S, Z, C, M, N, K, c.waves, stream);
-            default: return launch_gemv_t4<4, G32>(A, Wq, S, Z, C, M, N, K, c.waves, stream);
+            case 1: return launch_gemv_t4<1, G32>(A, Wq, S, Z, C, M, N, K, c.waves, c.split, sp, stream);
+            case 2: return launch_gemv_t4<2, G32>(A, Wq, S, Z, C, M, N, K, c.waves, c.split, sp, stream);
+            default: return launch_gemv_t4<4, G32>(A, Wq, S, Z, C, M, N, K, c.waves, c.split, sp, stream);
         }
     }
-    if (c.tiles == 2) return dispatch_nb<2, G32>(c.nb, A, Wq, S, Z, C, M, N, K, c.waves, stream);
-    return dispatch_nb<1, G32>(c.nb, A, Wq, S, Z, C, M, N, K, c.waves, stream);
+    if (c.tiles == 2)
+        return dispatch_nb<2, G32>(c.nb, A, Wq, S, Z, C, M, N, K, c.waves, c.split, sp, stream);
+    return dispatch_nb<1, G32>(c.nb, A, Wq, S, Z, C, M, N, K, c.waves, c.split, sp, stream);
 }
 
 // register-slot counts with a kernel instance (slots beyond a wave's share
@@ -967,16 +1049,43 @@ int nb_bucket(int need) {
 // (N >= 16384) take 2 n-tiles per strip and 8 waves while M <= 4; otherwise 16
 // waves, 2 n-tiles once N >= 6144 and M >= 4 (activation fragments then feed
 // two tiles).  The register-slot count is the exact per-wave block share.
-GemvCfg default_gemv_cfg(int M, int N, int K, bool g32) {
+GemvCfg default_gemv_cfg(int M, int N, int K, bool g32, bool can_split = false) {
     GemvCfg c;
+    if (can_split && M > 4 && !g32 && K % 128 == 0 && N % 64 == 0) {
+        // Splitting K over workgroups costs the last split of each strip a
+        // chain of device-coherent round trips (partials out, counter, partials
+        // back): ~2-3 us, so it pays only where the unsplit kernel re-reads
+        // the activations heavily.  Long K (the down projection): two splits
+        // of two tiles (M = 8: 11.8 -> 10.5 us, M = 16: 15.7 -> 12.6 at
+        // 4096 x 12288); wide N above M = 8: four tiles, two splits of one
+        // block per wave (18.6 -> 16.7 us at 24576 x 4096, M = 16).
+        const int nall = K / 128;
+        if (nall >= 64 && nall % 2 == 0 && nall / 2 <= 16 * 8) {
+            c.tiles = 2;
+            c.waves = 16;
+            c.nb = nb_bucket((nall / 2 + 15) / 16);
+            c.split = 2;
+            return c;
+        }
+        if (N >= 16384 && M > 8 && nall % 2 == 0 && nall / 2 <= 16) {
+            c.tiles = 4;
+            c.waves = nall / 2;
+            c.nb = 1;
+            c.split = 2;
+            return c;
+        }
+    }
     // four tiles above M = 8 on wide N: each workgroup reads all of A, and
     // the A bytes (M x K x 2 per workgroup) load the L1/TD path more than
     // the weights do there
-    c.tiles = N >= 16384 ? (M > 8 ? 4 : 2) : ((N >= 6144 && M >= 4) ? 2 : 1);
+    c.tiles = N >= 16384 ? (M > 8 ? 4 : 2) : (N >= 6144 ? 2 : 1);
     if (N % (16 * c.tiles)) c.tiles = 1;
     const int nfull = K / 128 > 0 ? K / 128 : 1;
     const int cap = g32 ? 4 : 8;
-    int waves = (N >= 16384 && M <= 8) ? 8 : 16;
+    // eight waves of four blocks beat sixteen of two where K <= 4096 (M <= 4:
+    // qkv 5.85 -> 5.40 us, o 4.36 -> 4.26; one tile at any M: o 5.67 -> 5.52
+    // at M = 8)
+    int waves = ((N >= 16384 && M <= 8) || (nfull <= 32 && (M <= 4 || c.tiles == 1))) ? 8 : 16;
     while (waves > 1 && nfull < waves) waves /= 2;  // at least one block per wave
     while ((nfull + waves - 1) / waves > cap && waves < 16) waves *= 2;
     c.waves = waves;
@@ -991,7 +1100,9 @@ bool gemv_cfg_ok(const GemvCfg& c, int M, int N, int K, bool g32) {
     if (c.tiles == 4 && c.nb > 4) return false;
     if (c.waves < 1 || c.waves > 16) return false;
     if (N % (16 * c.tiles)) return false;
-    const int nfull = K / 128;
+    if (c.split < 1 || c.split > 16) return false;
+    if (c.split > 1 && (K % 128 || (K / 128) % c.split)) return false;  // whole blocks per split
+    const int nfull = K / 128 / c.split;
     if (nfull < 1 && !(g32 && K == 64)) return false;
     const int need = (nfull + c.waves - 1) / c.waves;
     if (need > c.nb || c.nb > (g32 ? 4 : 8)) return false;
@@ -1074,7 +1185,8 @@ bool int4_gemm_large_m(const f16* A, const uint32_t* q, const f16* S, const uint
 
 bool int4_marlin_abi_gemm(const void* a, const uint32_t* q, const void* scales,
                           const uint32_t* zeros, void* c, int M, int N, int K, int group_size,
-                          hipStream_t stream, const GemvCfg* forced) {
+                          hipStream_t stream, const GemvCfg* forced, void* ws = nullptr,
+                          size_t ws_bytes = 0) {
     if (!int4_args_ok(a, q, scales, zeros, c, M, N, K, group_size)) return false;
     const bool g32 = group_size == 32;
     const f16* A = static_cast<const f16*>(a);
@@ -1096,15 +1208,25 @@ bool int4_marlin_abi_gemm(const void* a, const uint32_t* q, const void* scales,
     if (M > 16)
         return int4_gemm_large_m(A, q, static_cast<const f16*>(scales), zeros, Cp, M, N, K, g32,
                                  stream);
-    GemvCfg cfg = forced ? *forced : default_gemv_cfg(M, N, K, g32);
+    GemvCfg cfg = forced ? *forced : default_gemv_cfg(M, N, K, g32, ws != nullptr);
+    if (cfg.split > 1 && (!ws || !fl_aligned(ws, 256) ||
+                          ws_bytes < splitk_ws_bytes(M, N, cfg.split))) {
+        if (forced) return false;
+        cfg = default_gemv_cfg(M, N, K, g32, false);
+    }
     if (!gemv_cfg_ok(cfg, M, N, K, g32)) {
         if (forced) return false;
         return int4_gemm_large_m(A, q, static_cast<const f16*>(scales), zeros, Cp, M, N, K, g32,
                                  stream);
     }
+    SplitArgs sp;
+    if (cfg.split > 1) {
+        sp.cnt = static_cast<int*>(ws);
+        sp.ws = reinterpret_cast<float*>(static_cast<char*>(ws) + splitk_part_off(N));
+    }
     const uint16_t* S = static_cast<const uint16_t*>(scales);
-    const hipError_t e = g32 ? dispatch_gemv<true>(cfg, A, q, S, zeros, Cp, M, N, K, stream)
-                             : dispatch_gemv<false>(cfg, A, q, S, zeros, Cp, M, N, K, stream);
+    const hipError_t e = g32 ? dispatch_gemv<true>(cfg, A, q, S, zeros, Cp, M, N, K, stream, sp)
+                             : dispatch_gemv<false>(cfg, A, q, S, zeros, Cp, M, N, K, stream, sp);
     return report(e, "FastllmCudaMarlinHalfInt4Gemm");
 }
 
@@ -1324,6 +1446,32 @@ bool fastllm_int4_gemm_config(const void* a, const uint32_t* b_q_weight, const v
     if (size_m > 16) return false;
     return int4_marlin_abi_gemm(a, b_q_weight, b_scales, b_zeros, c, size_m, size_n, size_k,
                                 group_size, (hipStream_t)stream, &cfg);
+}
+
+size_t fastllm_int4_gemm_ws_bytes(int size_m, int size_n, int size_k, int group_size) {
+    if (size_m < 1 || size_m > 16 || size_n <= 0 || size_k <= 0) return 0;
+    if (group_size != 32 && group_size != 128) return 0;
+    const GemvCfg c = default_gemv_cfg(size_m, size_n, size_k, group_size == 32, true);
+    return c.split > 1 ? splitk_ws_bytes(size_m, size_n, c.split) : 0;
+}
+
+int fastllm_int4_gemm_ws(const void* a, const uint32_t* b_q_weight, const void* b_scales,
+                         const uint32_t* b_zeros, void* c, int size_m, int size_n, int size_k,
+                         int group_size, void* workspace, size_t workspace_bytes, const int* cfg,
+                         void* stream) {
+    if (!int4_args_ok(a, b_q_weight, b_scales, b_zeros, c, size_m, size_n, size_k, group_size)) return 1;
+    if (cfg && size_m > 16) return 1;
+    GemvCfg forced;
+    if (cfg) {
+        forced.tiles = cfg[0];
+        forced.waves = cfg[1];
+        forced.nb = cfg[2];
+        forced.split = cfg[3];
+    }
+    return int4_marlin_abi_gemm(a, b_q_weight, b_scales, b_zeros, c, size_m, size_n, size_k, group_size,
+                                (hipStream_t)stream, cfg ? &forced : nullptr, workspace, workspace_bytes)
+               ? 0
+               : 2;
 }
 
 int fastllm_int4_gemm_swiglu(const void* a, const uint32_t* b_q_weight, const void* b_scales,

@@ -28,6 +28,8 @@ SIGNATURES: dict[str, tuple] = {
     "FastllmCudaMarlinHalfInt4GemmStream": (_B, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P]),
     "fastllm_int4_tile_unrepack": (_B, [_P, _P, _I, _I, _P]),
     "fastllm_int4_gemm_config": (_B, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P]),
+    "fastllm_int4_gemm_ws_bytes": (_SZ, [_I, _I, _I, _I]),
+    "fastllm_int4_gemm_ws": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P, _P]),
     "fastllm_int4_gemm_swiglu": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "fastllm_add_rmsnorm": (_I, [_P, _I, _P, _I, _P, _I, _P, _P, _I, _I, _F, _P]),
     "fastllm_swiglu": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _P]),

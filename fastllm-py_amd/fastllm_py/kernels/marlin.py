@@ -91,12 +91,24 @@ def build_marlin_scales_zeros(scale, zero_int, group_size, xp=np):
     return nat.as_output(scales, numpy_in), nat.as_output(zeros, numpy_in)
 
 
+# Decode GEMVs above four rows split K in two where that pays (long K, or
+# wide N above eight rows); their per-strip counters (size_n // 16 ints from
+# offset 0) and fp32 partials live in the workspace: 128 * size_n bytes plus
+# the counters for up to 16 rows, beside the reference's (size_n // 64) * 16
+# ints.
+def _workspace_ints(size_n: int) -> int:
+    split_bytes = ((size_n // 16) * 4 + 255) // 256 * 256 + 2 * 16 * size_n * 4
+    return max(max(1, (size_n // 64) * 16), split_bytes // 4)
+
+
 def make_workspace(size_n, xp=None):
-    """Zeroed int32 workspace, size max(1, (size_n//64)*16) (marlin.py:162-167)."""
+    """Zeroed int32 workspace for one call site (marlin.py:162-167).  Besides
+    the reference's max(1, (size_n//64)*16) ints it holds the split-K
+    partials of the decode GEMVs above four rows (128 * size_n bytes); the
+    kernels leave its counters at zero."""
     t = nat.torch()
     nat.require_device()
-    n = max(1, (size_n // 64) * 16)
-    return t.zeros(n, dtype=t.int32, device="cuda")
+    return t.zeros(_workspace_ints(size_n), dtype=t.int32, device="cuda")
 
 
 # --------------------------------------------------------------------------
@@ -162,6 +174,17 @@ def gemm_fast(a_fp16, qweight, scales, zeros, size_n, size_k, stream=None, works
     group_size = size_k // scales.shape[0]
     c = out if out is not None else t.empty((size_m, size_n), dtype=t.float16, device=a_fp16.device)
     ws = workspace if workspace is not None else get_workspace(size_n)
+    if 4 < size_m <= 16:
+        need = lib.fastllm_int4_gemm_ws_bytes(size_m, size_n, size_k, group_size)
+        have = ws.numel() * ws.element_size()
+        if need and have >= need:
+            # split-K decode GEMV with the call site's workspace (no validation,
+            # like the reference: the result code is not checked)
+            lib.fastllm_int4_gemm_ws(nat.ptr(a_fp16), nat.ptr(qweight), nat.ptr(scales),
+                                     nat.ptr(zeros), nat.ptr(c), size_m, size_n, size_k,
+                                     group_size, nat.ptr(ws), have, None,
+                                     nat.stream_handle(stream))
+            return c
     if stream is not None:
         lib.FastllmCudaMarlinHalfInt4GemmStream(
             nat.ptr(a_fp16), nat.ptr(qweight), nat.ptr(scales), nat.ptr(zeros), nat.ptr(c),
@@ -286,9 +309,16 @@ def marlin_gemm_int4(a_fp16, packed_weights, scales, zeros, workspace=None, size
         zeros = zeros.to(t.int64).to(t.int32).view(t.uint32)
     qw = nat.to_device(packed_weights)
     c = t.empty((size_m, size_n), dtype=t.float16, device=a.device)
-    ok = lib.FastllmCudaMarlinHalfInt4Gemm(
-        nat.ptr(a), nat.ptr(qw), nat.ptr(scales), nat.ptr(zeros), nat.ptr(c),
-        size_m, size_n, size_k, group_size, nat.ptr(workspace))
+    have = workspace.numel() * workspace.element_size()
+    need = lib.fastllm_int4_gemm_ws_bytes(size_m, size_n, size_k, group_size)
+    if need and have >= need:
+        ok = lib.fastllm_int4_gemm_ws(nat.ptr(a), nat.ptr(qw), nat.ptr(scales), nat.ptr(zeros),
+                                      nat.ptr(c), size_m, size_n, size_k, group_size,
+                                      nat.ptr(workspace), have, None, None) == 0
+    else:
+        ok = lib.FastllmCudaMarlinHalfInt4Gemm(
+            nat.ptr(a), nat.ptr(qw), nat.ptr(scales), nat.ptr(zeros), nat.ptr(c),
+            size_m, size_n, size_k, group_size, nat.ptr(workspace))
     if sync:
         t.cuda.synchronize()
     if not ok:

@@ -84,6 +84,28 @@ bool fastllm_int4_gemm_config(const void *a, const uint32_t *b_q_weight,
                               int group_size, int tiles, int waves, int nb,
                               void *stream);
 
+/* The Marlin-format GEMM of FastllmCudaMarlinHalfInt4Gemm[Stream] (same
+ * arguments and result) with a caller workspace that lets the decode shapes
+ * (size_m <= 16) split K over several workgroups: each split stores its fp32
+ * partial, the last split of each output strip sums them in split order
+ * (deterministic) and writes c.  workspace: device memory of at least
+ * fastllm_int4_gemm_ws_bytes(size_m, size_n, size_k, group_size) bytes,
+ * 256-byte aligned, zero-filled once before first use (its counters are left
+ * at zero by every call); calls sharing a workspace must not overlap.  A
+ * workspace of 0 bytes (or NULL) runs the unsplit kernels.  cfg (NULL for
+ * the built-in choice) forces {tiles, waves, blocks per wave, splits} for
+ * tuning; a forced shape the kernels cannot take returns 2.  Returns 0, 1
+ * for bad arguments, 2 for a device or launch error.
+ * No reference counterpart: the reference's workspace (N/64*16 ints,
+ * fastllm_py/kernels/marlin.py:162-167) is too small for fp32 partials; the
+ * Python layer's gemm_fast passes a sized workspace here. */
+size_t fastllm_int4_gemm_ws_bytes(int size_m, int size_n, int size_k, int group_size);
+int fastllm_int4_gemm_ws(const void *a, const uint32_t *b_q_weight,
+                         const void *b_scales, const uint32_t *b_zeros, void *c,
+                         int size_m, int size_n, int size_k, int group_size,
+                         void *workspace, size_t workspace_bytes, const int *cfg,
+                         void *stream);
+
 /* Gate/up projection with the SwiGLU epilogue, decode-shaped (size_m <= 16):
  * the Marlin-format weight holds size_n = 2 I output columns, gate rows
  * [0, I) then up rows [I, 2 I) (I % 64 == 0, size_k % 128 == 0); writes

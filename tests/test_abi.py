@@ -84,3 +84,30 @@ def test_moe_entry_argument_checks():
     assert routed(ws_bytes=ws - 1) == 1
     assert lib.fastllm_moe_int4_tile_repack(p, p, p, p, p, 24, 256, 128, None) == 1  # rows % 16
     assert lib.fastllm_moe_int4_tile_repack(p, p, p, p, p, 32, 200, 128, None) == 1  # in % 128
+
+
+def test_int4_split_workspace_sizes():
+    """Split-K workspace query (host arithmetic only): above four rows the
+    long-K down shape and (above eight rows) the wide gate_up shape split in
+    two (counters for N / 16 strips from offset 0, then 2 x M x N fp32
+    partials); qkv / o and four rows or fewer do not split; the Python
+    layer's make_workspace covers every split shape."""
+    from fastllm_py.kernels.marlin import _workspace_ints
+
+    lib = _native.lib()
+    part = lambda N: (N // 16 * 4 + 255) // 256 * 256  # noqa: E731
+    down, gate_up = (4096, 12288), (24576, 4096)
+    for M in (5, 8, 16):
+        assert lib.fastllm_int4_gemm_ws_bytes(M, *down, 128) == part(4096) + 2 * M * 4096 * 4
+    assert lib.fastllm_int4_gemm_ws_bytes(16, *gate_up, 128) == part(24576) + 2 * 16 * 24576 * 4
+    assert lib.fastllm_int4_gemm_ws_bytes(8, *gate_up, 128) == 0
+    for N, K in ((6144, 4096), (4096, 4096)):
+        assert lib.fastllm_int4_gemm_ws_bytes(16, N, K, 128) == 0
+    for M in (1, 4, 17):
+        assert lib.fastllm_int4_gemm_ws_bytes(M, *down, 128) == 0
+    assert lib.fastllm_int4_gemm_ws_bytes(16, 4096, 12288, 32) == 0  # group 32 stays unsplit
+    assert lib.fastllm_int4_gemm_ws_bytes(16, 4096, 12288, 64) == 0  # not a Marlin group
+    for N in (64, 2048, 4096, 6144, 24576, 151936 // 64 * 64):
+        for K in range(1024, 32768 + 1, 1024):
+            for M in range(5, 17):
+                assert lib.fastllm_int4_gemm_ws_bytes(M, N, K, 128) <= 4 * _workspace_ints(N)

@@ -5,6 +5,8 @@ dequantize-then-matmul of the very same packed weights (the bar the path is
 held to; its fp16 output rounding alone is ~5e-4).
 Mirrors tests/test_native_kernels.py:79-154 of the reference.
 """
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -228,6 +230,86 @@ def test_gemv_four_tiles(torch_gpu, M, gs):
                                             y.data_ptr(), M, N, K, gs, tiles, waves, nb, None)
         torch.cuda.synchronize()
         assert Q.max_abs_rel(y.float().cpu().numpy(), ref) < TOL, (tiles, waves, nb)
+
+
+@pytest.mark.parametrize("gs", [128, 32])
+def test_gemv_split_k(torch_gpu, gs):
+    """Split-K decode GEMV through fastllm_int4_gemm_ws: every forced
+    {tiles, waves, blocks per wave, splits} within the oracle's tolerance,
+    bit-identical on a repeat (the last split of each strip sums the partials
+    in split order), and one workspace shared by calls of different M and
+    split (the strip counters sit at one offset and are left at zero)."""
+    from fastllm_py import _native
+
+    torch = torch_gpu
+    lib = _native.lib()
+    K, N = 4096, 2048
+    rng = np.random.default_rng(410 + gs)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    pay, w_hat, _ = _prep(torch, W, gs)
+    ws_bytes = 1024 * N + 4096  # 16 splits x 16 rows x N fp32 + the counters
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device="cuda")
+    cfgs = [(4, 16, 1, 2), (4, 8, 1, 4), (2, 4, 2, 4), (1, 4, 1, 8), (4, 4, 1, 8), (1, 2, 1, 16)]
+
+    def run(ad, M, cfg):
+        y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        c = None if cfg is None else (ctypes.c_int * 4)(*cfg)
+        rc = lib.fastllm_int4_gemm_ws(ad.data_ptr(), pay["qweight"].data_ptr(),
+                                      pay["scales"].data_ptr(), pay["zeros"].data_ptr(),
+                                      y.data_ptr(), M, N, K, gs, ws.data_ptr(), ws_bytes, c, None)
+        assert rc == 0, (M, cfg, rc)
+        return y
+
+    first = {}
+    for M in (1, 3, 5, 8, 16):
+        a = rng.standard_normal((M, K)).astype(np.float16)
+        ad = torch.from_numpy(a).cuda()
+        ref = Q.matmul_ref(a.astype(np.float32), w_hat)
+        for cfg in cfgs + [None]:
+            y = run(ad, M, cfg)
+            torch.cuda.synchronize()
+            assert Q.max_abs_rel(y.float().cpu().numpy(), ref) < TOL, (M, cfg)
+            first[(M, cfg)] = (ad, y)
+    # repeats after calls of other shapes on the same workspace: bit-identical
+    for (M, cfg), (ad, y) in first.items():
+        assert torch.equal(run(ad, M, cfg), y), (M, cfg)
+    torch.cuda.synchronize()
+    assert int(ws[:N // 16 * 4].count_nonzero()) == 0  # counters back at zero
+    # a forced split with too small a workspace is refused, no launch
+    y = torch.empty((8, N), dtype=torch.float16, device="cuda")
+    ad = first[(8, None)][0]
+    assert lib.fastllm_int4_gemm_ws(ad.data_ptr(), pay["qweight"].data_ptr(), pay["scales"].data_ptr(),
+                                    pay["zeros"].data_ptr(), y.data_ptr(), 8, N, K, gs,
+                                    ws.data_ptr(), 1024, (ctypes.c_int * 4)(4, 8, 1, 4), None) == 2
+
+
+@pytest.mark.parametrize("name,M", [("down", 5), ("down", 8), ("down", 16), ("gate_up", 16)])
+def test_gemm_split_default_workspace(torch_gpu, name, M):
+    """The Python layer's default above M = 4: gemm_fast with the call site's
+    make_workspace runs the split kernels where they pay (Qwen3-8B down, and
+    gate_up above M = 8), within the oracle's tolerance like the unsplit
+    entry."""
+    from fastllm_py import _native
+    from fastllm_py.kernels import marlin
+
+    torch = torch_gpu
+    pay, w_hat, rng = _qwen_payload(torch, name)
+    N, K = QWEN3_8B[name]
+    assert _native.lib().fastllm_int4_gemm_ws_bytes(M, N, K, 128) > 0
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    ad = torch.from_numpy(a).cuda()
+    ws = marlin.make_workspace(N)
+    ref = Q.matmul_ref(a.astype(np.float32), w_hat)
+    for _ in range(2):
+        y = marlin.gemm_fast(ad, pay["qweight"], pay["scales"], pay["zeros"], N, K, workspace=ws)
+        torch.cuda.synchronize()
+        assert Q.max_abs_rel(y.float().cpu().numpy(), ref) < TOL, (name, M)
+    unsplit = torch.empty((M, N), dtype=torch.float16, device="cuda")
+    assert _native.lib().FastllmCudaMarlinHalfInt4Gemm(
+        ad.data_ptr(), pay["qweight"].data_ptr(), pay["scales"].data_ptr(), pay["zeros"].data_ptr(),
+        unsplit.data_ptr(), M, N, K, 128, None)
+    torch.cuda.synchronize()
+    assert Q.max_abs_rel(unsplit.float().cpu().numpy(), ref) < TOL
 
 
 @pytest.mark.parametrize("M,I,K,gs", [(1, 12288, 4096, 128), (4, 1408, 2048, 128), (8, 3072, 1024, 32),
