@@ -577,8 +577,11 @@ FL_DEV void net_argsort(float (&kf)[4], int (&ix)[4], int maxN, int lane) {
 }
 
 // Keys -v (numpy's -select) of n values (lane + 64 c), padded to the
-// network's size, sorted; returns maxN.
-FL_DEV int net_load_sort(const float (&v)[4], int n, int lane, float (&kf)[4], int (&ix)[4]) {
+// network's size, sorted; returns maxN.  Out of line: it runs only for tied
+// rows, and inlined its ~10 KB of code would sit in the instruction stream of
+// every routing wave (a one-pass wave pays an instruction-cache miss for
+// each large block it jumps over).
+__device__ __attribute__((noinline)) int net_load_sort(const float (&v)[4], int n, int lane, float (&kf)[4], int (&ix)[4]) {
     int maxN = 8;
     while (maxN < n) maxN <<= 1;
 #pragma unroll
@@ -1041,6 +1044,47 @@ __global__ __launch_bounds__(256) void slot_lists_k(const float* __restrict__ rw
     }
 }
 
+// Row-major e4m3 codes (rows, in_f) -> FP8 tiles (rows/16, in_f/128, 2048):
+// one thread per 16 bytes; lane (c, q) of tile t, block kb takes row 16 t + c,
+// k 128 kb + 32 q .. + 31.  The 128x128 block scales are not moved.
+__global__ void moe_fp8_tile_repack_k(const uint8_t* __restrict__ q, uint8_t* __restrict__ qt, long rows,
+                                      int in_f) {
+    const int nkb = in_f / 128;
+    const size_t n = (size_t)rows * in_f / 16;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        // destination piece i: block (t, kb), lane l = c + 16 q, half h
+        const size_t blk = i / 128;
+        const int within = (int)(i % 128), l = within >> 1, h = within & 1;
+        const size_t t = blk / nkb;
+        const int kb = (int)(blk % nkb), c = l & 15, qq = l >> 4;
+        const size_t src = (16 * t + c) * (size_t)in_f + 128 * kb + 32 * qq + 16 * h;
+        reinterpret_cast<u32x4*>(qt)[i] = *reinterpret_cast<const u32x4*>(q + src);
+    }
+}
+
+// Row-major MXFP4 (codes (rows, in_f/2), e8 (rows, in_f/32)) -> tiles
+// (rows/16, in_f/128, 1024) + scale words (rows/16, in_f/128, 16): lane
+// (c, q)'s word j holds the codes of row 16 t + c, k 128 kb + 32 j + 8 q ..
+// + 7 (row-major bytes 64 kb + 16 j + 4 q .. + 3); scale word (t, kb, c)
+// holds the E8M0 bytes of blocks 4 kb .. 4 kb + 3 of that row.
+__global__ void moe_mxfp4_tile_repack_k(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ e8,
+                                        uint8_t* __restrict__ qt, uint32_t* __restrict__ ew, long rows,
+                                        int in_f) {
+    const int nkb = in_f / 128;
+    const size_t n = (size_t)rows * nkb * 4;  // lanes (c, q) per block: 64 per 16 rows
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t blk = i / 64;
+        const int l = (int)(i % 64), c = l & 15, qq = l >> 4;
+        const size_t t = blk / nkb;
+        const int kb = (int)(blk % nkb);
+        const size_t row = 16 * t + c;
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(codes + row * (in_f / 2) + 64 * kb + 4 * qq);
+        reinterpret_cast<u32x4*>(qt)[i] = u32x4{src[0], src[4], src[8], src[12]};
+        if (qq == 0)
+            ew[blk * 16 + c] = *reinterpret_cast<const uint32_t*>(e8 + row * (in_f / 32) + 4 * kb);
+    }
+}
+
 // ------------------------------------------------------- fused MoE layer
 // Stacked-expert tile layout (this library's device layout for the fused MoE;
 // build_stacked_experts produces it from the row-major format):
@@ -1110,6 +1154,96 @@ struct MoeExperts {
     int inter;
 };
 
+// Weight formats of the fused-MoE tiles (16 rows x 128 k per tile block):
+//   INT4  -- 1 KB nibbles + per (row, group) fp16 scale|zero words (sz);
+//   FP8   -- 2 KB e4m3 codes, lane (c, q) holding k 32 q .. 32 q + 31 of row
+//            c; sz is the fp32 128x128-block scale array of
+//            quantize_fp8_block (quantizer.py:65-85), one per (row/128, kb);
+//   MXFP4 -- 1 KB E2M1 nibbles, lane (c, q)'s word j holding k 32 j + 8 q ..
+//            + 7 (so MFMA step j covers MX block 4 kb + j) and sz one word
+//            per (tile, kb, row) with the four E8M0 scales in bytes j.
+// Both low-precision codes become fp16 exactly (scale-1 conversions); the
+// block scale multiplies the fp32 MFMA result.
+constexpr int kFmtInt4 = 0, kFmtFp8 = 1, kFmtMx4 = 2;
+
+template <int FMT>
+struct WBlk {  // one lane's share of a tile block
+    u32x4 w;
+    u32x4 w2;  // FP8: bytes 16..31
+    uint32_t sz;
+};
+
+// Tile block `tile` x `kb` of a matrix (q, sz) with nkb 128-k blocks per row
+// tile; INT4 group index g of this lane (G groups per row).
+template <int FMT>
+FL_DEV WBlk<FMT> wblk_load(const uint8_t* q, const uint32_t* sz, size_t tile, int nkb, int kb, int g,
+                           int G, int lane, int col) {
+    WBlk<FMT> b;
+    const size_t blk = tile * nkb + kb;
+    if (FMT == kFmtFp8) {
+        const u32x4* p = reinterpret_cast<const u32x4*>(q + blk * 2048 + lane * 32);
+        b.w = __builtin_nontemporal_load(p);
+        b.w2 = __builtin_nontemporal_load(p + 1);
+        b.sz = sz[(tile >> 3) * nkb + kb];  // fp32 bits of the 128x128 block scale
+    } else {
+        b.w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + blk * 1024 + lane * 16));
+        b.sz = FMT == kFmtMx4 ? sz[blk * 16 + col] : sz[(tile * G + g) * 16 + col];
+    }
+    return b;
+}
+
+// fp16 pair of e4m3 bytes (hi: bytes 2, 3 of w, else 0, 1), exact
+FL_DEV uint32_t fp8x2_f16(uint32_t w, bool hi) {
+    return hi ? bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true))
+              : bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+}
+
+// fp16 pair of the E2M1 nibbles of byte `bs` of w (low nibble first), exact
+template <int BS>
+FL_DEV uint32_t fp4x2_f16(uint32_t w) {
+    return bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, BS));
+}
+
+// 2^(e - 127) for an E8M0 byte (e = 0 gives 2^-127, a subnormal fp32)
+FL_DEV float e8m0_float(uint32_t e) { return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u); }
+
+// acc += live * (tile block of weights) x (activation fragments a[j]): a[j]
+// is MFMA step j's A operand (k 32 q + 8 j for INT4 / FP8, 32 j + 8 q for
+// MXFP4, q the lane's quarter).
+template <int FMT, bool G128>
+FL_DEV void wblk_mma(f32x4& acc, const u32x4 (&a)[4], const WBlk<FMT>& b, float live) {
+    if (FMT == kFmtInt4) {
+        tile_block_mma<G128>(acc, a, b.w, (uint16_t)(b.sz & 0xFFFFu), (uint16_t)(b.sz >> 16), live);
+    } else if (FMT == kFmtFp8) {
+        f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t lo = j < 2 ? b.w[2 * j] : b.w2[2 * j - 4];
+            const uint32_t hi = j < 2 ? b.w[2 * j + 1] : b.w2[2 * j - 3];
+            const u32x4 bj{fp8x2_f16(lo, false), fp8x2_f16(lo, true), fp8x2_f16(hi, false),
+                           fp8x2_f16(hi, true)};
+            part = mfma_f16(bitcast<f16x8>(a[j]), bitcast<f16x8>(bj), part);
+        }
+        const float s = __uint_as_float(b.sz) * live;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(s, part[e], acc[e]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t w = b.w[j];
+            const u32x4 bj{fp4x2_f16<0>(w), fp4x2_f16<1>(w), fp4x2_f16<2>(w), fp4x2_f16<3>(w)};
+            const f32x4 part = mfma_f16(bitcast<f16x8>(a[j]), bitcast<f16x8>(bj), f32x4{0.f, 0.f, 0.f, 0.f});
+            const float s = e8m0_float((b.sz >> (8 * j)) & 0xFFu) * live;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(s, part[e], acc[e]);
+        }
+    }
+}
+
+// activation offset (halves, within a 128-k block) of MFMA step j for lane quarter q
+template <int FMT>
+FL_DEV int a_koff(int q, int j) { return FMT == kFmtMx4 ? 32 * j + 8 * q : 32 * q + 8 * j; }
+
 // inter_buf (caller workspace) fp16 [max_entries + T][inter_pad] holds
 // silu(g) * u * w per list entry and, from row max_entries, per token of the
 // shared expert.  y is zeroed by the gate/up kernel and accumulated by the
@@ -1135,6 +1269,7 @@ struct MoeArgs {
     // outputs and the lists the down kernel reads
     int fuse_route;
     RouteArgs ra;
+    int fmt;  // weight format of both expert stacks (kFmt*)
 };
 
 // Fused routing of the one token (T == 1) in a routed gate/up workgroup:
@@ -1203,7 +1338,7 @@ FL_DEV uint16_t sz_zero(uint32_t v) { return (uint16_t)(v >> 16); }
 // The waves split the hidden (K) blocks, NB each; every weight load of a wave
 // (one 1 KB block per load) is issued before the token rows are gathered
 // into LDS.  Workgroup 0 also zeroes y for the down kernel's accumulation.
-template <bool G128, int NB, int TR>
+template <int FMT, bool G128, int NB, int TR>
 __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int nwaves = blockDim.x >> 6;
@@ -1309,8 +1444,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
     else
         wpre = a.scoef ? a.scoef[jw] : 1.0f;
 
-    u32x4 wg[NB][TR], wu[NB][TR];
-    uint32_t szg[NB][TR], szu[NB][TR];
+    WBlk<FMT> wg[NB][TR], wu[NB][TR];
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         int kb = moe_kb<NB>(wave, i, nwaves);
@@ -1318,12 +1452,8 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
         const int g = (kb * 128 + 32 * kq) / a.gs;
 #pragma unroll
         for (int r = 0; r < TR; ++r) {
-            const size_t off = ((tb0 + r) * nfull + kb) * 1024 + lane * 16;
-            wg[i][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ex->gq + off));
-            wu[i][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ex->uq + off));
-            const size_t so = ((tb0 + r) * G + g) * 16 + col;
-            szg[i][r] = ex->gsz[so];
-            szu[i][r] = ex->usz[so];
+            wg[i][r] = wblk_load<FMT>(ex->gq, ex->gsz, tb0 + r, nfull, kb, g, G, lane, col);
+            wu[i][r] = wblk_load<FMT>(ex->uq, ex->usz, tb0 + r, nfull, kb, g, G, lane, col);
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1342,8 +1472,9 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
         }
     } else {
         // the copies went out before this wave's weight loads (wg, wu: 2 per
-        // tile and block; the scale|zero words only make the wait stricter)
-        constexpr int WL = NB * TR * 2;
+        // tile and block, 4 for FP8; the scale words only make the wait
+        // stricter)
+        constexpr int WL = NB * TR * (FMT == kFmtFp8 ? 4 : 2);
         wait_vmcnt<(WL < 63 ? WL : 63)>();
     }
 
@@ -1358,11 +1489,11 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
         u32x4 av[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            av[j] = *reinterpret_cast<const u32x4*>(oslot + ((size_t)i * Tp + tok_r) * 256 + 2 * (32 * kq + 8 * j));
+            av[j] = *reinterpret_cast<const u32x4*>(oslot + ((size_t)i * Tp + tok_r) * 256 + 2 * a_koff<FMT>(kq, j));
 #pragma unroll
         for (int r = 0; r < TR; ++r) {
-            tile_block_mma<G128>(acc[2 * r], av, wg[i][r], sz_scale(szg[i][r]), sz_zero(szg[i][r]), live);
-            tile_block_mma<G128>(acc[2 * r + 1], av, wu[i][r], sz_scale(szu[i][r]), sz_zero(szu[i][r]), live);
+            wblk_mma<FMT, G128>(acc[2 * r], av, wg[i][r], live);
+            wblk_mma<FMT, G128>(acc[2 * r + 1], av, wu[i][r], live);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -1394,7 +1525,7 @@ __global__ __launch_bounds__(512) void moe_gate_up_k(MoeArgs a) {
 // (blockIdx.x), over that slot's entries; results are added to y[token] with
 // fp32 atomics (like the reference's moew_down), so the summation order of
 // a token's terms varies between calls.
-template <bool G128, int NB, int TRD>
+template <int FMT, bool G128, int NB, int TRD>
 __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int toks[16];
@@ -1432,15 +1563,14 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
     const int nkb = inter >> 7;  // 128-k blocks per row of the expert
     const int G = inter / a.gs;
     const int mrow = col < M ? col : M - 1;
-    const uint16_t* arow = a.inter_buf + (size_t)(row0 + mrow) * a.inter_pad + 32 * kq;
+    const uint16_t* arow = a.inter_buf + (size_t)(row0 + mrow) * a.inter_pad;
     const size_t tb0 = (size_t)e * (a.hidden / 16) + o0 / 16;  // first row tile
     if (threadIdx.x < 16)
         toks[threadIdx.x] = is_shared ? threadIdx.x
                                       : clampi(a.tok[row0 + (threadIdx.x < M ? threadIdx.x : 0)], 0, a.T - 1);
 
     u32x4 av[NB][4];
-    u32x4 wv[NB][TRD];
-    uint32_t sv[NB][TRD];
+    WBlk<FMT> wv[NB][TRD];
     // activations first (L2 hits), then weights (HBM): loads retire in
     // issue order, so each block then waits only for its own weights
 #pragma unroll
@@ -1448,7 +1578,7 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
         int kb = moe_kb<NB>(wave, i, nwaves);
         kb = kb0 + (kb < nfull ? kb : nfull - 1);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) av[i][j] = *reinterpret_cast<const u32x4*>(arow + kb * 128 + 8 * j);
+        for (int j = 0; j < 4; ++j) av[i][j] = *reinterpret_cast<const u32x4*>(arow + kb * 128 + a_koff<FMT>(kq, j));
     }
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
@@ -1456,11 +1586,7 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
         kb = kb0 + (kb < nfull ? kb : nfull - 1);
         const int g = (kb * 128 + 32 * kq) / a.gs;
 #pragma unroll
-        for (int r = 0; r < TRD; ++r) {
-            wv[i][r] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4*>(ex->dq + ((tb0 + r) * nkb + kb) * 1024 + lane * 16));
-            sv[i][r] = ex->dsz[((tb0 + r) * G + g) * 16 + col];
-        }
+        for (int r = 0; r < TRD; ++r) wv[i][r] = wblk_load<FMT>(ex->dq, ex->dsz, tb0 + r, nkb, kb, g, G, lane, col);
     }
     __builtin_amdgcn_sched_barrier(0);
     f32x4 acc[TRD];
@@ -1470,8 +1596,7 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
     for (int i = 0; i < NB; ++i) {
         const float live = moe_kb<NB>(wave, i, nwaves) < nfull ? 1.0f : 0.0f;
 #pragma unroll
-        for (int r = 0; r < TRD; ++r)
-            tile_block_mma<G128>(acc[r], av[i], wv[i][r], sz_scale(sv[i][r]), sz_zero(sv[i][r]), live);
+        for (int r = 0; r < TRD; ++r) wblk_mma<FMT, G128>(acc[r], av[i], wv[i][r], live);
         __builtin_amdgcn_sched_barrier(0);
     }
     float* red = reinterpret_cast<float*>(smem);
@@ -1806,7 +1931,8 @@ struct MoePlan {
 constexpr int down_tiles(int nb) { return nb <= 4 ? 2 : 1; }
 
 // false when the shape is outside what the kernels support.
-bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, MoePlan& p) {
+bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, MoePlan& p,
+              int fmt = kFmtInt4) {
     if (T <= 0 || hidden <= 0 || hidden % 128 || inter <= 0 || inter % 128) return false;
     if (shared_inter < 0 || shared_inter % 128 || max_entries <= 0) return false;
     p.grouped = T > 16;
@@ -1824,7 +1950,7 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
     if (p.nb_gu > 4) return false;  // hidden <= 4096
     p.waves_gu = (nfh + p.nb_gu - 1) / p.nb_gu;
     const size_t as_bytes = (size_t)p.waves_gu * p.nb_gu * ((T + 3) & ~3) * 256;
-    p.tr_gu = gu_tiles(T);
+    p.tr_gu = fmt == kFmtFp8 ? 1 : gu_tiles(T);
     const size_t red_bytes = (size_t)p.waves_gu * 2 * p.tr_gu * 1024;
     p.lds_gu = (as_bytes > red_bytes ? as_bytes : red_bytes) + (size_t)2 * p.tr_gu * 1024 + 16 * 4;
     if (p.lds_gu > 160 * 1024) return false;
@@ -1847,21 +1973,28 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
     return true;
 }
 
-template <bool G128, int NB>
+template <int FMT, bool G128, int NB>
 void launch_gate_up(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
     const int TR = p.tr_gu;
     const int grid = a.max_slots * (a.routed.inter / (16 * TR)) +
                      (a.has_shared ? a.shared.inter / (16 * TR) : 0);
-    if (TR == 1)
-        hipLaunchKernelGGL((moe_gate_up_k<G128, NB, 1>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu, st, a);
-    else
-        hipLaunchKernelGGL((moe_gate_up_k<G128, NB, 4>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu, st, a);
+    if constexpr (FMT == kFmtFp8) {  // two 16-byte loads per block: one tile per workgroup
+        hipLaunchKernelGGL((moe_gate_up_k<FMT, G128, NB, 1>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu, st,
+                           a);
+    } else {
+        if (TR == 1)
+            hipLaunchKernelGGL((moe_gate_up_k<FMT, G128, NB, 1>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu,
+                               st, a);
+        else
+            hipLaunchKernelGGL((moe_gate_up_k<FMT, G128, NB, 4>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu,
+                               st, a);
+    }
 }
 
-template <bool G128, int NB>
+template <int FMT, bool G128, int NB>
 void launch_down(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
     const dim3 grid(a.hidden / (16 * down_tiles(NB)), a.max_slots + (a.has_shared ? p.pieces : 0));
-    hipLaunchKernelGGL((moe_down_k<G128, NB, down_tiles(NB)>), grid, dim3(64 * p.waves_d), p.lds_d,
+    hipLaunchKernelGGL((moe_down_k<FMT, G128, NB, down_tiles(NB)>), grid, dim3(64 * p.waves_d), p.lds_d,
                        st, a);
 }
 
@@ -1881,7 +2014,7 @@ void moe_launch_grouped(const MoeArgs& a, hipStream_t st) {
     }
 }
 
-template <bool G128>
+template <int FMT, bool G128>
 void moe_launch(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
     if (a.T > kGuOwnT && !a.xh_ready) {
         const int n8 = a.T * a.hidden / 8;
@@ -1889,18 +2022,18 @@ void moe_launch(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
                            const_cast<uint16_t*>(a.xh), n8);
     }
     switch (p.nb_gu) {
-        case 1: launch_gate_up<G128, 1>(a, p, st); break;
-        case 2: launch_gate_up<G128, 2>(a, p, st); break;
-        case 3: launch_gate_up<G128, 3>(a, p, st); break;
-        default: launch_gate_up<G128, 4>(a, p, st); break;
+        case 1: launch_gate_up<FMT, G128, 1>(a, p, st); break;
+        case 2: launch_gate_up<FMT, G128, 2>(a, p, st); break;
+        case 3: launch_gate_up<FMT, G128, 3>(a, p, st); break;
+        default: launch_gate_up<FMT, G128, 4>(a, p, st); break;
     }
     switch (p.nb_d) {
-        case 1: launch_down<G128, 1>(a, p, st); break;
-        case 2: launch_down<G128, 2>(a, p, st); break;
-        case 3: launch_down<G128, 3>(a, p, st); break;
-        case 4: launch_down<G128, 4>(a, p, st); break;
-        case 6: launch_down<G128, 6>(a, p, st); break;
-        default: launch_down<G128, 8>(a, p, st); break;
+        case 1: launch_down<FMT, G128, 1>(a, p, st); break;
+        case 2: launch_down<FMT, G128, 2>(a, p, st); break;
+        case 3: launch_down<FMT, G128, 3>(a, p, st); break;
+        case 4: launch_down<FMT, G128, 4>(a, p, st); break;
+        case 6: launch_down<FMT, G128, 6>(a, p, st); break;
+        default: launch_down<FMT, G128, 8>(a, p, st); break;
     }
 }
 
@@ -2004,6 +2137,30 @@ int fastllm_moe_int4_tile_repack(const uint8_t* qweight, const void* scales, con
     return finish("fastllm_moe_int4_tile_repack");
 }
 
+int fastllm_moe_fp8_tile_repack(const uint8_t* q, uint8_t* qtile, long rows, int in_f, void* stream) {
+    if (!q || !qtile || rows <= 0 || rows % 16 || in_f <= 0 || in_f % 128) return 1;
+    if (!fl_aligned(q, 16) || !fl_aligned(qtile, 16)) return 1;
+    if (!fl_current_device_supported()) return 2;
+    const size_t n = (size_t)rows * in_f / 16;
+    const int grid = (int)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
+    hipLaunchKernelGGL(moe_fp8_tile_repack_k, dim3(grid), dim3(256), 0, (hipStream_t)stream, q, qtile, rows,
+                       in_f);
+    return finish("fastllm_moe_fp8_tile_repack");
+}
+
+int fastllm_moe_mxfp4_tile_repack(const uint8_t* codes, const uint8_t* e8, uint8_t* qtile, uint32_t* e8w,
+                                  long rows, int in_f, void* stream) {
+    if (!codes || !e8 || !qtile || !e8w || rows <= 0 || rows % 16 || in_f <= 0 || in_f % 128) return 1;
+    if (!fl_aligned(codes, 4) || !fl_aligned(e8, 4) || !fl_aligned(qtile, 16) || !fl_aligned(e8w, 4))
+        return 1;
+    if (!fl_current_device_supported()) return 2;
+    const size_t n = (size_t)rows * (in_f / 128) * 4;
+    const int grid = (int)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
+    hipLaunchKernelGGL(moe_mxfp4_tile_repack_k, dim3(grid), dim3(256), 0, (hipStream_t)stream, codes, e8,
+                       qtile, e8w, rows, in_f);
+    return finish("fastllm_moe_mxfp4_tile_repack");
+}
+
 int fastllm_moe_int4_tile_unpack(const uint8_t* qtile, const uint32_t* sz, uint8_t* qweight,
                                  void* scales, void* zeros, long rows, int in_f, int group_size,
                                  void* stream) {
@@ -2035,15 +2192,20 @@ static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int
                           const int* active, const int* offsets, const int* tok,
                           const float* tokw, int max_slots, int max_entries, void* workspace,
                           size_t workspace_bytes, float* y, void* stream, bool launch,
-                          const RouteArgs* fuse = nullptr, bool xh_ready = false) {
+                          const RouteArgs* fuse = nullptr, bool xh_ready = false,
+                          int fmt = kFmtInt4) {
     if (!x || !y || E <= 0 || !gq || !gsz || !uq || !usz || !dq || !dsz) return 1;
-    if (group_size != 32 && group_size != 64 && group_size != 128) return 1;
+    if (fmt == kFmtInt4 && group_size != 32 && group_size != 64 && group_size != 128) return 1;
+    if (fmt == kFmtFp8 && group_size != 128) return 1;
+    if (fmt == kFmtMx4 && group_size != 32) return 1;
+    if (fmt != kFmtInt4 && (T > 16 || inter % 128 || hidden % 128)) return 1;  // decode kernels only
+    if (fmt < kFmtInt4 || fmt > kFmtMx4) return 1;
     if (!n_active || !active || !offsets || !tok || !tokw) return 1;
     if (max_slots <= 0 || max_entries <= 0) return 1;
     const bool has_shared = shared_inter > 0;
     if (has_shared && (!sgq || !sgsz || !suq || !susz || !sdq || !sdsz)) return 1;
     MoePlan p;
-    if (!moe_plan(T, hidden, inter, has_shared ? shared_inter : 0, max_entries, p)) return 1;
+    if (!moe_plan(T, hidden, inter, has_shared ? shared_inter : 0, max_entries, p, fmt)) return 1;
     if (!workspace || workspace_bytes < p.bytes || !fl_aligned(workspace, 16)) return 1;
     if (!fl_aligned(x, 16) || !fl_aligned(y, 16)) return 1;
     const bool al = fl_aligned(gq, 16) && fl_aligned(uq, 16) && fl_aligned(dq, 16) &&
@@ -2077,13 +2239,18 @@ static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int
     a.y = y;
     a.fuse_route = (fuse && T == 1 && !p.grouped) ? 1 : 0;
     if (a.fuse_route) a.ra = *fuse;
+    a.fmt = fmt;
     hipStream_t st = (hipStream_t)stream;
     if (p.grouped)
         moe_launch_grouped(a, st);
+    else if (fmt == kFmtFp8)
+        moe_launch<kFmtFp8, true>(a, p, st);
+    else if (fmt == kFmtMx4)
+        moe_launch<kFmtMx4, true>(a, p, st);
     else if (group_size == 128)
-        moe_launch<true>(a, p, st);
+        moe_launch<kFmtInt4, true>(a, p, st);
     else
-        moe_launch<false>(a, p, st);
+        moe_launch<kFmtInt4, false>(a, p, st);
     return finish("fastllm_moe_int4_fused");
 }
 
@@ -2102,6 +2269,22 @@ int fastllm_moe_int4_fused(const float* x, int T, int hidden, int group_size, in
                           true);
 }
 
+int fastllm_moe_lowp_fused(int format, const float* x, int T, int hidden, int group_size, int E,
+                           int inter, const uint8_t* gq, const uint32_t* gsz, const uint8_t* uq,
+                           const uint32_t* usz, const uint8_t* dq, const uint32_t* dsz, int shared_inter,
+                           const uint8_t* sgq, const uint32_t* sgsz, const uint8_t* suq,
+                           const uint32_t* susz, const uint8_t* sdq, const uint32_t* sdsz,
+                           const float* shared_coef, const int* n_active, const int* active,
+                           const int* offsets, const int* tok, const float* tokw, int max_slots,
+                           int max_entries, void* workspace, size_t workspace_bytes, float* y,
+                           void* stream) {
+    if (format != kFmtFp8 && format != kFmtMx4) return 1;
+    return moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz, shared_inter,
+                          sgq, sgsz, suq, susz, sdq, sdsz, shared_coef, n_active, active, offsets,
+                          tok, tokw, max_slots, max_entries, workspace, workspace_bytes, y, stream,
+                          true, nullptr, false, format);
+}
+
 // Router + fused MoE of T <= 16 tokens (body of fastllm_moe_int4_routed and
 // of its static-scratch variant).  `scratch_of`, when given, supplies the
 // workspace once every argument has been validated (nullptr -> rc 2).
@@ -2116,7 +2299,8 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
                            int shared_inter, const uint8_t* sgq, const uint32_t* sgsz,
                            const uint8_t* suq, const uint32_t* susz, const uint8_t* sdq,
                            const uint32_t* sdsz, void* workspace, size_t workspace_bytes,
-                           float* y, void* stream, void* (*scratch_of)() = nullptr) {
+                           float* y, void* stream, void* (*scratch_of)() = nullptr,
+                           int fmt = kFmtInt4) {
     if (!logits || T <= 0 || T > 16 || E <= 0 || E > 256 || top_k <= 0 || top_k > 16 || top_k > E)
         return 1;
     if (!topk_ids || !topk_w || !n_active || !active || !offsets || !tok || !tokw) return 1;
@@ -2126,7 +2310,7 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
     const int max_entries = T * top_k, max_slots = E < max_entries ? E : max_entries;
     if (scratch_of) {
         MoePlan sp;
-        if (!moe_plan(T, hidden, inter, shared_inter > 0 ? shared_inter : 0, max_entries, sp))
+        if (!moe_plan(T, hidden, inter, shared_inter > 0 ? shared_inter : 0, max_entries, sp, fmt))
             return 1;
         if (sp.bytes > workspace_bytes) {
             fprintf(stderr,
@@ -2143,7 +2327,7 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
     const int rc = moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz,
                                   shared_inter, sgq, sgsz, suq, susz, sdq, sdsz, shared_coef,
                                   n_active, active, offsets, tok, tokw, max_slots, max_entries,
-                                  workspace, workspace_bytes, y, stream, false);
+                                  workspace, workspace_bytes, y, stream, false, nullptr, false, fmt);
     if (rc) return rc;
     const MoeLists lists{n_active, active, offsets, tok, tokw};
     const RouteArgs r{logits, e_score_bias, shared_logit, T, E, top_k, scoring, norm, n_group,
@@ -2153,11 +2337,11 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
                               shared_inter, sgq, sgsz, suq, susz, sdq, sdsz,
                               shared_logit ? shared_coef : nullptr, n_active, active, offsets, tok,
                               tokw, max_slots, max_entries, workspace, workspace_bytes, y, stream,
-                              true, &r);
+                              true, &r, false, fmt);
     // T > 4: the router also writes the fp16 token rows the gate/up kernel
     // stages (the plan was validated above)
     MoePlan p;
-    moe_plan(T, hidden, inter, shared_inter > 0 ? shared_inter : 0, max_entries, p);
+    moe_plan(T, hidden, inter, shared_inter > 0 ? shared_inter : 0, max_entries, p, fmt);
     RouteArgs rx = r;
     if (p.xh_off) {
         rx.x = x;
@@ -2174,7 +2358,7 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
                           shared_inter, sgq, sgsz, suq, susz, sdq, sdsz,
                           shared_logit ? shared_coef : nullptr, n_active, active, offsets, tok, tokw,
                           max_slots, max_entries, workspace, workspace_bytes, y, stream, true,
-                          nullptr, p.xh_off != 0);
+                          nullptr, p.xh_off != 0, fmt);
 }
 
 }  // extern "C"
@@ -2234,6 +2418,26 @@ int fastllm_moe_int4_routed(const float* logits, int top_k, int scoring, int nor
                            active, offsets, tok, tokw, x, T, hidden, group_size, E, inter, gq, gsz,
                            uq, usz, dq, dsz, shared_inter, sgq, sgsz, suq, susz, sdq, sdsz,
                            workspace, workspace_bytes, y, stream);
+}
+
+int fastllm_moe_lowp_routed(int format, const float* logits, int top_k, int scoring, int norm,
+                            float routed_scaling, const float* e_score_bias, int n_group,
+                            int topk_group, const float* shared_logit, int* topk_ids,
+                            float* topk_w, float* rw, float* shared_coef, int* n_active,
+                            int* active, int* offsets, int* tok, float* tokw, const float* x,
+                            int T, int hidden, int group_size, int E, int inter,
+                            const uint8_t* gq, const uint32_t* gsz, const uint8_t* uq,
+                            const uint32_t* usz, const uint8_t* dq, const uint32_t* dsz,
+                            int shared_inter, const uint8_t* sgq, const uint32_t* sgsz,
+                            const uint8_t* suq, const uint32_t* susz, const uint8_t* sdq,
+                            const uint32_t* sdsz, void* workspace, size_t workspace_bytes, float* y,
+                            void* stream) {
+    if (format != kFmtFp8 && format != kFmtMx4) return 1;
+    return moe_routed_impl(logits, top_k, scoring, norm, routed_scaling, e_score_bias, n_group,
+                           topk_group, shared_logit, topk_ids, topk_w, rw, shared_coef, n_active,
+                           active, offsets, tok, tokw, x, T, hidden, group_size, E, inter, gq, gsz,
+                           uq, usz, dq, dsz, shared_inter, sgq, sgsz, suq, susz, sdq, sdsz,
+                           workspace, workspace_bytes, y, stream, nullptr, format);
 }
 
 int fastllm_moe_int4_routed_noalloc(const float* logits, int top_k, int scoring, int norm,

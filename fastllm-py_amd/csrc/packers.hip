@@ -283,6 +283,72 @@ __global__ void dequantize_fp8_block_k(const uint8_t* __restrict__ q, const floa
     }
 }
 
+// ------------------------------------------------------------- MXFP4 (OCP MX)
+// Blocks of 32 consecutive elements of a row share an E8M0 scale X =
+// 2^(floor(log2 amax) - 2) (exponent clamped to [-127, 127]; X = 1 for an
+// all-zero block); elements are v / X rounded to E2M1 to nearest, ties to
+// the even code, saturating at 6, with the sign of v.  Codes: two per byte,
+// the lower column in the low nibble.  Finite inputs only.
+FL_DEV int mx_exponent(float amax) {
+    if (amax == 0.0f) return 0;
+    const int biased = (int)((__float_as_uint(amax) >> 23) & 0xFFu);
+    const int e = biased - 129;
+    return e < -127 ? -127 : (e > 127 ? 127 : e);
+}
+
+FL_DEV uint32_t e2m1_code(float p) {
+    const float a = fabsf(p);
+    const uint32_t c = (uint32_t)(a > 0.25f) + (uint32_t)(a >= 0.75f) + (uint32_t)(a > 1.25f) +
+                       (uint32_t)(a >= 1.75f) + (uint32_t)(a > 2.5f) + (uint32_t)(a >= 3.5f) +
+                       (uint32_t)(a > 5.0f);
+    return c | ((__float_as_uint(p) >> 28) & 8u);
+}
+
+// one thread per (row, 32-column block)
+__global__ void quantize_mxfp4_k(const float* __restrict__ w, uint8_t* __restrict__ codes,
+                                 uint8_t* __restrict__ e8, size_t nblk, int cols) {
+    const int bpr = cols / 32;
+    for (size_t b = (size_t)blockIdx.x * blockDim.x + threadIdx.x; b < nblk;
+         b += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = b / bpr;
+        const int g = (int)(b - r * bpr);
+        const f32x4* src = reinterpret_cast<const f32x4*>(w + r * cols + 32 * g);
+        f32x4 v[8];
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            v[i] = src[i];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(v[i][e]));
+        }
+        const int ex = mx_exponent(amax);
+        const float inv = __uint_as_float((uint32_t)(127 - ex) << 23);  // 2^-ex, ex in [-127, 125]
+        u32x4 out;
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) word |= e2m1_code(v[2 * wd + i / 4][i % 4] * inv) << (4 * i);
+            out[wd] = word;
+        }
+        *reinterpret_cast<u32x4*>(codes + r * (cols / 2) + 16 * g) = out;
+        e8[b] = (uint8_t)(ex + 127);
+    }
+}
+
+__global__ void dequantize_mxfp4_k(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ e8,
+                                   float* __restrict__ out, size_t n, int cols) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t r = i / cols;
+        const int c = (int)(i - r * cols);
+        const uint32_t code = (codes[r * (cols / 2) + c / 2] >> (4 * (c & 1))) & 0xFu;
+        const float mag[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+        const float v = (code & 8u) ? -mag[code & 7u] : mag[code & 7u];
+        out[i] = v * ldexpf(1.0f, (int)e8[r * (cols / 32) + c / 32] - 127);
+    }
+}
+
 unsigned grid_for(size_t n, int threads) {
     size_t b = (n + threads - 1) / threads;
     if (b > 65536) b = 65536;
@@ -409,6 +475,27 @@ int fastllm_quantize_fp8_block(const float* w, uint8_t* q, float* scales, int ro
     hipLaunchKernelGGL(quantize_fp8_block_k, grid, dim3(1024), 0, (hipStream_t)stream, w, q,
                        scales, rows, cols, block_size);
     return finish("fastllm_quantize_fp8_block");
+}
+
+int fastllm_quantize_mxfp4(const float* w, uint8_t* codes, uint8_t* e8, long rows, int cols,
+                           void* stream) {
+    if (!w || !codes || !e8 || rows <= 0 || cols <= 0 || cols % 32) return 1;
+    if (!fl_aligned(w, 16) || !fl_aligned(codes, 16)) return 1;
+    if (!fl_current_device_supported()) return 2;
+    const size_t nblk = (size_t)rows * (cols / 32);
+    hipLaunchKernelGGL(quantize_mxfp4_k, dim3(grid_for(nblk, 256)), dim3(256), 0, (hipStream_t)stream,
+                       w, codes, e8, nblk, cols);
+    return finish("fastllm_quantize_mxfp4");
+}
+
+int fastllm_dequantize_mxfp4(const uint8_t* codes, const uint8_t* e8, float* out, long rows, int cols,
+                             void* stream) {
+    if (!codes || !e8 || !out || rows <= 0 || cols <= 0 || cols % 32) return 1;
+    if (!fl_current_device_supported()) return 2;
+    const size_t n = (size_t)rows * cols;
+    hipLaunchKernelGGL(dequantize_mxfp4_k, dim3(grid_for(n, 256)), dim3(256), 0, (hipStream_t)stream,
+                       codes, e8, out, n, cols);
+    return finish("fastllm_dequantize_mxfp4");
 }
 
 int fastllm_dequantize_fp8_block(const uint8_t* q, const float* scales, float* out, int rows,

@@ -172,6 +172,89 @@ def stack_tiles(proj: str, qw, sc, ze, group_size: int) -> dict:
             f"{proj}.shape": (out_f, half * 2)}
 
 
+# low-precision expert formats of the fused MoE: name -> (C format code, group)
+LOWP_FORMATS = {"fp8": (1, 128), "mxfp4": (2, 32)}
+
+
+def stack_lowp(fmt: str, proj: str, W) -> dict:
+    """One projection of E stacked experts, W (E, out, in) float (device
+    tensor or numpy), quantized on the GPU and stored in the fused MoE's
+    low-precision tile layout:
+
+    * ``fp8``: 128x128-block e4m3 (quantize_fp8_block's format,
+      quantizer.py:65-85; out % 128 == 0 so no block spans two experts):
+      ``{proj}.qtile`` (E, out/16, in/128, 2048) u8, ``{proj}.sz`` the fp32
+      block scales (E, out/128, in/128);
+    * ``mxfp4``: OCP MXFP4 (quantizer.quantize_mxfp4): ``{proj}.qtile``
+      (E, out/16, in/128, 1024) u8, ``{proj}.sz`` (E, out/16, in/128, 16)
+      int32 words of four E8M0 scales.
+
+    Also ``{proj}.shape`` (out, in)."""
+    t = nat.torch()
+    if fmt not in LOWP_FORMATS:
+        raise ValueError(f"stack_lowp: unknown format {fmt!r} (fp8, mxfp4)")
+    wd = nat.to_device(W, t.float32).contiguous()
+    E, out_f, in_f = wd.shape
+    if out_f % 128 or in_f % 128:
+        raise ValueError(f"stack_lowp: out {out_f} and in {in_f} must be multiples of 128")
+    rows = E * out_f
+    w2 = wd.reshape(rows, in_f)
+    hs = nat.current_stream_handle()
+    lib = nat.lib()
+    qt = t.empty((E, out_f // 16, in_f // 128, 2048 if fmt == "fp8" else 1024), dtype=t.uint8,
+                 device=wd.device)
+    if fmt == "fp8":
+        q = t.empty((rows, in_f), dtype=t.uint8, device=wd.device)
+        sz = t.empty((E, out_f // 128, in_f // 128), dtype=t.float32, device=wd.device)
+        nat.check_rc(lib.fastllm_quantize_fp8_block(nat.ptr(w2), nat.ptr(q), nat.ptr(sz), rows, in_f,
+                                                    128, hs), "fastllm_quantize_fp8_block")
+        nat.check_rc(lib.fastllm_moe_fp8_tile_repack(nat.ptr(q), nat.ptr(qt), rows, in_f, hs),
+                     "fastllm_moe_fp8_tile_repack")
+    else:
+        codes = t.empty((rows, in_f // 2), dtype=t.uint8, device=wd.device)
+        e8 = t.empty((rows, in_f // 32), dtype=t.uint8, device=wd.device)
+        sz = t.empty((E, out_f // 16, in_f // 128, 16), dtype=t.int32, device=wd.device)
+        nat.check_rc(lib.fastllm_quantize_mxfp4(nat.ptr(w2), nat.ptr(codes), nat.ptr(e8), rows, in_f,
+                                                hs), "fastllm_quantize_mxfp4")
+        nat.check_rc(lib.fastllm_moe_mxfp4_tile_repack(nat.ptr(codes), nat.ptr(e8), nat.ptr(qt),
+                                                       nat.ptr(sz), rows, in_f, hs),
+                     "fastllm_moe_mxfp4_tile_repack")
+    return {f"{proj}.qtile": qt, f"{proj}.sz": sz, f"{proj}.shape": (out_f, in_f)}
+
+
+def build_stacked_experts_lowp(expert_ws, fmt: str) -> dict:
+    """``build_stacked_experts`` with FP8 (128x128 block e4m3) or MXFP4
+    expert weights: the tensor-core fused-MoE variant of
+    docs/next-optimizations.md:160-184.  ``expert_ws`` is a list over
+    experts of {"gate", "up", "down"} float weights (out, in).  The dict
+    goes to moe_forward / moe_route_forward like the INT4 one."""
+    t = nat.torch()
+    code, group = LOWP_FORMATS.get(fmt, (None, None))
+    if code is None:
+        raise ValueError(f"build_stacked_experts_lowp: unknown format {fmt!r} (fp8, mxfp4)")
+    out = {"group": group, "format": fmt, "layout": "tile16x128"}
+    for proj in ("gate", "up", "down"):
+        ws = [w[proj] for w in expert_ws]
+        stack = (t.stack([nat.to_device(w, t.float32) for w in ws]) if nat.is_tensor(ws[0])
+                 else np.stack([np.asarray(w, np.float32) for w in ws]))
+        out.update(stack_lowp(fmt, proj, stack))
+    return out
+
+
+def _format_code(stacked, shared=None) -> int:
+    """0 for INT4 stacks, else the low-precision format code (shared expert
+    in the same format)."""
+    fmt = stacked.get("format", "int4")
+    sfmt = shared.get("format", "int4") if shared is not None else fmt
+    if sfmt != fmt:
+        raise ValueError(f"fused MoE: routed experts are {fmt}, the shared expert {sfmt}")
+    if fmt == "int4":
+        return 0
+    if fmt not in LOWP_FORMATS:
+        raise ValueError(f"fused MoE: unknown expert format {fmt!r}")
+    return LOWP_FORMATS[fmt][0]
+
+
 def unpack_stacked(stacked) -> dict:
     """Tile-layout stacked experts -> row-major {proj}.qweight (E, out, in/2)
     u8, {proj}.scales / {proj}.zeros (E, out, in/gs) fp16 device tensors."""
@@ -333,13 +416,19 @@ def moe_forward(x, stacked, E, hidden, inter, lists, *, max_slots=None, max_entr
     y = out if out is not None else t.empty((T, hidden), dtype=t.float32, device=xd.device)
     sp = _stacked_ptrs(shared) if shared is not None else [None] * 6
     h = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
-    rc = nat.lib().fastllm_moe_int4_fused(
-        nat.ptr(x2), T, hidden, stacked["group"], E, inter, *_stacked_ptrs(stacked), sint, *sp,
-        nat.ptr(shared_coef) if shared_coef is not None else None,
-        nat.ptr(lists["n_active"]), nat.ptr(lists["active"]), nat.ptr(lists["offsets"]),
-        nat.ptr(lists["tok"]), nat.ptr(lists["tokw"]), int(max_slots), int(max_entries), nat.ptr(ws),
-        ws.numel() * ws.element_size(), nat.ptr(y), h)
-    nat.check_rc(rc, "fastllm_moe_int4_fused")
+    code = _format_code(stacked, shared)
+    if code and T > 16:
+        raise ValueError(f"moe_forward: {stacked['format']} experts run the decode kernels "
+                         f"(T <= 16), got T={T}")
+    args = [nat.ptr(x2), T, hidden, stacked["group"], E, inter, *_stacked_ptrs(stacked), sint, *sp,
+            nat.ptr(shared_coef) if shared_coef is not None else None,
+            nat.ptr(lists["n_active"]), nat.ptr(lists["active"]), nat.ptr(lists["offsets"]),
+            nat.ptr(lists["tok"]), nat.ptr(lists["tokw"]), int(max_slots), int(max_entries),
+            nat.ptr(ws), ws.numel() * ws.element_size(), nat.ptr(y), h]
+    if code:
+        nat.check_rc(nat.lib().fastllm_moe_lowp_fused(code, *args), "fastllm_moe_lowp_fused")
+    else:
+        nat.check_rc(nat.lib().fastllm_moe_int4_fused(*args), "fastllm_moe_int4_fused")
     return y
 
 
@@ -397,9 +486,15 @@ def moe_route_forward(x, logits, stacked, top_k, E, hidden, inter, *, norm_topk_
     h = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
     args = _routed_args(s, top_k, scoring, norm_topk_prob, routed_scaling, bias, n_group,
                         topk_group, sl, o, x2, T, hidden, stacked, E, inter, shared, sint)
-    rc = nat.lib().fastllm_moe_int4_routed(*args, nat.ptr(ws), ws.numel() * ws.element_size(),
-                                           nat.ptr(y), h)
-    nat.check_rc(rc, "fastllm_moe_int4_routed")
+    code = _format_code(stacked, shared)
+    if code:
+        rc = nat.lib().fastllm_moe_lowp_routed(code, *args, nat.ptr(ws), ws.numel() * ws.element_size(),
+                                               nat.ptr(y), h)
+        nat.check_rc(rc, "fastllm_moe_lowp_routed")
+    else:
+        rc = nat.lib().fastllm_moe_int4_routed(*args, nat.ptr(ws), ws.numel() * ws.element_size(),
+                                               nat.ptr(y), h)
+        nat.check_rc(rc, "fastllm_moe_int4_routed")
     return y
 
 
@@ -466,6 +561,9 @@ def moe_route_forward_noalloc(x, logits, stacked, top_k, E, hidden, inter, *, ro
         if buf is None or buf.dtype != getattr(t, dt) or not buf.is_contiguous() \
                 or buf.numel() < n:
             raise ValueError(f"moe_route_forward_noalloc: route[{k!r}] must hold {n} {dt}")
+    if _format_code(stacked, shared):
+        raise ValueError("moe_route_forward_noalloc: INT4 experts only (FP8 / MXFP4 experts take "
+                         "moe_route_forward)")
     bias = None
     if scoring == "sigmoid" and e_score_bias is not None:
         bias = e_score_bias

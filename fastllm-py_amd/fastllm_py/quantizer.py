@@ -135,3 +135,40 @@ def dequantize_int4_group(qt: QuantizedTensor, xp=np):
                                                  nat.current_stream_handle())
     nat.check_rc(rc, "fastllm_dequantize_int4_group")
     return nat.as_output(out, numpy_in)
+
+
+def quantize_mxfp4(w, xp=np) -> QuantizedTensor:
+    """OCP MXFP4 (Microscaling v1.0): blocks of 32 consecutive in_features
+    share a power-of-two scale 2^(floor(log2 amax) - 2), stored as an E8M0
+    byte; elements are E2M1 (magnitudes 0, 0.5, 1, 1.5, 2, 3, 4, 6) rounded to
+    nearest, ties to the even code, saturating at 6.  data (out, in/2) uint8,
+    even column in the low nibble; scales (out, in/32) uint8 E8M0; block_size
+    32.  No reference counterpart: the format of the planned MXFP4 experts
+    (docs/next-optimizations.md:160-184)."""
+    t = nat.torch()
+    numpy_in = nat.host_out(w, xp)
+    wd = _f32_device(w).contiguous()
+    out_f, in_f = wd.shape
+    if in_f % 32:
+        raise ValueError(f"quantize_mxfp4: in_features {in_f} is not a multiple of 32")
+    codes = t.empty((out_f, in_f // 2), dtype=t.uint8, device=wd.device)
+    e8 = t.empty((out_f, in_f // 32), dtype=t.uint8, device=wd.device)
+    rc = nat.lib().fastllm_quantize_mxfp4(nat.ptr(wd), nat.ptr(codes), nat.ptr(e8), out_f, in_f,
+                                          nat.current_stream_handle())
+    nat.check_rc(rc, "fastllm_quantize_mxfp4")
+    return QuantizedTensor("mxfp4", nat.as_output(codes, numpy_in), nat.as_output(e8, numpy_in),
+                           (out_f, in_f), 32)
+
+
+def dequantize_mxfp4(qt: QuantizedTensor, xp=np):
+    """E2M1(code) * 2^(e8 - 127) as float32 (out, in)."""
+    t = nat.torch()
+    numpy_in = nat.host_out(qt.data, xp)
+    out_f, in_f = qt.shape
+    c = nat.to_device(qt.data, t.uint8).contiguous()
+    e = nat.to_device(qt.scales, t.uint8).contiguous()
+    out = t.empty((out_f, in_f), dtype=t.float32, device=c.device)
+    rc = nat.lib().fastllm_dequantize_mxfp4(nat.ptr(c), nat.ptr(e), nat.ptr(out), out_f, in_f,
+                                            nat.current_stream_handle())
+    nat.check_rc(rc, "fastllm_dequantize_mxfp4")
+    return nat.as_output(out, numpy_in)

@@ -270,6 +270,21 @@ int fastllm_dequantize_fp8_block(const uint8_t *q, const float *scales,
                                  float *out, int rows, int cols,
                                  int block_size, void *stream);
 
+/* MXFP4 (OCP Microscaling v1.0, section 6.3): w f32 [rows, cols], cols % 32
+ * == 0 -> codes u8 [rows, cols/2] (E2M1, column 2i in the low nibble of byte
+ * i) and e8 u8 [rows, cols/32] (E8M0 exponent + 127 of each 32-column
+ * block).  Block scale X = 2^(floor(log2 amax) - 2), exponent clamped to
+ * [-127, 127], X = 1 for an all-zero block; codes = w / X rounded to
+ * nearest E2M1, ties to the even code, saturating at 6, sign kept.  Finite
+ * inputs only.
+ * No reference counterpart: the reference plans MXFP4 expert weights
+ * (docs/next-optimizations.md:160-184) without a format of its own. */
+int fastllm_quantize_mxfp4(const float *w, uint8_t *codes, uint8_t *e8,
+                           long rows, int cols, void *stream);
+/* E2M1(code) * 2^(e8 - 127) -> f32 [rows, cols]. */
+int fastllm_dequantize_mxfp4(const uint8_t *codes, const uint8_t *e8,
+                             float *out, long rows, int cols, void *stream);
+
 /* ------------------------------------------------------------------------
  * FP8-E4M3 block-scaled GEMV
  * Return 0 on success, 1 on bad arguments, 2 on a device/launch error
@@ -415,6 +430,26 @@ int fastllm_moe_int4_tile_unpack(const uint8_t *qtile, const uint32_t *sz,
                                  long rows, int in_f, int group_size,
                                  void *stream);
 
+/* Low-precision expert tiles for fastllm_moe_lowp_* (rows % 16 == 0,
+ * in_f % 128 == 0; stacked experts are rows e * out + r):
+ *  - FP8: row-major e4m3 codes q u8 [rows, in_f] (fastllm_quantize_fp8_block
+ *    with 128x128 blocks, out % 128 == 0 so no block straddles two experts)
+ *    -> qtile u8 [rows/16, in_f/128, 2048]: block (t, kb) holds at byte
+ *    32*(c + 16*q) the 32 codes of row 16*t + c, k = 128*kb + 32*q .. + 31.
+ *    The block scales f32 [rows/128, in_f/128] are used as they are.
+ *  - MXFP4: codes u8 [rows, in_f/2] and e8 u8 [rows, in_f/32] from
+ *    fastllm_quantize_mxfp4 -> qtile u8 [rows/16, in_f/128, 1024] whose
+ *    block (t, kb) holds at byte 16*(c + 16*q) + 4*j the 8 codes of row
+ *    16*t + c, k = 128*kb + 32*j + 8*q .. + 7 (row-major bytes
+ *    64*kb + 16*j + 4*q .. + 3), and e8w u32 [rows/16, in_f/128, 16] whose
+ *    word (t, kb, c) holds the E8M0 bytes of blocks 4*kb + j, byte j.
+ * No reference counterpart (the layouts feed this library's MFMA kernels). */
+int fastllm_moe_fp8_tile_repack(const uint8_t *q, uint8_t *qtile, long rows,
+                                int in_f, void *stream);
+int fastllm_moe_mxfp4_tile_repack(const uint8_t *codes, const uint8_t *e8,
+                                  uint8_t *qtile, uint32_t *e8w, long rows,
+                                  int in_f, void *stream);
+
 /* Bytes of device workspace fastllm_moe_int4_fused needs for this shape
  * (0 when the shape is unsupported). */
 size_t fastllm_moe_int4_workspace_bytes(int T, int hidden, int inter,
@@ -466,6 +501,53 @@ int fastllm_moe_int4_fused(const float *x, int T, int hidden, int group_size,
  * (fastllm_py/graph_decode.py:669-700). */
 int fastllm_moe_int4_routed(const float *logits, int top_k, int scoring,
                             int norm, float routed_scaling,
+                            const float *e_score_bias, int n_group,
+                            int topk_group, const float *shared_logit,
+                            int *topk_ids, float *topk_w, float *rw,
+                            float *shared_coef, int *n_active, int *active,
+                            int *offsets, int *tok, float *tokw,
+                            const float *x, int T, int hidden, int group_size,
+                            int E, int inter, const uint8_t *gq,
+                            const uint32_t *gsz, const uint8_t *uq,
+                            const uint32_t *usz, const uint8_t *dq,
+                            const uint32_t *dsz, int shared_inter,
+                            const uint8_t *sgq, const uint32_t *sgsz,
+                            const uint8_t *suq, const uint32_t *susz,
+                            const uint8_t *sdq, const uint32_t *sdsz,
+                            void *workspace, size_t workspace_bytes, float *y,
+                            void *stream);
+
+/* The fused MoE with FP8 or MXFP4 expert weights, T <= 16 tokens (the
+ * decode kernels; the workspace is sized as for INT4 by
+ * fastllm_moe_int4_workspace_bytes).  format FASTLLM_MOE_FP8 (group_size
+ * must be 128): gq/uq/dq are the FP8 tiles and gsz/usz/dsz the f32 block
+ * scales (passed as uint32 pointers); FASTLLM_MOE_MXFP4 (group_size 32):
+ * the MXFP4 tiles and scale words.  The codes become fp16 exactly and run on
+ * the f16 matrix cores against the fp16 activations; block scales multiply
+ * the fp32 results.  Other arguments, outputs and return codes as
+ * fastllm_moe_int4_fused / fastllm_moe_int4_routed; other formats or T > 16
+ * return 1.
+ * No single reference counterpart: the tensor-core fused MoE with FP8 /
+ * MXFP4 experts of docs/next-optimizations.md:160-184 (the reference's
+ * graph path runs INT4 experts only, fastllm_py/graph_decode.py:669-700). */
+#define FASTLLM_MOE_FP8 1
+#define FASTLLM_MOE_MXFP4 2
+int fastllm_moe_lowp_fused(int format, const float *x, int T, int hidden,
+                           int group_size, int E, int inter,
+                           const uint8_t *gq, const uint32_t *gsz,
+                           const uint8_t *uq, const uint32_t *usz,
+                           const uint8_t *dq, const uint32_t *dsz,
+                           int shared_inter, const uint8_t *sgq,
+                           const uint32_t *sgsz, const uint8_t *suq,
+                           const uint32_t *susz, const uint8_t *sdq,
+                           const uint32_t *sdsz, const float *shared_coef,
+                           const int *n_active, const int *active,
+                           const int *offsets, const int *tok,
+                           const float *tokw, int max_slots, int max_entries,
+                           void *workspace, size_t workspace_bytes, float *y,
+                           void *stream);
+int fastllm_moe_lowp_routed(int format, const float *logits, int top_k,
+                            int scoring, int norm, float routed_scaling,
                             const float *e_score_bias, int n_group,
                             int topk_group, const float *shared_logit,
                             int *topk_ids, float *topk_w, float *rw,
