@@ -431,8 +431,18 @@ def run_fp8_prefill(torch, lib, stream, M=512):
 
 
 # ------------------------------------------------------------------- MoE
-def run_moe(torch, lib, stream, T_list=(1, 16)):
-    """Fused Qwen1.5-MoE-A2.7B INT4 layer: router from fp16 logits ~ N(0,1)
+def moe_weight_bytes(fmt, out_f, in_f):
+    """Packed bytes of one (out, in) expert matrix: INT4 g128 (nibbles + fp16
+    scale and zero per group), FP8 (codes + fp32 per 128x128 block), MXFP4
+    (nibbles + one E8M0 byte per 32)."""
+    n = out_f * in_f
+    return {"int4": n // 2 + n // 128 * 4, "fp8": n + n // (128 * 128) * 4,
+            "mxfp4": n // 2 + n // 32}[fmt]
+
+
+def run_moe(torch, lib, stream, T_list=(1, 16), fmt="int4"):
+    """Fused Qwen1.5-MoE-A2.7B layer with `fmt` expert weights (INT4 g128,
+    FP8 128x128-block e4m3 or MXFP4): router from fp16 logits ~ N(0,1)
     (top-4 softmax, no renorm) + routed experts + shared expert (sigmoid gate).
     Timed unit = one layer: router + gate/up + down launches
     (moe_route_forward)."""
@@ -445,18 +455,23 @@ def run_moe(torch, lib, stream, T_list=(1, 16)):
 
     def stacked(d, proj, n, out_f, in_f):
         w = (torch.randn((n, out_f, in_f), generator=gen, device="cuda") * 0.02).half()
-        qw, sc, ze, _ = moe_int4._quantize_int4_rowmajor_batched(w, 128)
-        d.update(moe_int4.stack_tiles(proj, qw, sc, ze, 128))
+        if fmt == "int4":
+            qw, sc, ze, _ = moe_int4._quantize_int4_rowmajor_batched(w, 128)
+            d.update(moe_int4.stack_tiles(proj, qw, sc, ze, 128))
+        else:
+            d.update(moe_int4.stack_lowp(fmt, proj, w.float()))
 
     def layer():
-        st, sh = {"group": 128}, {"group": 128}
+        meta = {"group": 128} if fmt == "int4" else {"group": moe_int4.LOWP_FORMATS[fmt][1],
+                                                     "format": fmt}
+        st, sh = dict(meta), dict(meta)
         for d, n, inn in ((st, E, inter), (sh, 1, sinter)):
             for proj, (o, i) in (("gate", (inn, hidden)), ("up", (inn, hidden)),
                                  ("down", (hidden, inn))):
                 stacked(d, proj, n, o, i)
         return st, sh
-    expert_bytes = 3 * inter * hidden // 2 + 3 * inter * hidden // 128 * 4
-    shared_bytes = 3 * sinter * hidden // 2 + 3 * sinter * hidden // 128 * 4
+    expert_bytes = 3 * moe_weight_bytes(fmt, inter, hidden)
+    shared_bytes = 3 * moe_weight_bytes(fmt, sinter, hidden)
     # layer copies: one token's routed set + the shared expert, over 2.2x MALL
     nl = copies_for(K * expert_bytes + shared_bytes)
     layers = [layer() for _ in range(nl)]
@@ -811,7 +826,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--only", default="int4,swiglu,layer,group,rm,fp8,fp8p,moe,gemm")
+    ap.add_argument("--only", default="int4,swiglu,layer,group,rm,fp8,fp8p,moe,moelp,gemm")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy a 64 MiB buffer 5 times (a known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -891,6 +906,10 @@ def main():
     if "moe" in only:
         breakdown["moe_qwen15_a27b_int4"] = run_moe(torch, lib, stream)
         log(f"MoE: {breakdown['moe_qwen15_a27b_int4']}")
+    if "moelp" in only:
+        for fmt in ("fp8", "mxfp4"):
+            breakdown[f"moe_qwen15_a27b_{fmt}"] = run_moe(torch, lib, stream, fmt=fmt)
+            log(f"MoE {fmt}: {breakdown[f'moe_qwen15_a27b_{fmt}']}")
 
     head = per_m[ms_list[0]]
     M0 = ms_list[0]
