@@ -440,6 +440,30 @@ FL_DEV uint32_t wave_umax(uint32_t k) {
     return umax4(r0, r1, r2, r3);
 }
 
+// np_sum_f32 of n <= 64 values held one per lane in v0, also stored at a[e]
+// (LDS): np_sum_wave128 with at most eight 8-value blocks.
+FL_DEV float np_sum_wave64(const float* a, int n, int lane, float v0) {
+    float res = 0.0f;
+    int i0 = 0;
+    if (n >= 8) {
+        const int q = n >> 3;  // 8-value blocks, 1..8
+        const int j = lane & 7;
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = a[8 * i + j];
+        float r = x[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) r = i < q ? r + x[i] : r;
+        r = r + bitcast<float>(__builtin_amdgcn_update_dpp(0, bitcast<int>(r), 0xB1, 0xF, 0xF, false));
+        r = r + bitcast<float>(__builtin_amdgcn_update_dpp(0, bitcast<int>(r), 0x4E, 0xF, 0xF, false));
+        r = r + bitcast<float>(__builtin_amdgcn_update_dpp(0, bitcast<int>(r), 0x141, 0xF, 0xF, false));
+        res = bitcast<float>(__builtin_amdgcn_readlane(bitcast<int>(r), 0));
+        i0 = 8 * q;
+    }
+    for (int i = i0; i < n; ++i) res += bitcast<float>(__builtin_amdgcn_readlane(bitcast<int>(v0), i));
+    return res;
+}
+
 // numpy's float32 row sum (np_sum_f32) of n <= 128 values held one per lane
 // in v[0] (e < 64) and v[1] (e >= 64), also stored at a[e] (LDS): lanes
 // j < 8 read their accumulator's values a[j + 8 i] at once and add them in
@@ -636,7 +660,9 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        const float z = E <= 128 ? np_sum_wave128(exw, E, lane, p[0], p[1]) : np_sum_wave(exw, E, lane);
+        const float z = E <= 64    ? np_sum_wave64(exw, E, lane, p[0])
+                        : E <= 128 ? np_sum_wave128(exw, E, lane, p[0], p[1])
+                                   : np_sum_wave(exw, E, lane);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int e = lane + 64 * c;
@@ -718,6 +744,22 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
     my_id = 0;
     my_w = 0.f;
     bool tie = false;  // some round's maximum held by more than one expert
+    if (nc == 1) {
+        // one expert per lane (E <= 64): the same rounds without slot loops
+        uint32_t k0 = key[0];
+        for (int i = 0; i < K; ++i) {
+            const uint32_t m = wave_umax(k0);
+            const unsigned long long bm = __ballot(k0 == m);
+            const int l = __builtin_ctzll(bm);
+            tie |= (bm & (bm - 1ull)) != 0ull;
+            const float w = bitcast<float>(__builtin_amdgcn_readlane(bitcast<int>(p[0]), l));
+            k0 = lane == l ? 0u : k0;
+            if (lane == i) {
+                my_id = l;
+                my_w = w;
+            }
+        }
+    } else {
     for (int i = 0; i < K; ++i) {
         const uint32_t m = wave_umax(umax4(key[0], key[1], key[2], key[3]));
         int e = 0, holders = 0;
@@ -742,6 +784,7 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
             my_id = e;
             my_w = w;
         }
+    }
     }
     if (tie) {
         // numpy's argpartition(-select)[:K]: the set at a tied k-th value and
