@@ -1993,7 +1993,10 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
     if (p.nb_gu > 4) return false;  // hidden <= 4096
     p.waves_gu = (nfh + p.nb_gu - 1) / p.nb_gu;
     const size_t as_bytes = (size_t)p.waves_gu * p.nb_gu * ((T + 3) & ~3) * 256;
-    p.tr_gu = fmt == kFmtFp8 ? 1 : gu_tiles(T);
+    // FP8 blocks take twice the weight registers: four tiles only with two
+    // blocks per wave, two with more
+    p.tr_gu = gu_tiles(T);
+    if (fmt == kFmtFp8 && p.tr_gu > 1 && (hidden / 128 + 7) / 8 > 2) p.tr_gu = 2;
     const size_t red_bytes = (size_t)p.waves_gu * 2 * p.tr_gu * 1024;
     p.lds_gu = (as_bytes > red_bytes ? as_bytes : red_bytes) + (size_t)2 * p.tr_gu * 1024 + 16 * 4;
     if (p.lds_gu > 160 * 1024) return false;
@@ -2021,17 +2024,12 @@ void launch_gate_up(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
     const int TR = p.tr_gu;
     const int grid = a.max_slots * (a.routed.inter / (16 * TR)) +
                      (a.has_shared ? a.shared.inter / (16 * TR) : 0);
-    if constexpr (FMT == kFmtFp8) {  // two 16-byte loads per block: one tile per workgroup
-        hipLaunchKernelGGL((moe_gate_up_k<FMT, G128, NB, 1>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu, st,
-                           a);
-    } else {
-        if (TR == 1)
-            hipLaunchKernelGGL((moe_gate_up_k<FMT, G128, NB, 1>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu,
-                               st, a);
-        else
-            hipLaunchKernelGGL((moe_gate_up_k<FMT, G128, NB, 4>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu,
-                               st, a);
-    }
+    if (TR == 1)
+        hipLaunchKernelGGL((moe_gate_up_k<FMT, G128, NB, 1>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu, st, a);
+    else if (FMT == kFmtFp8 && TR == 2)
+        hipLaunchKernelGGL((moe_gate_up_k<FMT, G128, NB, 2>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu, st, a);
+    else
+        hipLaunchKernelGGL((moe_gate_up_k<FMT, G128, NB, 4>), dim3(grid), dim3(64 * p.waves_gu), p.lds_gu, st, a);
 }
 
 template <int FMT, bool G128, int NB>
