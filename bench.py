@@ -410,13 +410,18 @@ def run_fp8_prefill(torch, lib, stream, M=512):
         del W
         x = torch.randn((M, K), generator=gen, device="cuda").to(torch.bfloat16)
         y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-        f = lib.fastllm_fp8_b128x128_gemv
+        # the Python layer's entry (kernels.fp8.fp8_gemv_block): split-K for
+        # grids under 256 tiles, partials in a zeroed workspace
+        f = lib.fastllm_fp8_b128x128_gemm_ws
+        wsb = lib.fastllm_fp8_b128x128_gemm_ws_bytes(M, N, K)
+        ws = torch.zeros(max(wsb, 1), dtype=torch.uint8, device="cuda")
         n = copies_for(N * K)
         cps = [(qt.data, qt.scales)] + [(qt.data.clone(), qt.scales.clone()) for _ in range(n - 1)]
 
-        def mk(q, s, x=x, y=y, N=N, K=K):
+        def mk(q, s, x=x, y=y, N=N, K=K, ws=ws, wsb=wsb):
             def go(h):
-                if f(x.data_ptr(), q.data_ptr(), s.data_ptr(), None, y.data_ptr(), M, N, K, 1, h):
+                if f(x.data_ptr(), q.data_ptr(), s.data_ptr(), None, y.data_ptr(), M, N, K, 1,
+                     ws.data_ptr(), wsb, h):
                     raise RuntimeError("fp8 gemm failed")
             return go
         seq = [mk(q, s) for q, s in cps]

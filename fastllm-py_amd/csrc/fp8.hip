@@ -641,20 +641,31 @@ constexpr int kF8Ahead = 1, kF8Stages = kF8Ahead + 1;
 constexpr int kF8StA = 0, kF8StB = 16384, kF8Stage = kF8StB + 16384;
 constexpr size_t kF8Lds = (size_t)kF8Stages * kF8Stage;
 
+// Split-K (gridDim.y > 1, grids of fewer than 256 tiles): split y takes 128-k
+// blocks [y kb_per, (y + 1) kb_per); each split stores its fp32 64 x 128
+// accumulator tile (thread order) with device-coherent stores, waits for
+// them, and bumps the tile's counter; the split that finds gridDim.y - 1
+// sums the tiles in split order (deterministic), finishes the epilogue and
+// resets the counter.  Nothing waits on another workgroup.
+constexpr int kF8TileF = kF8BM * kF8BN;  // fp32 partials per tile and split
+
 template <bool BF16>
 __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict__ A,
                                                      const uint8_t* __restrict__ W,
                                                      const float* __restrict__ Sc,
                                                      const uint16_t* __restrict__ bias,
                                                      uint16_t* __restrict__ C, int M, int N, int K,
-                                                     int nks) {
+                                                     int nks, int kb_per, float* __restrict__ part,
+                                                     int* __restrict__ cnt) {
     constexpr int D = kF8Ahead, NS = kF8Stages, NTW = kF8NTW, AF = kF8AF;
     constexpr int LPB = AF + 2 * NTW;  // copies per block and wave: A fragments, 2 halves per tile
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, kq = lane >> 4;
-    const int nkb = (K + 127) >> 7;  // a trailing 64-wide block counts as one
+    const int nkb_all = (K + 127) >> 7;  // a trailing 64-wide block counts as one
+    const int kb_lo = (int)blockIdx.y * kb_per;
+    const int nkb = (nkb_all - kb_lo) < kb_per ? (nkb_all - kb_lo) : kb_per;  // this split's blocks
     const int ntiles = (N + 15) >> 4;
 
     const int nblk = (N + kF8BN - 1) / kF8BN, mblk = (M + kF8BM - 1) / kF8BM;
@@ -689,7 +700,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
         for (int h = 0; h < 2; ++h) bo[t][h] = (uint32_t)n * K + 64 * h + 16 * kq;
     }
     auto issue = [&](int kb, int slot) {
-        kb = kb < nkb ? kb : nkb - 1;
+        kb = kb_lo + (kb < nkb ? kb : nkb - 1);
         unsigned char* st = smem + (size_t)slot * kF8Stage;
 #pragma unroll
         for (int i = 0; i < AF; ++i)
@@ -754,7 +765,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
             }
 #pragma unroll
             for (int t = 0; t < NTW; ++t) {
-                const float s = live ? srow[t][kb < nkb ? kb : nkb - 1] : 0.0f;
+                const float s = live ? srow[t][kb_lo + (kb < nkb ? kb : nkb - 1)] : 0.0f;
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -763,6 +774,41 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
         }
     }
     wait_vmcnt<0>();  // no LDS copy may still be in flight when the workgroup ends
+
+    if (gridDim.y > 1) {
+        static_assert(NTW == 1, "split-K partials assume one n-tile per wave");
+        __shared__ int last;
+        const int nsplit = (int)gridDim.y;
+        const size_t tile_off = (size_t)blockIdx.x * kF8TileF;
+        const size_t split_stride = (size_t)gridDim.x * kF8TileF;
+        float* mine = part + (size_t)blockIdx.y * split_stride + tile_off;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                __hip_atomic_store(mine + ((wave * 4 + mt) * 4 + e) * 64 + lane, acc[mt][0][e], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        // this wave's partial stores are complete (device-coherent stores: no
+        // cache write-back needed)
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(cnt + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   nsplit - 1;
+        __syncthreads();
+        if (!last) return;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const size_t idx = tile_off + ((wave * 4 + mt) * 4 + e) * 64 + lane;
+                float v = 0.0f;
+                for (int q = 0; q < nsplit; ++q)
+                    v += __hip_atomic_load(part + q * split_stride + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                acc[mt][0][e] = v;
+            }
+        if (threadIdx.x == 0) __hip_atomic_store(cnt + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 
 #pragma unroll
     for (int t = 0; t < NTW; ++t) {
@@ -817,9 +863,37 @@ hipError_t fp8_dispatch_nb(int nb, const uint16_t* A, const uint8_t* W, const fl
     }
 }
 
+// K splits of the prefill GEMM for M x N x K: grids under 256 tiles split
+// until they reach 256 workgroups, at most 4 splits of >= 16 blocks each
+// (1: no split).  M = 512: 2048 x 10944 118.6 -> 79.3 us with two splits;
+// 2048 x 2048 (16 blocks) gains nothing from two halves (26.7 us against
+// 25.2-27.1 whole), so short K stays whole.
+int fp8_gemm_splits(int M, int N, int K) {
+    const int tiles = ((N + kF8BN - 1) / kF8BN) * ((M + kF8BM - 1) / kF8BM);
+    const int nkb = (K + 127) / 128;
+    if (tiles >= 256) return 1;
+    int s = (256 + tiles - 1) / tiles;
+    s = s > 4 ? 4 : s;
+    while (s > 1 && nkb / s < 16) --s;
+    if (s > 1) s = (nkb + (nkb + s - 1) / s - 1) / ((nkb + s - 1) / s);  // no empty split
+    return s;
+}
+
+// workspace: the tile counters in a fixed 1 KB (only grids under 256 tiles
+// split), so calls of any shape on one workspace find theirs at zero, then
+// fp32 partials [split][tile][64 x 128]
+constexpr size_t kF8CntBytes = 256 * 4;
+size_t fp8_gemm_ws_bytes(int M, int N, int K) {
+    const int s = fp8_gemm_splits(M, N, K);
+    if (s <= 1) return 0;
+    const size_t tiles = (size_t)((N + kF8BN - 1) / kF8BN) * ((M + kF8BM - 1) / kF8BM);
+    return kF8CntBytes + (size_t)s * tiles * kF8TileF * 4;
+}
+
 template <bool INLINE, bool BF16>
 hipError_t fp8_gemm(const uint16_t* A, const uint8_t* W, const float* Sc, const uint16_t* bias,
-                    uint16_t* C, int M, int N, int K, int rs, int nks, hipStream_t st) {
+                    uint16_t* C, int M, int N, int K, int rs, int nks, hipStream_t st,
+                    void* ws = nullptr, size_t ws_bytes = 0) {
     // few 16-row strips and M <= 4: the quartered 4-row kernel up to
     // K = 8192; beyond, the halved kernel's activation traffic (half of the
     // quartered one's per weight byte) wins (2048 x 10944, M = 1: 8.4 us
@@ -833,8 +907,14 @@ hipError_t fp8_gemm(const uint16_t* A, const uint8_t* W, const float* Sc, const 
     if (!INLINE && M > kF8MinM && K % 64 == 0 && (size_t)N * K < (1ull << 31) &&
         (size_t)M * K * 2 < (1ull << 31)) {
         const int tiles = ((N + kF8BN - 1) / kF8BN) * ((M + kF8BM - 1) / kF8BM);
-        hipLaunchKernelGGL((fp8_gemm_mfma<BF16>), dim3(tiles), dim3(64 * kF8Waves), kF8Lds, st, A, W, Sc, bias, C, M,
-                           N, K, nks);
+        const int nkb = (K + 127) / 128;
+        int s = fp8_gemm_splits(M, N, K);
+        if (s > 1 && (!ws || !fl_aligned(ws, 256) || ws_bytes < fp8_gemm_ws_bytes(M, N, K))) s = 1;
+        const int kb_per = (nkb + s - 1) / s;
+        int* cnt = s > 1 ? static_cast<int*>(ws) : nullptr;
+        float* part = s > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kF8CntBytes) : nullptr;
+        hipLaunchKernelGGL((fp8_gemm_mfma<BF16>), dim3(tiles, s), dim3(64 * kF8Waves), kF8Lds, st, A, W, Sc, bias, C,
+                           M, N, K, nks, kb_per, part, cnt);
         return hipGetLastError();
     }
     // decode-shaped kernel, 16 activation rows per launch
@@ -960,9 +1040,9 @@ int fastllm_fp8_block128_gemv_stream(const void* A, const void* weight, void* C,
     return fp8_inline_gemv(A, weight, C, bias, n, m, k, perRow, isBf16, (hipStream_t)stream);
 }
 
-int fastllm_fp8_b128x128_gemv(const void* A, const uint8_t* Wq, const float* scales,
-                              const void* bias, void* C, int M, int N, int K, int isBf16,
-                              void* stream) {
+static int fp8_b128x128_impl(const void* A, const uint8_t* Wq, const float* scales,
+                             const void* bias, void* C, int M, int N, int K, int isBf16,
+                             void* stream, void* ws, size_t ws_bytes) {
     if (M <= 0 || N <= 0 || K <= 0 || (K % 64) != 0 || !A || !Wq || !scales || !C) return 1;
     if (K < 128) return 1;
     if (!fl_aligned(A, 16) || !fl_aligned(Wq, 16) || (K % 16) != 0) return 1;
@@ -970,14 +1050,32 @@ int fastllm_fp8_b128x128_gemv(const void* A, const uint8_t* Wq, const float* sca
     const int nks = (K + 127) / 128;
     const hipError_t e =
         isBf16 ? fp8_gemm<false, true>((const uint16_t*)A, Wq, scales, (const uint16_t*)bias,
-                                       (uint16_t*)C, M, N, K, K, nks, (hipStream_t)stream)
+                                       (uint16_t*)C, M, N, K, K, nks, (hipStream_t)stream, ws, ws_bytes)
                : fp8_gemm<false, false>((const uint16_t*)A, Wq, scales, (const uint16_t*)bias,
-                                        (uint16_t*)C, M, N, K, K, nks, (hipStream_t)stream);
+                                        (uint16_t*)C, M, N, K, K, nks, (hipStream_t)stream, ws, ws_bytes);
     if (e != hipSuccess) {
         fprintf(stderr, "fastllm_fp8_b128x128_gemv launch error: %s\n", hipGetErrorString(e));
         return 2;
     }
     return 0;
+}
+
+int fastllm_fp8_b128x128_gemv(const void* A, const uint8_t* Wq, const float* scales,
+                              const void* bias, void* C, int M, int N, int K, int isBf16,
+                              void* stream) {
+    return fp8_b128x128_impl(A, Wq, scales, bias, C, M, N, K, isBf16, stream, nullptr, 0);
+}
+
+size_t fastllm_fp8_b128x128_gemm_ws_bytes(int M, int N, int K) {
+    if (M <= kF8MinM || N <= 0 || K <= 0 || K % 64) return 0;
+    return fp8_gemm_ws_bytes(M, N, K);
+}
+
+int fastllm_fp8_b128x128_gemm_ws(const void* A, const uint8_t* Wq, const float* scales,
+                                 const void* bias, void* C, int M, int N, int K, int isBf16,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+    return fp8_b128x128_impl(A, Wq, scales, bias, C, M, N, K, isBf16, stream, workspace,
+                             workspace_bytes);
 }
 
 }  // extern "C"

@@ -54,6 +54,8 @@ SIGNATURES: dict[str, tuple] = {
     "fastllm_fp8_block128_gemv_fp16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "fastllm_fp8_block128_gemv_stream": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "fastllm_fp8_b128x128_gemv": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "fastllm_fp8_b128x128_gemm_ws_bytes": (_SZ, [_I, _I, _I]),
+    "fastllm_fp8_b128x128_gemm_ws": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P]),
     # row-major INT4 / router / fused MoE
     "fastllm_int4_rowmajor_gemv": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "fastllm_int4_group_gemv": (_I, [_P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),

@@ -92,10 +92,32 @@ def fp8_gemv(x_fp16, weight_fp8_block128, scales=None, out=None, k=None):
     return out
 
 
-def fp8_gemv_block(x, q, scales, out=None, bias=None, stream=None):
+# one zeroed split-K workspace per device for the prefill GEMM, grown as
+# shapes need it (its tile counters are left at zero by every call)
+_gemm_ws: dict = {}
+
+
+def _gemm_workspace(M: int, N: int, K: int):
+    t = nat.torch()
+    need = int(_load().fastllm_fp8_b128x128_gemm_ws_bytes(M, N, K))
+    if need == 0:
+        return None, 0
+    dev = t.cuda.current_device()
+    ws = _gemm_ws.get(dev)
+    if ws is None or ws.numel() < need:
+        ws = t.zeros(need, dtype=t.uint8, device="cuda")
+        _gemm_ws[dev] = ws
+    return ws, ws.numel()
+
+
+def fp8_gemv_block(x, q, scales, out=None, bias=None, stream=None, workspace=None):
     """128x128-block FP8 GEMV: x [M, K] fp16/bf16, q uint8 [N, K], scales fp32
     [ceil(N/128), ceil(K/128)] (quantizer.quantize_fp8_block's format).
-    Returns [M, N] in x's dtype.  K % 64 == 0, K >= 128."""
+    Returns [M, N] in x's dtype.  K % 64 == 0, K >= 128.  Above 64 rows with
+    fewer than 256 output tiles the GEMM splits K; its partials go to
+    ``workspace`` (a zeroed uint8 device tensor of at least
+    fastllm_fp8_b128x128_gemm_ws_bytes bytes) or to a per-device workspace
+    shared by calls without one (such calls must not overlap)."""
     t = nat.torch()
     lib = _load()
     x = nat.to_device(x)
@@ -109,9 +131,14 @@ def fp8_gemv_block(x, q, scales, out=None, bias=None, stream=None):
         out = t.empty((M, N), dtype=x.dtype, device=x.device)
     b = nat.to_device(bias, x.dtype) if bias is not None else None
     h = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
-    rc = lib.fastllm_fp8_b128x128_gemv(nat.ptr(x), nat.ptr(qd), nat.ptr(sd),
-                                       nat.ptr(b) if b is not None else None, nat.ptr(out),
-                                       M, N, K, 1 if x.dtype == t.bfloat16 else 0, h)
+    if workspace is not None:
+        ws, wsb = workspace, workspace.numel() * workspace.element_size()
+    else:
+        ws, wsb = _gemm_workspace(M, N, K)
+    rc = lib.fastllm_fp8_b128x128_gemm_ws(nat.ptr(x), nat.ptr(qd), nat.ptr(sd),
+                                          nat.ptr(b) if b is not None else None, nat.ptr(out),
+                                          M, N, K, 1 if x.dtype == t.bfloat16 else 0,
+                                          nat.ptr(ws) if ws is not None else None, wsb, h)
     if rc != 0:
-        raise RuntimeError(f"fastllm_fp8_b128x128_gemv failed (rc={rc})")
+        raise RuntimeError(f"fastllm_fp8_b128x128_gemm_ws failed (rc={rc})")
     return out

@@ -338,6 +338,24 @@ int fastllm_fp8_b128x128_gemv(const void *A, const uint8_t *Wq,
                               const float *scales, const void *bias, void *C,
                               int M, int N, int K, int isBf16, void *stream);
 
+/* fastllm_fp8_b128x128_gemv with a caller workspace for the prefill GEMM's
+ * split-K (M > 64 with fewer than 256 64x128 output tiles: the 2048-wide
+ * outputs): up to 4 splits of the 128-k blocks, each storing fp32 partials;
+ * the last split of each tile sums them in split order (deterministic) and
+ * writes C.  workspace: fastllm_fp8_b128x128_gemm_ws_bytes(M, N, K) bytes
+ * (0: no split for this shape), 256-byte aligned, zero-filled once (the
+ * tile counters sit in its first 1 KB for every shape and are left at
+ * zero, so one workspace serves calls of any shape); calls sharing a
+ * workspace must not overlap.  A smaller workspace runs unsplit.  Other arguments and
+ * return codes as fastllm_fp8_b128x128_gemv.
+ * No reference counterpart (the reference has no FP8 prefill GEMM). */
+size_t fastllm_fp8_b128x128_gemm_ws_bytes(int M, int N, int K);
+int fastllm_fp8_b128x128_gemm_ws(const void *A, const uint8_t *Wq,
+                                 const float *scales, const void *bias,
+                                 void *C, int M, int N, int K, int isBf16,
+                                 void *workspace, size_t workspace_bytes,
+                                 void *stream);
+
 /* ------------------------------------------------------------------------
  * Row-major INT4 GEMV, router, fused selective INT4 MoE
  * (kernels the reference launches as CuPy RawKernels).  Return 0 on

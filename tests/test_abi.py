@@ -111,3 +111,21 @@ def test_int4_split_workspace_sizes():
         for K in range(1024, 32768 + 1, 1024):
             for M in range(5, 17):
                 assert lib.fastllm_int4_gemm_ws_bytes(M, N, K, 128) <= 4 * _workspace_ints(N)
+
+
+def test_fp8_gemm_split_workspace_sizes():
+    """Split-K workspace query of the FP8 prefill GEMM (host arithmetic only):
+    grids under 256 64x128 tiles split (at most 4 splits of >= 4 blocks),
+    larger grids and decode shapes do not."""
+    lib = _native.lib()
+    tile = 64 * 128 * 4
+    # counters in a fixed 1 KB (every splitting grid has < 256 tiles), then partials
+    # M=512, N=2048: 8 x 16 = 128 tiles -> 2 splits where K gives >= 16 blocks each
+    assert lib.fastllm_fp8_b128x128_gemm_ws_bytes(512, 2048, 10944) == 1024 + 2 * 128 * tile
+    assert lib.fastllm_fp8_b128x128_gemm_ws_bytes(512, 2048, 2048) == 0  # 16 blocks: whole
+    # M=128, N=2048: 32 tiles -> 4 splits (86 blocks: 22 each)
+    assert lib.fastllm_fp8_b128x128_gemm_ws_bytes(128, 2048, 10944) == 1024 + 4 * 32 * tile
+    assert lib.fastllm_fp8_b128x128_gemm_ws_bytes(128, 2048, 4096) == 1024 + 2 * 32 * tile
+    assert lib.fastllm_fp8_b128x128_gemm_ws_bytes(512, 10944, 2048) == 0  # 688 tiles
+    assert lib.fastllm_fp8_b128x128_gemm_ws_bytes(16, 2048, 2048) == 0    # decode kernels
+    assert lib.fastllm_fp8_b128x128_gemm_ws_bytes(96, 256, 320) == 0      # 3 blocks: no split

@@ -182,3 +182,44 @@ def test_fp8_block_gemm_prefill(torch_gpu, M, N, K, bf16):
     ref = Q.matmul_ref(x.float().cpu().numpy(), Q.dequantize_fp8_block(q_ref, s_ref, 128))
     ref = ref + b.float().cpu().numpy()[None]
     assert Q.max_abs_rel(out.float().cpu().numpy(), ref) < TOL
+
+
+def test_fp8_block_gemm_split_k(torch_gpu):
+    """Split-K of the prefill GEMM (grids under 256 tiles): within the
+    oracle's tolerance, bit-identical on a repeat (partials summed in split
+    order), equal in tolerance to the unsplit entry, and one workspace shared
+    by calls of different shapes (tile counters left at zero)."""
+    from fastllm_py import _native, quantizer
+
+    torch = torch_gpu
+    lib = _native.lib()
+    rng = np.random.default_rng(8300)
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device="cuda")
+    outs = []
+    for M, N, K in ((512, 2048, 4096), (128, 2048, 10944), (200, 1000, 4096), (256, 2048, 8192)):
+        need = lib.fastllm_fp8_b128x128_gemm_ws_bytes(M, N, K)
+        assert 0 < need <= ws.numel(), (M, N, K, need)
+        W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda().to(torch.bfloat16)
+        b = torch.from_numpy(rng.standard_normal(N).astype(np.float32)).cuda().to(torch.bfloat16)
+        qt = quantizer.quantize_fp8_block(torch.from_numpy(W).cuda(), 128)
+        q_ref, s_ref = Q.quantize_fp8_block(W, 128)
+        ref = Q.matmul_ref(x.float().cpu().numpy(), Q.dequantize_fp8_block(q_ref, s_ref, 128))
+        ref = ref + b.float().cpu().numpy()[None]
+        args = (x.data_ptr(), qt.data.data_ptr(), qt.scales.data_ptr(), b.data_ptr())
+        y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+        assert lib.fastllm_fp8_b128x128_gemm_ws(*args, y.data_ptr(), M, N, K, 1, ws.data_ptr(),
+                                                ws.numel(), None) == 0
+        y0 = torch.empty_like(y)
+        assert lib.fastllm_fp8_b128x128_gemv(*args, y0.data_ptr(), M, N, K, 1, None) == 0
+        torch.cuda.synchronize()
+        assert Q.max_abs_rel(y.float().cpu().numpy(), ref) < TOL
+        assert Q.max_abs_rel(y.float().cpu().numpy(), y0.float().cpu().numpy()) < 1e-2
+        outs.append((args, M, N, K, y, (x, b, qt)))  # the tensors stay alive for the repeats
+    for args, M, N, K, y, _keep in outs:  # repeats after the other shapes on the same workspace
+        y2 = torch.empty_like(y)
+        assert lib.fastllm_fp8_b128x128_gemm_ws(*args, y2.data_ptr(), M, N, K, 1, ws.data_ptr(),
+                                                ws.numel(), None) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(y, y2), (M, N, K)
+    assert int(ws[:1024].count_nonzero()) == 0  # counters back at zero
