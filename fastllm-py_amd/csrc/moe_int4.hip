@@ -1250,6 +1250,22 @@ FL_DEV uint32_t fp4x2_f16(uint32_t w) {
 // 2^(e - 127) for an E8M0 byte (e = 0 gives 2^-127, a subnormal fp32)
 FL_DEV float e8m0_float(uint32_t e) { return e ? __uint_as_float(e << 23) : __uint_as_float(0x00400000u); }
 
+// MFMA step j's fp16 B operand of an FP8 / MXFP4 tile block (exact codes)
+template <int FMT>
+FL_DEV f16x8 wblk_operand(const WBlk<FMT>& b, int j) {
+    if (FMT == kFmtFp8) {
+        const uint32_t lo = j < 2 ? b.w[2 * j] : b.w2[2 * j - 4];
+        const uint32_t hi = j < 2 ? b.w[2 * j + 1] : b.w2[2 * j - 3];
+        return bitcast<f16x8>(u32x4{fp8x2_f16(lo, false), fp8x2_f16(lo, true), fp8x2_f16(hi, false),
+                                    fp8x2_f16(hi, true)});
+    }
+    const uint32_t w = b.w[j];
+    return bitcast<f16x8>(u32x4{fp4x2_f16<0>(w), fp4x2_f16<1>(w), fp4x2_f16<2>(w), fp4x2_f16<3>(w)});
+}
+
+// MXFP4: the scale of MFMA step j (the E8M0 byte j of the lane's column)
+FL_DEV float mx_step_scale(uint32_t sz, int j) { return e8m0_float((sz >> (8 * j)) & 0xFFu); }
+
 // acc += live * (tile block of weights) x (activation fragments a[j]): a[j]
 // is MFMA step j's A operand (k 32 q + 8 j for INT4 / FP8, 32 j + 8 q for
 // MXFP4, q the lane's quarter).
@@ -1260,23 +1276,15 @@ FL_DEV void wblk_mma(f32x4& acc, const u32x4 (&a)[4], const WBlk<FMT>& b, float 
     } else if (FMT == kFmtFp8) {
         f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t lo = j < 2 ? b.w[2 * j] : b.w2[2 * j - 4];
-            const uint32_t hi = j < 2 ? b.w[2 * j + 1] : b.w2[2 * j - 3];
-            const u32x4 bj{fp8x2_f16(lo, false), fp8x2_f16(lo, true), fp8x2_f16(hi, false),
-                           fp8x2_f16(hi, true)};
-            part = mfma_f16(bitcast<f16x8>(a[j]), bitcast<f16x8>(bj), part);
-        }
+        for (int j = 0; j < 4; ++j) part = mfma_f16(bitcast<f16x8>(a[j]), wblk_operand(b, j), part);
         const float s = __uint_as_float(b.sz) * live;
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(s, part[e], acc[e]);
     } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const uint32_t w = b.w[j];
-            const u32x4 bj{fp4x2_f16<0>(w), fp4x2_f16<1>(w), fp4x2_f16<2>(w), fp4x2_f16<3>(w)};
-            const f32x4 part = mfma_f16(bitcast<f16x8>(a[j]), bitcast<f16x8>(bj), f32x4{0.f, 0.f, 0.f, 0.f});
-            const float s = e8m0_float((b.sz >> (8 * j)) & 0xFFu) * live;
+            const f32x4 part = mfma_f16(bitcast<f16x8>(a[j]), wblk_operand(b, j), f32x4{0.f, 0.f, 0.f, 0.f});
+            const float s = mx_step_scale(b.sz, j) * live;
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(s, part[e], acc[e]);
         }
@@ -1674,10 +1682,11 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
 // block accumulate in fp32; m-tiles past the chunk's rows skip their MFMAs.
 constexpr int kMgAhead = 1, kMgStages = kMgAhead + 1;
 constexpr int kMgWaves = 8;                     // waves per workgroup
-constexpr int kMgWaveStage = 2 * 1024 + 2 * 256;  // B tiles + scale|zero rows
+// per wave and stage: two tile blocks (1 KB, FP8 2 KB) + two 256-byte scale rows
+constexpr int mg_wave_stage(int fmt) { return 2 * (fmt == kFmtFp8 ? 2048 : 1024) + 2 * 256; }
 constexpr int kMgABytes = 64 * 128 * 2;            // A tile of one stage
-constexpr int kMgStage = kMgABytes + kMgWaves * kMgWaveStage;
-constexpr size_t kMgLds = (size_t)kMgStages * kMgStage;
+constexpr int mg_stage(int fmt) { return kMgABytes + kMgWaves * mg_wave_stage(fmt); }
+constexpr size_t mg_lds(int fmt) { return (size_t)kMgStages * mg_stage(fmt); }
 
 // xh[t, :] = fp16(x[t, :]) for the grouped kernels' A copies
 __global__ void x_to_f16_k(const float* __restrict__ x, uint16_t* __restrict__ xh, int n8) {
@@ -1694,12 +1703,15 @@ __global__ void x_to_f16_k(const float* __restrict__ x, uint16_t* __restrict__ x
     }
 }
 
-template <int PHASE, bool G128>
+template <int PHASE, bool G128, int FMT = kFmtInt4>
 __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     constexpr int D = kMgAhead, NS = kMgStages;
     constexpr int NW = kMgWaves, FPW = 16 / NW;  // waves, A fragments copied per wave
-    constexpr int LPB = FPW + 2 + 2;  // per block and wave: A fragments, 2 B tiles, 2 sz rows
+    constexpr int BPT = FMT == kFmtFp8 ? 2 : 1;  // 1 KB copies per tile block
+    constexpr int TB = 1024 * BPT;               // tile block bytes
+    constexpr int WST = mg_wave_stage(FMT), STG = mg_stage(FMT);
+    constexpr int LPB = FPW + 2 * BPT + 2;  // per block and wave: A fragments, B copies, 2 scale rows
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, kq = lane >> 4;
@@ -1753,15 +1765,25 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
             tq = ex->dq;
             tsz = ex->dsz;
         }
-        rq[t] = buf_rsrc(tq + tile * nkb * 1024, nkb * 1024);
-        rz[t] = buf_rsrc(tsz + tile * G * 16, G * 64);
+        rq[t] = buf_rsrc(tq + tile * nkb * TB, nkb * TB);
+        if (FMT == kFmtFp8)  // one fp32 scale per (128-row band, block)
+            rz[t] = buf_rsrc(tsz + (tile >> 3) * nkb, nkb * 4);
+        else if (FMT == kFmtMx4)  // 16 E8M0 words per block
+            rz[t] = buf_rsrc(tsz + tile * nkb * 16, nkb * 64);
+        else
+            rz[t] = buf_rsrc(tsz + tile * G * 16, G * 64);
     }
     // A rows: PHASE 0 token rows of xh, PHASE 1 the slot's inter_buf rows
     const uint16_t* abase = PHASE == 0 ? a.xh : a.inter_buf;
     const int astride = PHASE == 0 ? a.hidden : a.inter_pad;  // halves
     const int arows = PHASE == 0 ? a.T : a.max_entries + a.T;
     const __amdgpu_buffer_rsrc_t rA = buf_rsrc(abase, (uint32_t)arows * astride * 2);
-    const uint32_t zlane = 4u * (lane < 16 * spb ? lane : 16 * spb - 1);
+    // scale-row copy: INT4 16 words per group, MXFP4 16 words, FP8 the one
+    // block scale (every lane copies it)
+    const uint32_t zlane = FMT == kFmtFp8 ? 0u
+                         : FMT == kFmtMx4 ? 4u * (lane < 16 ? lane : 15)
+                                          : 4u * (lane < 16 * spb ? lane : 16 * spb - 1);
+    const int zstep = FMT == kFmtFp8 ? 4 : (FMT == kFmtMx4 ? 64 : spb * 64);  // scale bytes per block
     const int g_local = kq * 32 / a.gs;  // this lane's group within a block
 
     for (int mc = 0; mc < M; mc += 64) {
@@ -1775,25 +1797,28 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
             m = m < M ? m : M - 1;
             const int row = PHASE == 0 ? (is_shared ? m : clampi(a.tok[row0 + m], 0, a.T - 1))
                                        : row0 + m;
-            ao[i] = 2u * ((uint32_t)row * astride + 32 * kq + 8 * (f & 3));
+            ao[i] = 2u * ((uint32_t)row * astride + a_koff<FMT>(kq, f & 3));
         }
         auto issue = [&](int kb, int stg) {
             kb = kb < nkb ? kb : nkb - 1;
-            unsigned char* st = smem + (size_t)stg * kMgStage;
+            unsigned char* st = smem + (size_t)stg * STG;
 #pragma unroll
             for (int i = 0; i < FPW; ++i)
                 if (kMgAhead > 1 || wave * FPW + i < 4 * mt_live)  // dead m-tiles: no copy
                     __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(st + (wave * FPW + i) * 1024),
                                                              16, ao[i], kb * 256, 0, 0);
-            unsigned char* wst = st + kMgABytes + wave * kMgWaveStage;
+            unsigned char* wst = st + kMgABytes + wave * WST;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rq[t], (lptr_t)(wst + t * 1024), 16,
-                                                         lane * 16, kb * 1024, 0, 0);
+#pragma unroll
+                for (int h = 0; h < BPT; ++h)  // FP8: lane l's 32 bytes at 32 l (two copies)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rq[t], (lptr_t)(wst + t * TB + h * 1024), 16,
+                                                             BPT == 2 ? lane * 32 + h * 16 : lane * 16,
+                                                             kb * TB, 0, 0);
 #pragma unroll
             for (int t = 0; t < 2; ++t)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rz[t], (lptr_t)(wst + 2048 + t * 256), 4,
-                                                         zlane, kb * spb * 64, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rz[t], (lptr_t)(wst + 2 * TB + t * 256), 4,
+                                                         zlane, kb * zstep, 0, 0);
         };
 
         f32x4 acc[4][2];
@@ -1808,8 +1833,64 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
             wait_vmcnt<(D - 1) * LPB>();
             asm volatile("s_barrier" ::: "memory");
             issue(kb + D, (kb + D) % NS);
-            const unsigned char* st = smem + (size_t)(kb % NS) * kMgStage;
-            const unsigned char* wst = st + kMgABytes + wave * kMgWaveStage;
+            const unsigned char* st = smem + (size_t)(kb % NS) * STG;
+            const unsigned char* wst = st + kMgABytes + wave * WST;
+            if constexpr (FMT != kFmtInt4) {
+                // FP8 / MXFP4: codes to fp16 once per (tile, step) for the
+                // four m-tiles; FP8 scales the block's partial once, MXFP4
+                // every step (one MX block per step)
+                WBlk<FMT> bl[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    bl[t].w = *reinterpret_cast<const u32x4*>(wst + t * TB + lane * 16);
+                    if (FMT == kFmtFp8) bl[t].w2 = *reinterpret_cast<const u32x4*>(wst + t * TB + 1024 + lane * 16);
+                    bl[t].sz = *reinterpret_cast<const uint32_t*>(wst + 2 * TB + t * 256 +
+                                                                  (FMT == kFmtMx4 ? 4 * col : 0));
+                }
+                const unsigned char* ab = st + lane * 16;
+                f32x4 part[4][2];
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) part[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    f16x8 av[4];
+#pragma unroll
+                    for (int mt = 0; mt < 4; ++mt)
+                        av[mt] = *reinterpret_cast<const f16x8*>(ab + (mt * 4 + j) * 1024);
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const f16x8 b = wblk_operand(bl[t], j);
+                        if (FMT == kFmtMx4) {
+                            const float sj = mx_step_scale(bl[t].sz, j);
+#pragma unroll
+                            for (int mt = 0; mt < 4; ++mt)
+                                if (mt < mt_live) {
+                                    const f32x4 p = mfma_f16(av[mt], b, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                                    for (int i = 0; i < 4; ++i) acc[mt][t][i] = __builtin_fmaf(sj, p[i], acc[mt][t][i]);
+                                }
+                        } else {
+#pragma unroll
+                            for (int mt = 0; mt < 4; ++mt)
+                                if (mt < mt_live) part[mt][t] = mfma_f16(av[mt], b, part[mt][t]);
+                        }
+                    }
+                }
+                if (FMT == kFmtFp8) {
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const float sv = __uint_as_float(bl[t].sz);
+#pragma unroll
+                        for (int mt = 0; mt < 4; ++mt)
+                            if (mt < mt_live)
+#pragma unroll
+                                for (int i = 0; i < 4; ++i) acc[mt][t][i] = __builtin_fmaf(sv, part[mt][t][i], acc[mt][t][i]);
+                    }
+                }
+                continue;
+            }
             u32x4 wv[2];
             uint32_t zlo[2], zhi[2];
             uint16_t sc[2];
@@ -2039,6 +2120,12 @@ void launch_down(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
                        st, a);
 }
 
+template <int FMT, bool G128>
+void launch_grouped_pair(const MoeArgs& a, dim3 gu, dim3 dn, hipStream_t st) {
+    hipLaunchKernelGGL((moe_gemm_k<0, G128, FMT>), gu, dim3(64 * kMgWaves), mg_lds(FMT), st, a);
+    hipLaunchKernelGGL((moe_gemm_k<1, G128, FMT>), dn, dim3(64 * kMgWaves), mg_lds(FMT), st, a);
+}
+
 void moe_launch_grouped(const MoeArgs& a, hipStream_t st) {
     const int n8 = a.T * a.hidden / 8;
     hipLaunchKernelGGL(x_to_f16_k, dim3((n8 + 255) / 256 < 1024 ? (n8 + 255) / 256 : 1024), dim3(256), 0,
@@ -2046,13 +2133,14 @@ void moe_launch_grouped(const MoeArgs& a, hipStream_t st) {
     const int slots = a.max_slots + (a.has_shared ? 1 : 0);
     const int inter_max = a.routed.inter > a.shared.inter ? a.routed.inter : a.shared.inter;
     const dim3 gu(inter_max / (16 * kMgWaves), slots), dn(a.hidden / (32 * kMgWaves), slots);
-    if (a.gs == 128) {
-        hipLaunchKernelGGL((moe_gemm_k<0, true>), gu, dim3(64 * kMgWaves), kMgLds, st, a);
-        hipLaunchKernelGGL((moe_gemm_k<1, true>), dn, dim3(64 * kMgWaves), kMgLds, st, a);
-    } else {
-        hipLaunchKernelGGL((moe_gemm_k<0, false>), gu, dim3(64 * kMgWaves), kMgLds, st, a);
-        hipLaunchKernelGGL((moe_gemm_k<1, false>), dn, dim3(64 * kMgWaves), kMgLds, st, a);
-    }
+    if (a.fmt == kFmtFp8)
+        launch_grouped_pair<kFmtFp8, true>(a, gu, dn, st);
+    else if (a.fmt == kFmtMx4)
+        launch_grouped_pair<kFmtMx4, true>(a, gu, dn, st);
+    else if (a.gs == 128)
+        launch_grouped_pair<kFmtInt4, true>(a, gu, dn, st);
+    else
+        launch_grouped_pair<kFmtInt4, false>(a, gu, dn, st);
 }
 
 template <int FMT, bool G128>
@@ -2239,7 +2327,7 @@ static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int
     if (fmt == kFmtInt4 && group_size != 32 && group_size != 64 && group_size != 128) return 1;
     if (fmt == kFmtFp8 && group_size != 128) return 1;
     if (fmt == kFmtMx4 && group_size != 32) return 1;
-    if (fmt != kFmtInt4 && (T > 16 || inter % 128 || hidden % 128)) return 1;  // decode kernels only
+    if (fmt != kFmtInt4 && (inter % 128 || hidden % 128)) return 1;
     if (fmt < kFmtInt4 || fmt > kFmtMx4) return 1;
     if (!n_active || !active || !offsets || !tok || !tokw) return 1;
     if (max_slots <= 0 || max_entries <= 0) return 1;

@@ -417,9 +417,6 @@ def moe_forward(x, stacked, E, hidden, inter, lists, *, max_slots=None, max_entr
     sp = _stacked_ptrs(shared) if shared is not None else [None] * 6
     h = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
     code = _format_code(stacked, shared)
-    if code and T > 16:
-        raise ValueError(f"moe_forward: {stacked['format']} experts run the decode kernels "
-                         f"(T <= 16), got T={T}")
     args = [nat.ptr(x2), T, hidden, stacked["group"], E, inter, *_stacked_ptrs(stacked), sint, *sp,
             nat.ptr(shared_coef) if shared_coef is not None else None,
             nat.ptr(lists["n_active"]), nat.ptr(lists["active"]), nat.ptr(lists["offsets"]),

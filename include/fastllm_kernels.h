@@ -535,16 +535,16 @@ int fastllm_moe_int4_routed(const float *logits, int top_k, int scoring,
                             void *workspace, size_t workspace_bytes, float *y,
                             void *stream);
 
-/* The fused MoE with FP8 or MXFP4 expert weights, T <= 16 tokens (the
- * decode kernels; the workspace is sized as for INT4 by
- * fastllm_moe_int4_workspace_bytes).  format FASTLLM_MOE_FP8 (group_size
+/* The fused MoE with FP8 or MXFP4 expert weights: the decode kernels up to
+ * 16 tokens, the grouped MFMA kernels above (the workspace is sized as for
+ * INT4 by fastllm_moe_int4_workspace_bytes; fastllm_moe_lowp_routed takes
+ * T <= 16 like fastllm_moe_int4_routed).  format FASTLLM_MOE_FP8 (group_size
  * must be 128): gq/uq/dq are the FP8 tiles and gsz/usz/dsz the f32 block
  * scales (passed as uint32 pointers); FASTLLM_MOE_MXFP4 (group_size 32):
  * the MXFP4 tiles and scale words.  The codes become fp16 exactly and run on
  * the f16 matrix cores against the fp16 activations; block scales multiply
  * the fp32 results.  Other arguments, outputs and return codes as
- * fastllm_moe_int4_fused / fastllm_moe_int4_routed; other formats or T > 16
- * return 1.
+ * fastllm_moe_int4_fused / fastllm_moe_int4_routed; other formats return 1.
  * No single reference counterpart: the tensor-core fused MoE with FP8 /
  * MXFP4 experts of docs/next-optimizations.md:160-184 (the reference's
  * graph path runs INT4 experts only, fastllm_py/graph_decode.py:669-700). */

@@ -173,27 +173,49 @@ def test_lowp_moe_config4_shape(torch_gpu, fmt):
     assert Q.max_abs_rel(y.cpu().numpy(), ref) < TOL
 
 
+@pytest.mark.parametrize("fmt", ["fp8", "mxfp4"])
+@pytest.mark.parametrize("T,E,K,hidden,inter,sinter,norm", [
+    (40, 16, 4, 1024, 512, 1024, False),
+    (200, 32, 8, 512, 768, 0, True),
+    (130, 8, 2, 256, 256, 512, False),
+])
+def test_lowp_moe_prefill_parity(torch_gpu, fmt, T, E, K, hidden, inter, sinter, norm):
+    """More than 16 tokens: the grouped MFMA kernels with FP8 / MXFP4 experts
+    (router lists from route_topk_device) vs the fp32 oracle."""
+    from fastllm_py.expert_router import route_topk_device
+    from fastllm_py.kernels import moe_int4
+
+    torch = torch_gpu
+    rng = np.random.default_rng(1500 + T + E + (0 if fmt == "fp8" else 1))
+    st, deq, sh, sdeq = _layer(rng, fmt, E, hidden, inter, sinter)
+    x = torch.from_numpy((rng.standard_normal((T, hidden)) * 0.5).astype(np.float32)).cuda()
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float16).astype(np.float32)).cuda()
+    sl = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).cuda() if sinter else None
+    r = route_topk_device(logits, K, norm_topk_prob=norm, shared_logit=sl)
+    ids, w = r["topk_ids"].cpu().numpy(), r["topk_w"].cpu().numpy()
+    coef = 1.0 / (1.0 + np.exp(-sl.cpu().numpy())) if sinter else None
+    ref = OM.moe_ref(x.cpu().numpy(), deq, ids, w, sdeq, coef)
+    y = moe_int4.moe_forward(x, st, E, hidden, inter, r, max_slots=E, max_entries=T * K, shared=sh,
+                             shared_inter=sinter, shared_coef=r.get("shared_coef"))
+    torch.cuda.synchronize()
+    assert Q.max_abs_rel(y.cpu().numpy(), ref) < TOL, fmt
+
+
 def test_lowp_rejects(torch_gpu):
-    """More than 16 tokens, a wrong group size or mixed formats are refused
-    before any launch."""
+    """A wrong group size or mixed formats are refused before any launch."""
     from fastllm_py import _native
     from fastllm_py.kernels import moe_int4
 
     torch = torch_gpu
     rng = np.random.default_rng(15)
     st, _, _, _ = _layer(rng, "fp8", 4, 256, 256, 0)
-    x = torch.zeros((17, 256), device="cuda")
-    i32 = lambda n: torch.zeros(n, dtype=torch.int32, device="cuda")  # noqa: E731
-    L = {"n_active": i32(1), "active": i32(4), "offsets": i32(5), "tok": i32(68),
-         "tokw": torch.zeros(68, device="cuda")}
-    with pytest.raises(ValueError):
-        moe_int4.moe_forward(x, st, 4, 256, 256, L)
+    x = torch.zeros((1, 256), device="cuda")
     int4_sh = moe_int4.build_stacked_experts(
         [{"gate": np.zeros((256, 256), np.float16), "up": np.zeros((256, 256), np.float16),
           "down": np.zeros((256, 256), np.float16)}], 128)
     L1 = moe_int4.build_lists(1, 4, rw=torch.full((1, 4), 0.25, device="cuda"))
     with pytest.raises(ValueError):
-        moe_int4.moe_forward(x[:1], st, 4, 256, 256, L1, shared=int4_sh, shared_inter=256)
+        moe_int4.moe_forward(x, st, 4, 256, 256, L1, shared=int4_sh, shared_inter=256)
     lib = _native.lib()
     p = 1 << 20  # never dereferenced: the checks fail first
     ws = moe_int4.moe_workspace_bytes(1, 256, 256, 0, 4)
