@@ -562,11 +562,12 @@ def run_gemm_prefill(torch, lib, stream, M=512, N=8192, K=2048):
             **cycle(n * marlin_bytes(0, N, K))}
 
 
-def run_moe_prefill(torch, lib, stream, T=512):
+def run_moe_prefill(torch, lib, stream, T=512, fmt="int4"):
     """Config 5's grouped MoE layer (Qwen3-30B-A3B): 128 experts, hidden 2048,
     inter 768, top-8 softmax with renormalisation from fp16 logits ~ N(0,1),
-    M=512 tokens.  Timed unit = one layer: route + gate/up + down launches;
-    HBM-bound on the routed experts' packed weights."""
+    M=512 tokens, `fmt` expert weights.  Timed unit = one layer: route +
+    gate/up + down launches; HBM-bound on the routed experts' packed
+    weights."""
     from fastllm_py.expert_router import route_topk_device
     from fastllm_py.kernels import moe_int4
 
@@ -575,15 +576,19 @@ def run_moe_prefill(torch, lib, stream, T=512):
     gen.manual_seed(5100)
 
     def layer():
-        st = {"group": 128}
+        st = {"group": 128} if fmt == "int4" else {"group": moe_int4.LOWP_FORMATS[fmt][1],
+                                                   "format": fmt}
         for proj, (o, i) in (("gate", (inter, hidden)), ("up", (inter, hidden)),
                              ("down", (hidden, inter))):
             w = (torch.randn((E, o, i), generator=gen, device="cuda") * 0.02).half()
-            qw, sc, ze, _ = moe_int4._quantize_int4_rowmajor_batched(w, 128)
+            if fmt == "int4":
+                qw, sc, ze, _ = moe_int4._quantize_int4_rowmajor_batched(w, 128)
+                st.update(moe_int4.stack_tiles(proj, qw, sc, ze, 128))
+            else:
+                st.update(moe_int4.stack_lowp(fmt, proj, w.float()))
             del w
-            st.update(moe_int4.stack_tiles(proj, qw, sc, ze, 128))
         return st
-    expert_bytes = 3 * inter * hidden // 2 + 3 * inter * hidden // 128 * 4
+    expert_bytes = moe_weight_bytes(fmt, inter, hidden) * 2 + moe_weight_bytes(fmt, hidden, inter)
     nl = copies_for(E * expert_bytes)
     layers = [layer() for _ in range(nl)]
     logits = torch.randn((T, E), generator=gen, device="cuda").half().float()
@@ -831,7 +836,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--only", default="int4,swiglu,layer,group,rm,fp8,fp8p,moe,moelp,gemm")
+    ap.add_argument("--only", default="int4,swiglu,layer,group,rm,fp8,fp8p,moe,moelp,gemm,moelpp")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy a 64 MiB buffer 5 times (a known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -902,6 +907,11 @@ def main():
         log(f"GEMM: {breakdown['int4_gemm_prefill']}")
         breakdown["moe_prefill_qwen3_30b_a3b_int4"] = run_moe_prefill(torch, lib, stream)
         log(f"MoE prefill: {breakdown['moe_prefill_qwen3_30b_a3b_int4']}")
+    if "moelpp" in only:
+        for fmt in ("fp8", "mxfp4"):
+            key = f"moe_prefill_qwen3_30b_a3b_{fmt}"
+            breakdown[key] = run_moe_prefill(torch, lib, stream, fmt=fmt)
+            log(f"MoE prefill {fmt}: {breakdown[key]}")
     if "fp8" in only:
         breakdown["fp8_b128x128_bf16"] = run_fp8(torch, lib, stream)
         log(f"FP8: {breakdown['fp8_b128x128_bf16']}")

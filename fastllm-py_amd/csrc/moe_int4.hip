@@ -601,11 +601,10 @@ FL_DEV void net_argsort(float (&kf)[4], int (&ix)[4], int maxN, int lane) {
 }
 
 // Keys -v (numpy's -select) of n values (lane + 64 c), padded to the
-// network's size, sorted; returns maxN.  Out of line: it runs only for tied
-// rows, and inlined its ~10 KB of code would sit in the instruction stream of
-// every routing wave (a one-pass wave pays an instruction-cache miss for
-// each large block it jumps over).
-__device__ __attribute__((noinline)) int net_load_sort(const float (&v)[4], int n, int lane, float (&kf)[4], int (&ix)[4]) {
+// network's size, sorted; returns maxN.  Inlined: called out of line it cost
+// config 5's router (T = 512, 18 tied tokens) 7.6 us, and the smaller routing
+// code it gave the one-token path measured no faster.
+FL_DEV int net_load_sort(const float (&v)[4], int n, int lane, float (&kf)[4], int (&ix)[4]) {
     int maxN = 8;
     while (maxN < n) maxN <<= 1;
 #pragma unroll

@@ -67,7 +67,7 @@ __host__ __device__ inline float np_sum_f32(const float* a, int n) { return np_s
 // same sums: float addition is commutative), add the leaf's tail, and lane 0
 // joins the leaves as the recursion does.  `a` may be LDS.  All lanes return
 // the sum.
-__device__ __attribute__((noinline)) float np_sum_wave(const float* a, int n, int lane) {
+__device__ inline float np_sum_wave(const float* a, int n, int lane) {
     int s1 = 0, l0 = n, l1 = 0, s2 = 0, l2 = 0, nl = 1;
     if (n > 128) {
         const int h = n / 2, n2 = h - h % 8, m = n - n2;
