@@ -411,20 +411,27 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q4(
     }
 }
 
-// Decode GEMV for 4 < M <= 8 on 8-row tiles ("halved" MFMA), the q4 scheme
+// Decode GEMV for M <= 8 (above four rows, or up to four when K >= 8192) on
+// 8-row tiles ("halved" MFMA), the q4 scheme
 // with two k-parts: B column 8 h + r = weight row r in half h of K, A row
 // 8 h' + m = activation row m in half h'; the diagonal blocks h' == h are the
 // half partial sums.  A workgroup needs 8 weight rows (N = 2048: 256
 // workgroups instead of 128).  M x K activations are too large for LDS here
-// (8 x 10944 bf16 = 175 KB), so each lane loads its own A fragments of all
-// its slots into registers, ahead of its weight loads.
+// (8 x 10944 bf16 = 175 KB), so above four rows each lane loads its own A
+// fragments of all its slots into registers, ahead of its weight loads.  Up
+// to four rows (ALDS) each wave first copies the activation bytes its slots
+// need (M rows x 2 halves x 256 B per slot) into its LDS slot, 64 chunks of
+// 16 B per buffer_load ... lds, and its lanes read their fragments there:
+// sixteen lanes share each fragment, so the register loads moved 8 x the
+// unique bytes through the address path and held every wave's weight loads
+// back (2048 x 10944, M = 1: the last wave's loads went out 5.4 us in).
 //   * Half h holds blocks [h HB, (h + 1) HB) (HB = ceil(nfull / 2)); waves
 //     take slots round-robin, NB at most; blocks past nfull repeat the last
 //     one with a zero scale.
 //   * Accumulator element e of lane l is A row 4 (l / 16) + e: half
 //     (l / 16) / 2, activation row 4 ((l / 16) % 2) + e; it is a diagonal
 //     element when that half equals the lane's column half.
-template <int NB, bool INLINE, bool BF16>
+template <int NB, bool INLINE, bool BF16, bool ALDS>
 __global__ __launch_bounds__(1024) void fp8_gemv_q2(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ Sc,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int rs,
@@ -445,14 +452,32 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
     // A fragments first: lane (col, kq) = activation row col % 8 (clamped),
     // half col / 8, k 32 kq + {0, 8, 16, 24} of the slot's block
     const int arow = (col & 7) < M ? (col & 7) : M - 1;
-    const uint16_t* ap = A + (size_t)arow * K + 32 * kq;
     u32x4 ar[NB][4];
+    unsigned char* aslot = smem + (size_t)wave * NB * 2048;
+    if (ALDS) {
+        // chunk q = ((i M + m) 2 + half) 16 + p (16 B each) lands at 16 q
+        const int total = NB * M * 32;
+        const int ncp = (total + 63) >> 6;
+        const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)M * K * 2);
+        for (int c = 0; c < ncp; ++c) {
+            int q = c * 64 + lane;
+            q = q < total ? q : total - 1;
+            const int i = q / (M * 32), rem = q - i * M * 32;
+            const int m = rem >> 5, hh = (rem >> 4) & 1, pc = q & 15;
+            int kb = hh * HB + slot_b(i);
+            kb = kb < nfull ? kb : nfull - 1;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(aslot + c * 1024), 16,
+                                                     2u * ((uint32_t)m * K + kb * 128 + pc * 8), 0, 0, 0);
+        }
+    } else {
+        const uint16_t* ap = A + (size_t)arow * K + 32 * kq;
 #pragma unroll
-    for (int i = 0; i < NB; ++i) {
-        int kb = h * HB + slot_b(i);
-        kb = kb < nfull ? kb : nfull - 1;
+        for (int i = 0; i < NB; ++i) {
+            int kb = h * HB + slot_b(i);
+            kb = kb < nfull ? kb : nfull - 1;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ar[i][j] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 8 * j);
+            for (int j = 0; j < 4; ++j) ar[i][j] = *reinterpret_cast<const u32x4*>(ap + kb * 128 + 8 * j);
+        }
     }
     const int wrow = row0 + r < N ? row0 + r : N - 1;
     const uint8_t* rbase = W + (size_t)wrow * rs;
@@ -477,17 +502,29 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
         sv[i] = (i < nb && kbr < nfull) ? sc : 0.0f;
     }
     __builtin_amdgcn_sched_barrier(0);
+    if (ALDS) {
+        // this wave's copies went out first: done once at most its code loads
+        // (two per slot; a vector scale load only makes the wait stricter)
+        // are outstanding
+        constexpr int WL = NB * 2;
+        wait_vmcnt<(WL < 63 ? WL : 63)>();
+    }
 
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         u32x4 lo, hi;
         trade_pieces(ld0[i], ld1[i], up, lo, hi);
+        u32x4 a[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            a[j] = ALDS ? *reinterpret_cast<const u32x4*>(aslot + (size_t)(((i * M + arow) * 2 + h) * 16 + 4 * kq + j) * 16)
+                        : ar[i][j];
         f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
-        part = mfma16<BF16>(ar[i][0], fp8x8_to_16<BF16>(lo[0], lo[1]), part);
-        part = mfma16<BF16>(ar[i][1], fp8x8_to_16<BF16>(lo[2], lo[3]), part);
-        part = mfma16<BF16>(ar[i][2], fp8x8_to_16<BF16>(hi[0], hi[1]), part);
-        part = mfma16<BF16>(ar[i][3], fp8x8_to_16<BF16>(hi[2], hi[3]), part);
+        part = mfma16<BF16>(a[0], fp8x8_to_16<BF16>(lo[0], lo[1]), part);
+        part = mfma16<BF16>(a[1], fp8x8_to_16<BF16>(lo[2], lo[3]), part);
+        part = mfma16<BF16>(a[2], fp8x8_to_16<BF16>(hi[0], hi[1]), part);
+        part = mfma16<BF16>(a[3], fp8x8_to_16<BF16>(hi[2], hi[3]), part);
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(sv[i], part[e], acc[e]);
         __builtin_amdgcn_sched_barrier(0);
@@ -513,7 +550,7 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
     }
 
     // diagonal elements: half (kq / 2) == h, activation row 4 (kq % 2) + e
-    float* red = reinterpret_cast<float*>(smem);
+    float* red = reinterpret_cast<float*>(smem + (ALDS ? (size_t)nwaves * NB * 2048 : 0));
     if ((kq >> 1) == h) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) red[(wave * 16 + col) * 8 + 4 * (kq & 1) + e] = acc[e];
@@ -537,9 +574,13 @@ template <int NB, bool INLINE, bool BF16>
 hipError_t launch_fp8_q2(const uint16_t* A, const uint8_t* W, const float* Sc, const uint16_t* bias,
                          uint16_t* C, int M, int N, int K, int rs, int nks, int waves,
                          hipStream_t st) {
-    const size_t lds = (size_t)waves * 16 * 8 * sizeof(float);
-    hipLaunchKernelGGL((fp8_gemv_q2<NB, INLINE, BF16>), dim3((N + 7) / 8), dim3(64 * waves), lds, st,
-                       A, W, Sc, bias, C, M, N, K, rs, nks);
+    const size_t red = (size_t)waves * 16 * 8 * sizeof(float);
+    if (M <= 4)
+        hipLaunchKernelGGL((fp8_gemv_q2<NB, INLINE, BF16, true>), dim3((N + 7) / 8), dim3(64 * waves),
+                           (size_t)waves * NB * 2048 + red, st, A, W, Sc, bias, C, M, N, K, rs, nks);
+    else
+        hipLaunchKernelGGL((fp8_gemv_q2<NB, INLINE, BF16, false>), dim3((N + 7) / 8), dim3(64 * waves), red, st,
+                           A, W, Sc, bias, C, M, N, K, rs, nks);
     return hipGetLastError();
 }
 
