@@ -20,8 +20,8 @@ Every figure is timed with HIP events around HIP-graph replays on the launch
 stream.  Each graph cycles through enough weight copies (and, for the MoE,
 router logits) that the bytes touched between two reads of the same weight
 exceed 2.2x the 256 MB Infinity Cache, so weights stream from HBM; each leg
-records its `cycle_bytes`.  `--warmup W` untimed replays precede each timed
-region.
+records its `cycle_bytes`.  `--warmup W` untimed replays, and at least 30 ms
+of replays, precede each timed region.
 
 CPU baselines (BASELINE.md's plan): the numpy oracle on the host, 3 warm-up
 runs then the median of 20; figure (i) dequantize-then-fp32-matmul per call
@@ -74,10 +74,16 @@ def log(msg):
 WARMUP = [5]  # untimed replays before each timed region (--warmup)
 
 
+WARM_MS = 30.0  # minimum busy time before each timed region
+
+
 def graph_time(torch, stream, launches, reps, warmup=None):
     """Capture the enqueue callbacks in one HIP graph on `stream`, replay it
-    `warmup` (default --warmup) times, then time `reps` replays with HIP
-    events on that stream.  Returns ms per replay."""
+    `warmup` (default --warmup) times and on until the GPU has been busy for
+    WARM_MS, then time `reps` replays with HIP events on that stream.
+    Returns ms per replay.  (After the host-side setup of a leg -- quantizing
+    and copying its weights -- the first few ms of replays run up to 30 %
+    slower: 24576x4096 row-major 14.7-16.1 us, then 11.9-12.7 us.)"""
     if warmup is None:
         warmup = WARMUP[0]
     g = torch.cuda.CUDAGraph()
@@ -85,8 +91,13 @@ def graph_time(torch, stream, launches, reps, warmup=None):
         h = torch.cuda.current_stream().cuda_stream
         for fn in launches:
             fn(h)
-    for _ in range(max(1, warmup)):
-        g.replay()
+    t_start = time.perf_counter()
+    done = 0
+    while done < max(1, warmup) or (time.perf_counter() - t_start) * 1e3 < WARM_MS:
+        for _ in range(8):
+            g.replay()
+        done += 8
+        torch.cuda.synchronize()
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)

@@ -247,6 +247,274 @@ __global__ __launch_bounds__(1024) void rm_gemv_nb(const void* __restrict__ Xv,
     });
 }
 
+// ------------------------------- row-major INT4 GEMV, whole-line loads (M <= 4)
+// The decode shape of the row-major GEMV (the graph decoder's dgemv,
+// graph_decode.py:170-216, M = 1).  A 128-byte line of a weight row holds
+// two 128-k blocks (2p, 2p + 1), so the waves take k in pairs of blocks and
+// every load instruction reads eight whole lines: load 0 of lane (q, c)
+// reads 16-byte piece q + 4 [c >= 8] of tile row c mod 8, load 1 piece
+// q + 4 [c < 8] of row 8 + c mod 8, and one DPP row rotation by 8 trades
+// the misplaced pieces between lanes c and c ^ 8 (trade_rm).  Lane (q, c)
+// then holds bytes [16q, 16q + 16) of row c's block 2p and of its block
+// 2p + 1, i.e. k = 32q + 8j + r for word j, nibble position r.
+//   * Dequantization in the nibbles' own order: (w & 0x000F000F) etc. give
+//     the fp16 pairs (k0, k4), (k1, k5), (k2, k6), (k3, k7) of a word
+//     (dequant_word_fast), so the MFMA reads the activations in that order:
+//     fp16 rows are permuted in place once they land in LDS, fp32 rows are
+//     paired that way when rounded to fp16.
+//   * Wave w takes the NP consecutive pairs [w NP, w NP + NP), so the scales
+//     and zeros of its blocks are one 16-byte piece per row (two where the
+//     range crosses a piece): one copy global -> LDS per piece carries both
+//     arrays for all its rows (lane = (array, tile, row)).  Per-block dword
+//     loads of them put 16 requests on each scale line (one per pair) and
+//     measured 1-4 us slower per launch.
+//     fp16 scale/zero (group 128), or quantize_int4_group's fp32 scale and
+//     minimum (group 128: s*sum(x q) + min*sum(x), the second sum against a
+//     B operand of ones).
+//   * Activations: each wave copies the rows of its own blocks global -> LDS
+//     (buffer_load ... lds).  XC 0: fp16 rows, one copy = 4 rows x 128 k;
+//     XC 1: fp32 rows, one copy = 2 rows x 128 k (M <= 2); XC 2: fp32, two
+//     copies (M <= 4).  fp32 rows are rounded to fp16 at the MFMA, as
+//     rm_gemv_nb stages them.
+//   * All copies go out before the weight loads and a wave waits only for
+//     its own (vmcnt = its weight loads); no workgroup barrier until the
+//     reduction, whose partials go into each wave's own activation slots.
+//   * Strips of T tiles, XCD-grouped.
+FL_DEV void trade_rm(const u32x4& i0, const u32x4& i1, bool up, u32x4& own, u32x4& mate) {
+    const u32x4 send = up ? i0 : i1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        own[e] = up ? i1[e] : i0[e];
+        mate[e] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)send[e], 0x128 /* row_ror:8 */, 0xF, 0xF,
+                                                        false);
+    }
+}
+
+// 8 consecutive k (h0..h7) in the order dequant_word_fast produces them
+FL_DEV f16x8 nib_order(f16x8 v) { return f16x8{v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]}; }
+
+template <int XC>
+constexpr int rm_slot_bytes() {
+    return XC == 2 ? 2048 : 1024;
+}
+// 16-byte scale/zero pieces a range of NP consecutive pairs can span (PP
+// pairs per piece: 4 for fp16 values, 2 for fp32)
+constexpr int rm_sz_pieces(int np, int pp) {
+    int worst = 1;
+    for (int w = 0; w < pp; ++w) {  // wave w starts at pair w np: offset (w np) mod pp
+        const int n = ((w * np) % pp + np + pp - 1) / pp;
+        worst = n > worst ? n : worst;
+    }
+    return worst;
+}
+// LDS bytes of one wave: activation slots (NP x 2 blocks; the reduction
+// partials reuse them) and its scale/zero pieces
+__host__ __device__ inline size_t rm_line_wave_lds(int np, int slot, int T, int pieces) {
+    const size_t a = (size_t)np * 2 * slot;
+    const size_t r = (size_t)T * 1024;
+    return (a > r ? a : r) + (size_t)pieces * 1024;
+}
+
+template <int T, int NP, int XC, bool AFMT>
+__global__ __launch_bounds__(1024) void rm_gemv_line(const void* __restrict__ Xv,
+                                                     const uint8_t* __restrict__ Wq,
+                                                     const void* __restrict__ Sv,
+                                                     const void* __restrict__ Zv, void* __restrict__ Yv,
+                                                     int y_fp32, int M, int N, int K) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int BSL = rm_slot_bytes<XC>();  // LDS bytes of one block's activation rows
+    constexpr int ES = AFMT ? 4 : 2;          // bytes per scale / zero value
+    constexpr int PP = 16 / (2 * ES);         // pairs per 16-byte scale piece
+    constexpr int NPC = rm_sz_pieces(NP, PP);
+    const int nwaves = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int strip = xcd_block();
+    const int npairs = K >> 8;
+    const int G = K >> 7;
+    const int col = lane & 15, kq = lane >> 4;
+    const int p_first = wave * NP;
+    const int np = p_first < npairs ? (npairs - p_first < NP ? npairs - p_first : NP) : 0;
+    const size_t wl = rm_line_wave_lds(NP, BSL, T, NPC);
+    unsigned char* aslot = smem + (size_t)wave * wl;
+    unsigned char* szl = aslot + (wl - (size_t)NPC * 1024);
+    auto pair_of = [&](int i) {
+        const int p = p_first + (i < np ? i : (np > 0 ? np - 1 : 0));
+        return p < npairs ? p : npairs - 1;
+    };
+
+    // scale / zero pieces of this wave's pairs: copy c, lane (array, tile,
+    // row) -> 16 B at szl + c KB + 16 lane
+    const int piece0 = pair_of(0) / PP;
+    {
+        const int arr = lane >> 5, t = (lane >> 4) & 1, c = lane & 15;
+        const int row = (strip * T + (t < T ? t : T - 1)) * 16 + c;
+        const uint32_t rowoff = (uint32_t)(row < N ? row : N - 1) * G * ES;
+        const uint32_t nbytes = (uint32_t)N * G * ES;
+        const __amdgpu_buffer_rsrc_t r = buf_rsrc(arr ? Zv : Sv, nbytes);
+#pragma unroll
+        for (int c2 = 0; c2 < NPC; ++c2)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lptr_t)(szl + c2 * 1024), 16, rowoff + 16 * (piece0 + c2),
+                                                     0, 0, 0);
+    }
+    // activation copies of this wave's blocks
+    if (XC == 0) {
+        const __amdgpu_buffer_rsrc_t rA = buf_rsrc(Xv, (uint32_t)M * K * 2);
+        const int own_m = (lane >> 4) < M ? (lane >> 4) : M - 1;
+        const uint32_t ao = 2u * ((uint32_t)own_m * K + 8 * (lane & 15));
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int p = pair_of(i);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(aslot + (2 * i + h) * BSL), 16, ao,
+                                                         (2 * p + h) * 256, 0, 0);
+        }
+    } else {
+        const __amdgpu_buffer_rsrc_t rA = buf_rsrc(Xv, (uint32_t)M * K * 4);
+#pragma unroll
+        for (int c = 0; c < XC; ++c) {
+            const int m = 2 * c + (lane >> 5);
+            const int own_m = m < M ? m : M - 1;
+            const uint32_t ao = 4u * ((uint32_t)own_m * K + 4 * (lane & 31));
+#pragma unroll
+            for (int i = 0; i < NP; ++i) {
+                const int p = pair_of(i);
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        rA, (lptr_t)(aslot + (2 * i + h) * BSL + c * 1024), 16, ao, (2 * p + h) * 512, 0, 0);
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the copies go out before every load below
+
+    const bool up = col >= 8;
+    const int p0 = 16 * (kq + (up ? 4 : 0)), p1 = 16 * (kq + (up ? 0 : 4));
+    const size_t rs = (size_t)(K >> 1);
+    const uint8_t* rb0[T];
+    const uint8_t* rb1[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int n0 = (strip * T + t) * 16 + (col & 7), n1 = n0 + 8;
+        rb0[t] = Wq + (size_t)(n0 < N ? n0 : N - 1) * rs + p0;
+        rb1[t] = Wq + (size_t)(n1 < N ? n1 : N - 1) * rs + p1;
+    }
+    u32x4 ld0[NP][T], ld1[NP][T];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const int p = pair_of(i);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            ld0[i][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rb0[t] + (size_t)p * 128));
+            ld1[i][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rb1[t] + (size_t)p * 128));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // this wave's copies are done once at most its weight loads (two per
+    // pair and tile) are outstanding
+    constexpr int WL = NP * T * 2;
+    wait_vmcnt<(WL < 63 ? WL : 63)>();
+    if (XC == 0) {
+        // fp16 rows into the nibble order, in place: lane l owns 16 B of
+        // every block slot
+#pragma unroll
+        for (int s = 0; s < 2 * NP; ++s) {
+            f16x8* pv = reinterpret_cast<f16x8*>(aslot + s * BSL + 16 * lane);
+            *pv = nib_order(*pv);
+        }
+    }
+
+    const int arow_m = col < M ? col : M - 1;
+    const uint32_t mlo = 0x64006400u, mhi = 0x54005400u;
+    uint32_t zlo0, zhi0;
+    zero_bits(0, zlo0, zhi0);
+    f32x4 acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const float live = i < np ? 1.0f : 0.0f;
+        const int p = pair_of(i);
+        u32x4 wb[T][2];  // blocks 2p and 2p + 1 of each tile
+#pragma unroll
+        for (int t = 0; t < T; ++t) trade_rm(ld0[i][t], ld1[i][t], up, wb[t][0], wb[t][1]);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            // k offsets 32 kq + 8 j of block 2p + h, in the nibble order
+            f16x8 a[4];
+            const unsigned char* ak = aslot + (2 * i + h) * BSL;
+            if (XC == 0) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    a[j] = *reinterpret_cast<const f16x8*>(ak + arow_m * 256 + 64 * kq + 16 * j);
+            } else {
+                const float* af = reinterpret_cast<const float*>(ak + arow_m * 512) + 32 * kq;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f32x4 lo = *reinterpret_cast<const f32x4*>(af + 8 * j);
+                    const f32x4 hi = *reinterpret_cast<const f32x4*>(af + 8 * j + 4);
+                    a[j] = f16x8{(f16)lo[0], (f16)hi[0], (f16)lo[1], (f16)hi[1],
+                                 (f16)lo[2], (f16)hi[2], (f16)lo[3], (f16)hi[3]};
+                }
+            }
+            // value index of block 2p + h in this wave's pieces of its row
+            const int vi = 2 * p + h - 2 * PP * piece0;
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const unsigned char* rowp = szl + (vi / (2 * PP)) * 1024 + (t * 16 + col) * 16;
+                const int vo = (vi % (2 * PP)) * ES;
+                f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+                if constexpr (AFMT) {
+                    const float s = *reinterpret_cast<const float*>(rowp + vo) * live;
+                    const float mn = *reinterpret_cast<const float*>(rowp + 512 + vo) * live;
+                    f32x4 xsum = f32x4{0.f, 0.f, 0.f, 0.f};
+                    const f16x8 ones = f16x8{1, 1, 1, 1, 1, 1, 1, 1};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        part = mfma_f16(a[j], dequant_word_fast(wb[t][h][j], zlo0, zhi0, mlo, mhi), part);
+                        xsum = mfma_f16(a[j], ones, xsum);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        acc[t][e] = __builtin_fmaf(mn, xsum[e], __builtin_fmaf(s, part[e], acc[t][e]));
+                } else {
+                    const uint16_t s16 = *reinterpret_cast<const uint16_t*>(rowp + vo);
+                    const uint16_t z16 = *reinterpret_cast<const uint16_t*>(rowp + 512 + vo);
+                    uint32_t zlo, zhi;
+                    zero_bits((uint32_t)(float)bitcast<f16>(z16), zlo, zhi);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        part = mfma_f16(a[j], dequant_word_fast(wb[t][h][j], zlo, zhi, mlo, mhi), part);
+                    const float s = (float)bitcast<f16>(s16) * live;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[t][e] = __builtin_fmaf(s, part[e], acc[t][e]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // cross-wave reduction: wave w's partials into its own slots (their
+    // activations are consumed), read back by all after one barrier
+#pragma unroll
+    for (int t = 0; t < T; ++t) *reinterpret_cast<f32x4*>(aslot + t * 1024 + lane * 16) = acc[t];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < T * 256; idx += blockDim.x) {
+        const int l = (idx & 255) >> 2, e = idx & 3, t = idx >> 8;
+        const int m = 4 * (l >> 4) + e;
+        const int n = (strip * T + t) * 16 + (l & 15);
+        if (m >= M || n >= N) continue;
+        float v = 0.f;
+        for (int w = 0; w < nwaves; ++w)
+            v += reinterpret_cast<const float*>(smem + (size_t)w * wl + t * 1024)[idx & 255];
+        if (y_fp32)
+            reinterpret_cast<float*>(Yv)[(size_t)m * N + n] = v;
+        else
+            reinterpret_cast<f16*>(Yv)[(size_t)m * N + n] = (f16)v;
+    }
+}
+
 // ------------------------------------------------------------- gate matvec
 // logits[t, e] = sum_h x[t, h] * W[e, h] in fp32 (fp16 W), t < T, for the E
 // router rows and, when sgw is given, one more row (shared-expert gate) into
@@ -2000,12 +2268,62 @@ void rm_dispatch(int nb, const void* X, const uint8_t* W, const void* S, const v
     }
 }
 
+template <int T, int XC, bool AFMT>
+void launch_rm_line_np(int np, dim3 grid, dim3 block, size_t lds, const void* X, const uint8_t* W,
+                       const void* S, const void* Z, void* Y, int y_fp32, int M, int N, int K,
+                       hipStream_t st) {
+    switch (np) {
+        case 1: hipLaunchKernelGGL((rm_gemv_line<T, 1, XC, AFMT>), grid, block, lds, st, X, W, S, Z, Y, y_fp32, M, N, K); break;
+        case 2: hipLaunchKernelGGL((rm_gemv_line<T, 2, XC, AFMT>), grid, block, lds, st, X, W, S, Z, Y, y_fp32, M, N, K); break;
+        default:
+            if constexpr (T == 1) {  // two tiles take at most two pairs per wave
+                if (np == 3)
+                    hipLaunchKernelGGL((rm_gemv_line<1, 3, XC, AFMT>), grid, block, lds, st, X, W, S, Z, Y, y_fp32, M, N, K);
+                else
+                    hipLaunchKernelGGL((rm_gemv_line<1, 4, XC, AFMT>), grid, block, lds, st, X, W, S, Z, Y, y_fp32, M, N, K);
+            }
+            break;
+    }
+}
+
+// The whole-line kernel for M <= 4, K % 256 == 0 and one group per 128-k
+// block; false (nothing launched) for shapes it does not take.  Sixteen
+// waves of one pair up to K = 4096 (4096 x 4096: 4.75 us against 5.15 with
+// eight of two), eight of two on wide N (24576 x 4096: 12.3 against 13.4
+// us), more pairs per wave above; two tiles per workgroup from N = 6144.
+template <bool AFMT>
+bool launch_rm_line(const void* X, int x_fp32, const uint8_t* W, const void* S, const void* Z, void* Y,
+                    int y_fp32, int M, int N, int K, bool g128, hipStream_t st) {
+    if (M > 4 || K % 256 || !g128) return false;
+    if (!fl_aligned(S, AFMT ? 8 : 4) || !fl_aligned(Z, AFMT ? 8 : 4)) return false;
+    const int npairs = K / 256;
+    int waves = (npairs <= 16 && N >= 16384) ? 8 : 16;
+    while (waves > 1 && npairs < waves) waves /= 2;
+    const int np = (npairs + waves - 1) / waves;
+    if (np > 4) return false;
+    const int xc = x_fp32 ? (M <= 2 ? 1 : 2) : 0;
+    // two tiles take 2x the weight registers: at most two pairs per wave
+    const int T = (N >= 6144 && N % 32 == 0 && np <= 2) ? 2 : 1;
+    const int pieces = rm_sz_pieces(np, AFMT ? 2 : 4);
+    const size_t lds = (size_t)waves * rm_line_wave_lds(np, xc == 2 ? 2048 : 1024, T, pieces);
+    if (lds > 160 * 1024) return false;
+    const dim3 grid((N + 16 * T - 1) / (16 * T)), block(64 * waves);
+#define RM_LINE(TT, XCC) \
+    if (T == TT && xc == XCC) launch_rm_line_np<TT, XCC, AFMT>(np, grid, block, lds, X, W, S, Z, Y, y_fp32, M, N, K, st);
+    RM_LINE(1, 0) RM_LINE(1, 1) RM_LINE(1, 2) RM_LINE(2, 0) RM_LINE(2, 1) RM_LINE(2, 2)
+#undef RM_LINE
+    return true;
+}
+
 // Shared body of the two row-major GEMV entries: M in chunks whose fp16 rows
 // fit the LDS staging area, one launch per chunk.
 template <bool AFMT>
 int rm_gemv_entry(const char* what, const void* x, int x_fp32, const uint8_t* qweight,
                   const void* scales, const void* zeros, void* y, int y_fp32, int M, int out_f,
                   int in_f, int group_size, bool g128, void* stream) {
+    if (launch_rm_line<AFMT>(x, x_fp32, qweight, scales, zeros, y, y_fp32, M, out_f, in_f,
+                             g128 && group_size == 128, (hipStream_t)stream))
+        return finish(what);
     const int nfull = in_f / 128;
     int waves = 16;
     while (waves > 1 && nfull < waves) waves /= 2;

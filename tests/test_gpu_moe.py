@@ -165,6 +165,37 @@ def test_dgemv_fp16_batched(torch_gpu, M):
     assert Q.max_abs_rel(y.float().cpu().numpy(), ref) < 2e-3
 
 
+RM_LINE_CASES = [
+    # (out, in, M, x dtype, y dtype): the whole-line kernel (M <= 4, in % 256 == 0)
+    (6144, 4096, 1, "f16", "f16"),   # Qwen3-8B qkv: two tiles per workgroup
+    (4096, 12288, 1, "f16", "f16"),  # down: three pairs per wave
+    (4096, 12288, 2, "f32", "f32"),  # fp32 rows, one copy per block
+    (6144, 4096, 3, "f32", "f16"),   # fp32 rows, two copies per block
+    (1000, 1536, 4, "f16", "f32"),   # ragged N, 6 pairs on 8 waves
+    (17, 768, 2, "f16", "f16"),      # N < one tile
+    (64, 16384, 1, "f32", "f32"),    # four pairs per wave
+    (2048, 1408, 1, "f16", "f16"),   # in % 256 == 128: the tile kernel
+]
+
+
+@pytest.mark.parametrize("out_f,in_f,M,xd,yd", RM_LINE_CASES)
+def test_rowmajor_gemv_shapes(torch_gpu, out_f, in_f, M, xd, yd):
+    from fastllm_py.kernels import moe_int4
+
+    torch = torch_gpu
+    dt = {"f16": torch.float16, "f32": torch.float32}
+    rng = np.random.default_rng(out_f + in_f + M)
+    w = (rng.standard_normal((out_f, in_f)) * 0.02).astype(np.float32)
+    x = rng.standard_normal((M, in_f)).astype(np.float32)
+    payload = moe_int4.quantize_int4_rowmajor(torch.from_numpy(w).cuda(), 128)
+    xg = torch.from_numpy(x).cuda().to(dt[xd])
+    y = moe_int4._rm_gemv(xg, payload, None, dt[yd])
+    assert y.shape == (M, out_f) and y.dtype == dt[yd]
+    p, s, z = Q.quantize_int4_rowmajor(w, 128)
+    ref = xg.float().cpu().numpy() @ Q.dequantize_int4_rowmajor(p, s, z, 128).T
+    assert Q.max_abs_rel(y.float().cpu().numpy(), ref) < 2e-3
+
+
 def test_gate_matvec(torch_gpu):
     # reference tests/test_moe_int4.py:57-64
     from fastllm_py.kernels import moe_int4
