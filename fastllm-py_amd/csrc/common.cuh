@@ -75,6 +75,40 @@ FL_DEV __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
                                              0x00020000);
 }
 
+// Copy rings of the MFMA GEMMs.  With the buffer_load ... lds builtin the
+// compiler cannot tell which LDS bytes a copy in flight will write, so
+// before every LDS read it waits for all of them (s_waitcnt vmcnt(0)): a
+// ring of several stages then drains on every block and holds one block in
+// flight.  These copies are issued from inline asm, which the compiler's
+// wait insertion does not see; the kernels that use them order every LDS
+// read after its copies themselves (s_waitcnt vmcnt(n) + s_barrier), and
+// read nothing else through the vector memory counter inside the ring (a
+// vector load issued behind the copies would return only after them).
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+// Buffer descriptor as four SGPR words (same fields as buf_rsrc).
+FL_DEV i32x4_t raw_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    return i32x4_t{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xFFFFu), (int)bytes, 0x00020000};
+}
+// BYTES (16 or 4) per lane from rsrc + voff + soff into LDS at lds_addr +
+// BYTES lane (lds_addr and soff wave-uniform; offsets past the buffer read 0).
+template <int BYTES = 16>
+FL_DEV void lds_copy(i32x4_t rsrc, uint32_t lds_addr, uint32_t voff, uint32_t soff = 0) {
+    static_assert(BYTES == 16 || BYTES == 4, "copy width");
+    if constexpr (BYTES == 16)
+        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                     :
+                     : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(rsrc),
+                       "s"(__builtin_amdgcn_readfirstlane(soff))
+                     : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+                     :
+                     : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(rsrc),
+                       "s"(__builtin_amdgcn_readfirstlane(soff))
+                     : "memory", "m0");
+}
+
 // Host-side launch error check: returns the HIP error of the last launch.
 static inline hipError_t fl_last_error() { return hipGetLastError(); }
 

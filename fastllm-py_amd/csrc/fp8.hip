@@ -653,12 +653,16 @@ constexpr size_t kFp8LdsCap = 96 * 1024;
 // 0) on the matrix cores: the INT4 MFMA GEMM's structure with e4m3 weights.
 //   * Workgroup tile 64 (m) x 128 (n), eight waves side by side along n, a
 //     64 x 16 wave tile (4 m-tiles x one n-tile of 16 x 16 fp32).
-//   * Every main-loop load goes global -> LDS (buffer_load ... lds) one
-//     128-k block ahead into two 32 KB stages (64 KB: two workgroups per CU),
-//     one vmcnt wait and one barrier per block.  At M = 512 for 2048 x 2048 /
-//     10944 x 2048 / 2048 x 10944 this measured 25.2 / 60.7 / 118.6 us,
-//     against 26.7 / 79.4 / 120.4 with four stages (one workgroup per CU)
-//     and 40 / 82 / 162 with 64 x 256 tiles in three 48 KB stages.
+//   * Every main-loop load goes global -> LDS (lds_copy: buffer_load ...
+//     lds from inline asm) three 128-k blocks ahead into four 32 KB stages
+//     (one workgroup per CU), one vmcnt wait and one barrier per block.
+//     Per-block timestamps at one block ahead showed every block waiting
+//     1.2-1.4 us for its copies (a 16-block tile: 16 x 1.5 us); deeper rings
+//     had measured no faster only because the builtin copies made the
+//     compiler drain them all before each block's LDS reads.  M = 512,
+//     2048 x 2048 / 10944 x 2048 / 2048 x 10944 (two K splits): 27.1 / 59.2
+//     / 79.4 us with one block ahead, 20.6 / 58.9 / 53.6 with two, 19.7 /
+//     56.4 / 53.6 with three.
 //     A stage holds the 64 x 128 activation tile
 //     fragment-major (the 1 KB of (m-tile, 32-k step j) holds lane l's MFMA A
 //     operand at 16 l) and the strip's 128 weight rows x 128 codes: n-tile s,
@@ -678,7 +682,7 @@ constexpr int kF8BM = 64, kF8BN = 128, kF8MinM = 64;
 // per SIMD to hide the LDS and conversion latencies.
 constexpr int kF8NTW = 1, kF8Waves = 8 / kF8NTW;
 constexpr int kF8AF = 16 / kF8Waves;               // A fragments each wave copies per block
-constexpr int kF8Ahead = 1, kF8Stages = kF8Ahead + 1;
+constexpr int kF8Ahead = 3, kF8Stages = kF8Ahead + 1;
 constexpr int kF8StA = 0, kF8StB = 16384, kF8Stage = kF8StB + 16384;
 constexpr size_t kF8Lds = (size_t)kF8Stages * kF8Stage;
 
@@ -717,8 +721,9 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
     const int m0 = mb_i * kF8BM;
     const int nt_base = nb_i * 8;
 
-    const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)M * K * 2);
-    const __amdgpu_buffer_rsrc_t rW = buf_rsrc(W, (uint32_t)N * K);
+    const i32x4_t rA = raw_rsrc(A, (uint32_t)M * K * 2);
+    const i32x4_t rW = raw_rsrc(W, (uint32_t)N * K);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
     // per-lane source offsets; a piece at k >= K (the second half of a
     // trailing 64-wide block) points past the buffer, and the copy reads zeros
     constexpr uint32_t kOut = 0x80000000u;
@@ -742,19 +747,16 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
     }
     auto issue = [&](int kb, int slot) {
         kb = kb_lo + (kb < nkb ? kb : nkb - 1);
-        unsigned char* st = smem + (size_t)slot * kF8Stage;
+        const uint32_t st = lds0 + (uint32_t)slot * kF8Stage;
 #pragma unroll
         for (int i = 0; i < AF; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                rA, (lptr_t)(st + kF8StA + (wave * AF + i) * 1024), 16,
-                kb * 128 + ak[i] < K ? ao[i] + kb * 256 : kOut, 0, 0, 0);
+            lds_copy(rA, st + kF8StA + (wave * AF + i) * 1024, kb * 128 + ak[i] < K ? ao[i] + kb * 256 : kOut);
 #pragma unroll
         for (int i = 0; i < NTW; ++i)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rW, (lptr_t)(st + kF8StB + (wave * NTW + i) * 2048 + h * 1024), 16,
-                    kb * 128 + 64 * h + bk[i] < K ? bo[i][h] + kb * 128 : kOut, 0, 0, 0);
+                lds_copy(rW, st + kF8StB + (wave * NTW + i) * 2048 + h * 1024,
+                           kb * 128 + 64 * h + bk[i] < K ? bo[i][h] + kb * 128 : kOut);
     };
     // block-scale rows of this wave's two n-tiles (a 16-row tile lies in one band)
     const float* srow[NTW];
@@ -906,9 +908,9 @@ hipError_t fp8_dispatch_nb(int nb, const uint16_t* A, const uint8_t* W, const fl
 
 // K splits of the prefill GEMM for M x N x K: grids under 256 tiles split
 // until they reach 256 workgroups, at most 4 splits of >= 16 blocks each
-// (1: no split).  M = 512: 2048 x 10944 118.6 -> 79.3 us with two splits;
-// 2048 x 2048 (16 blocks) gains nothing from two halves (26.7 us against
-// 25.2-27.1 whole), so short K stays whole.
+// (1: no split).  M = 512: 2048 x 10944 118.6 -> 79.3 us with two splits
+// (one block ahead); 2048 x 2048 (16 blocks) is slower in two halves (24.0
+// us against 19.7 whole, three blocks ahead), so short K stays whole.
 int fp8_gemm_splits(int M, int N, int K) {
     const int tiles = ((N + kF8BN - 1) / kF8BN) * ((M + kF8BM - 1) / kF8BM);
     const int nkb = (K + 127) / 128;

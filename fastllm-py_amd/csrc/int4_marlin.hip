@@ -747,7 +747,10 @@ __global__ __launch_bounds__(1024) void int4_gemv_norm(NormArgs nrm, const uint3
 constexpr int kGemmBM = 64, kGemmBN = 256;
 constexpr int kGemmMfmaMinM = 64;   // M above this takes the MFMA GEMM
 // one block ahead in two 35 KB stages: two workgroups per CU (M512 N8192
-// K2048 26.4 us, M1024 44.1 us) against one with four stages (27.2, 49.7)
+// K2048 21.5 us) against 23.8 us for two blocks ahead in three stages (one
+// workgroup per CU; copies from inline asm, so the ring really holds two
+// blocks: see lds_copy) -- the second workgroup's dequantization work hides
+// more than the deeper ring
 constexpr int kGemmAhead = 1;       // blocks in flight ahead of the one computed
 constexpr int kGemmStages = kGemmAhead + 1;
 constexpr int kStA = 0, kStB = 16384, kStS = kStB + 16384, kStZ = kStS + 2048;
@@ -791,10 +794,11 @@ __global__ __launch_bounds__(512) void int4_gemm_mfma(
     const int m0 = mb_i * kGemmBM;
     const int nt_base = nb_i * 16;
 
-    const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)M * K * 2);
-    const __amdgpu_buffer_rsrc_t rW = buf_rsrc(Wq, (uint32_t)N * K / 2);
-    const __amdgpu_buffer_rsrc_t rS = buf_rsrc(S, (uint32_t)G * N * 2);
-    const __amdgpu_buffer_rsrc_t rZ = buf_rsrc(Z, (uint32_t)G * zwords * 4);
+    const i32x4_t rA = raw_rsrc(A, (uint32_t)M * K * 2);
+    const i32x4_t rW = raw_rsrc(Wq, (uint32_t)N * K / 2);
+    const i32x4_t rS = raw_rsrc(S, (uint32_t)G * N * 2);
+    const i32x4_t rZ = raw_rsrc(Z, (uint32_t)G * zwords * 4);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
     // DMA sources of this wave: A rows 4 q .. 4 q + 3, q = 2 wave + i (whole
     // 256-byte rows of the block, so every copy reads 8 full cache lines),
@@ -843,20 +847,15 @@ __global__ __launch_bounds__(512) void int4_gemm_mfma(
 
     auto issue = [&](int kb, int slot) {
         kb = kb < nkb ? kb : nkb - 1;
-        unsigned char* st = smem + (size_t)slot * kStageBytes;
+        const uint32_t st = lds0 + (uint32_t)slot * kStageBytes;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(st + kStA + (wave * 2 + i) * 1024),
-                                                     16, ao[i], kb * 256, 0, 0);
+        for (int i = 0; i < 2; ++i) lds_copy(rA, st + kStA + (wave * 2 + i) * 1024, ao[i], kb * 256);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rW, (lptr_t)(st + kStB + (wave * 2 + i) * 1024),
-                                                     16, bo[i], kb * 1024, 0, 0);
+        for (int i = 0; i < 2; ++i) lds_copy(rW, st + kStB + (wave * 2 + i) * 1024, bo[i], kb * 1024);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const uint32_t grp = (uint32_t)kb * SPB + pgrp[i];
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(pis_s[i] ? rS : rZ, (lptr_t)(st + pdst[i]), 4,
-                                                     pvo[i], grp * prow_bytes[i], 0, 0);
+            lds_copy<4>(pis_s[i] ? rS : rZ, st + pdst[i], pvo[i], grp * prow_bytes[i]);
         }
     };
 

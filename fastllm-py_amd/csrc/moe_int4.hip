@@ -1936,9 +1936,12 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
 //     adds them into y[token] with fp32 atomics, like the decode kernel.
 // Slot indices >= max_slots are the shared expert (rows max_entries + t,
 // tokens t = 0..T-1, coefficient scoef[t] or 1).
-// Every main-loop load goes global -> LDS (buffer_load ... lds), kMgAhead
-// blocks ahead, into a ring of kMgAhead + 1 stages; one vmcnt wait and one
-// barrier per 128-k block hand a stage to all waves.  A stage holds
+// Every main-loop load goes global -> LDS (lds_copy: buffer_load ... lds
+// from inline asm, see common.cuh), kMgAhead blocks ahead, into a ring of
+// kMgAhead + 1 stages; one vmcnt wait and one barrier per 128-k block hand
+// a stage to all waves.  One block ahead in two stages (two workgroups per
+// CU): config 5 148.8-154.2 us per layer, against 190.9 us two blocks ahead
+// in three stages (one workgroup per CU).  A stage holds
 //   * A (16 KB): 64 rows x 128 k fp16, fragment-major for the row-major k
 //     order of the stacked tile layout -- lane (c, q) of MFMA step j reads
 //     row c, k 32 q + 8 j .. + 7 at 16 (64 (4 mt + j) + c + 16 q);
@@ -2017,7 +2020,7 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
     const int spb = 128 / a.gs;  // groups per 128-k block
 
     // this wave's two weight tiles
-    __amdgpu_buffer_rsrc_t rq[2], rz[2];
+    i32x4_t rq[2], rz[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
         size_t tile;
@@ -2032,19 +2035,20 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
             tq = ex->dq;
             tsz = ex->dsz;
         }
-        rq[t] = buf_rsrc(tq + tile * nkb * TB, nkb * TB);
+        rq[t] = raw_rsrc(tq + tile * nkb * TB, nkb * TB);
         if (FMT == kFmtFp8)  // one fp32 scale per (128-row band, block)
-            rz[t] = buf_rsrc(tsz + (tile >> 3) * nkb, nkb * 4);
+            rz[t] = raw_rsrc(tsz + (tile >> 3) * nkb, nkb * 4);
         else if (FMT == kFmtMx4)  // 16 E8M0 words per block
-            rz[t] = buf_rsrc(tsz + tile * nkb * 16, nkb * 64);
+            rz[t] = raw_rsrc(tsz + tile * nkb * 16, nkb * 64);
         else
-            rz[t] = buf_rsrc(tsz + tile * G * 16, G * 64);
+            rz[t] = raw_rsrc(tsz + tile * G * 16, G * 64);
     }
     // A rows: PHASE 0 token rows of xh, PHASE 1 the slot's inter_buf rows
     const uint16_t* abase = PHASE == 0 ? a.xh : a.inter_buf;
     const int astride = PHASE == 0 ? a.hidden : a.inter_pad;  // halves
     const int arows = PHASE == 0 ? a.T : a.max_entries + a.T;
-    const __amdgpu_buffer_rsrc_t rA = buf_rsrc(abase, (uint32_t)arows * astride * 2);
+    const i32x4_t rA = raw_rsrc(abase, (uint32_t)arows * astride * 2);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
     // scale-row copy: INT4 16 words per group, MXFP4 16 words, FP8 the one
     // block scale (every lane copies it)
     const uint32_t zlane = FMT == kFmtFp8 ? 0u
@@ -2068,24 +2072,19 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
         }
         auto issue = [&](int kb, int stg) {
             kb = kb < nkb ? kb : nkb - 1;
-            unsigned char* st = smem + (size_t)stg * STG;
+            const uint32_t st = lds0 + (uint32_t)stg * STG;
 #pragma unroll
             for (int i = 0; i < FPW; ++i)
                 if (kMgAhead > 1 || wave * FPW + i < 4 * mt_live)  // dead m-tiles: no copy
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(st + (wave * FPW + i) * 1024),
-                                                             16, ao[i], kb * 256, 0, 0);
-            unsigned char* wst = st + kMgABytes + wave * WST;
+                    lds_copy(rA, st + (wave * FPW + i) * 1024, ao[i], kb * 256);
+            const uint32_t wst = st + kMgABytes + wave * WST;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int h = 0; h < BPT; ++h)  // FP8: lane l's 32 bytes at 32 l (two copies)
-                    __builtin_amdgcn_raw_ptr_buffer_load_lds(rq[t], (lptr_t)(wst + t * TB + h * 1024), 16,
-                                                             BPT == 2 ? lane * 32 + h * 16 : lane * 16,
-                                                             kb * TB, 0, 0);
+                    lds_copy(rq[t], wst + t * TB + h * 1024, BPT == 2 ? lane * 32 + h * 16 : lane * 16, kb * TB);
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(rz[t], (lptr_t)(wst + 2 * TB + t * 256), 4,
-                                                         zlane, kb * zstep, 0, 0);
+            for (int t = 0; t < 2; ++t) lds_copy<4>(rz[t], wst + 2 * TB + t * 256, zlane, kb * zstep);
         };
 
         f32x4 acc[4][2];
