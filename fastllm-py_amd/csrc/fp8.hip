@@ -330,8 +330,21 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q4(
     // reads quarters 0 and 1, load 1 quarters 2 and 3
     const bool up = h >= 2;
     const int p0 = 16 * (2 * kq + (up ? 1 : 0)), p1 = 16 * (2 * kq + (up ? 0 : 1));
+    // block scales first, then the codes: the live select below waits for
+    // the scales only (loads return in issue order), with the codes still
+    // in flight.  A select right after each scale load, among the code
+    // loads, waited for all of them before the first MFMA; a scale used
+    // only at its block was moved past the copy wait below.
     u32x4 ld0[NB], ld1[NB];
     float sv[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const int kbr = h * QB + slot_b(i);  // the lane's own block
+        const int kb = kbr < nfull ? kbr : nfull - 1;
+        sv[i] = INLINE ? *reinterpret_cast<const float*>(rbase + (size_t)kb * BSTRIDE + 128)
+                       : Sc[(size_t)(wrow >> 7) * nks + kb];
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         const int b = slot_b(i);
@@ -340,17 +353,17 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q4(
             rbase + (size_t)(k0 < nfull ? k0 : nfull - 1) * BSTRIDE + p0));
         ld1[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(
             rbase + (size_t)(k1 < nfull ? k1 : nfull - 1) * BSTRIDE + p1));
-        const int kbr = h * QB + b;  // the lane's own block
-        const int kb = kbr < nfull ? kbr : nfull - 1;
-        float sc = INLINE ? *reinterpret_cast<const float*>(rbase + (size_t)kb * BSTRIDE + 128)
-                          : Sc[(size_t)(wrow >> 7) * nks + kb];
-        sv[i] = (i < nb && kbr < nfull) ? sc : 0.0f;
     }
     __builtin_amdgcn_sched_barrier(0);
-    // the activation copies went out first: done once at most the weight
-    // loads (2 or 3 per slot) are outstanding
+#pragma unroll
+    for (int i = 0; i < NB; ++i) sv[i] = (i < nb && h * QB + slot_b(i) < nfull) ? sv[i] : 0.0f;
+    __builtin_amdgcn_sched_barrier(0);
+    // the activation copies went out first: done once at most the code
+    // loads (two per slot, issued last) are outstanding; the scale loads
+    // between them and the copies are then done too (the select above
+    // needs them anyway), whichever memory path they take
     {
-        constexpr int WL = NB * 3;  // lo, hi, scale
+        constexpr int WL = NB * 2;  // lo, hi
         wait_vmcnt<(WL < 63 ? WL : 63)>();
     }
 
@@ -485,8 +498,17 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
     // half 0, load 1 half 1
     const bool up = h == 1;
     const int p0 = 16 * (2 * kq + h), p1 = 16 * (2 * kq + 1 - h);
+    // block scales first, then the codes (as in the quartered kernel)
     u32x4 ld0[NB], ld1[NB];
     float sv[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        const int kbr = h * HB + slot_b(i);  // the lane's own block
+        const int kb = kbr < nfull ? kbr : nfull - 1;
+        sv[i] = INLINE ? *reinterpret_cast<const float*>(rbase + (size_t)kb * BSTRIDE + 128)
+                       : Sc[(size_t)(wrow >> 7) * nks + kb];
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         const int b = slot_b(i);
@@ -495,17 +517,14 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
             rbase + (size_t)(k0 < nfull ? k0 : nfull - 1) * BSTRIDE + p0));
         ld1[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_a4*>(
             rbase + (size_t)(k1 < nfull ? k1 : nfull - 1) * BSTRIDE + p1));
-        const int kbr = h * HB + b;  // the lane's own block
-        const int kb = kbr < nfull ? kbr : nfull - 1;
-        const float sc = INLINE ? *reinterpret_cast<const float*>(rbase + (size_t)kb * BSTRIDE + 128)
-                                : Sc[(size_t)(wrow >> 7) * nks + kb];
-        sv[i] = (i < nb && kbr < nfull) ? sc : 0.0f;
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) sv[i] = (i < nb && h * HB + slot_b(i) < nfull) ? sv[i] : 0.0f;
     __builtin_amdgcn_sched_barrier(0);
     if (ALDS) {
         // this wave's copies went out first: done once at most its code loads
-        // (two per slot; a vector scale load only makes the wait stricter)
-        // are outstanding
+        // (two per slot, issued after the scale loads) are outstanding
         constexpr int WL = NB * 2;
         wait_vmcnt<(WL < 63 ? WL : 63)>();
     }
