@@ -250,6 +250,13 @@ __global__ __launch_bounds__(1024) void int4_tile_mm(
 //         and by the time the later blocks' weights have arrived so have
 //         their activations (loaded at use, each block would wait a full L2
 //         round trip after all of the wave's weights);
+//       AM 5 (4 < M <= 8): AM 0's per-wave copies, two per block (rows 0-7
+//         in MFMA fragment order, so the 8 distinct rows do not share LDS
+//         banks).  Against AM 3 it moves the unique 2 KB per block instead
+//         of 16 rows' fragments and holds no VGPRs: Qwen3-8B M = 8 qkv 6.38
+//         -> 5.99, o 5.41 -> 5.00, gate_up 14.8 -> 13.8, down 10.5 -> 9.9 us.
+//         The same copies of 16 rows (4 KB per block) were no faster than
+//         AM 3 at M = 16 (gate_up split 16.1 -> 20.6 us);
 //       AM 3 (M > 4, NB <= 4): each lane loads its own MFMA A operands of all
 //         its blocks from global memory into registers (4 x 16 B per block),
 //         first of all, so they arrive ahead of the weights in issue order;
@@ -319,11 +326,14 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
         Z += (size_t)kbo * SPB * zwords;
     }
     constexpr bool ALDS = AM == 1;
+    // per-wave LDS copies of the wave's own blocks: ACP 1 KB copies per block
+    constexpr bool ACOPY = AM == 0 || AM == 4 || AM == 5;
+    constexpr int ACP = AM == 5 ? 2 : 1;
     const int lda = K + 8;
     f16* As = reinterpret_cast<f16*>(smem);
-    // AM 0: wave w's slot of NB blocks x 1 KB (4 rows x 128 k) at w * NB KB
-    const size_t abytes = (AM == 0 || AM == 4) ? (size_t)nwaves * NB * 1024
-                                  : (ALDS ? (((size_t)M * lda * 2 + 15) & ~(size_t)15) : 0);
+    // AM 0/4/5: wave w's slot of NB blocks x ACP KB at w * NB * ACP KB
+    const size_t abytes = ACOPY ? (size_t)nwaves * NB * ACP * 1024
+                                : (ALDS ? (((size_t)M * lda * 2 + 15) & ~(size_t)15) : 0);
     float* red = reinterpret_cast<float*>(smem + abytes);
 
     const int nb = wave < nfull ? (nfull - wave + nwaves - 1) / nwaves : 0;
@@ -364,7 +374,7 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
     if (stager) stg.load(A, M, K, lda, wave, lane);
     // AM 0: lane l of block slot i copies row min(l / 16, M - 1), 16-byte
     // piece l % 16 of the block into this wave's LDS slot
-    unsigned char* aslot = smem + (size_t)wave * NB * 1024;
+    unsigned char* aslot = smem + (size_t)wave * NB * ACP * 1024;
     const int arow_m = col < M ? col : M - 1;
     f16x8 ar[NB][4];
     constexpr int kRing = 3;  // AM 2 register slots
@@ -398,6 +408,26 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
             int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
             kb = kb < nfull ? kb : nfull - 1;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(aslot + i * 1024), 16, ao, kb * 256, 0, 0);
+        }
+    }
+    if (AM == 5) {
+        // fragment-major copies of rows 0-7, read back by each lane at its
+        // own 16 bytes (the row-major slot of AM 0 would put 8 distinct rows
+        // on the same LDS banks): copy p of a block holds MFMA steps 2p and
+        // 2p + 1 -- lane l takes row l & 7, k 32 (2p + l / 32) + 8 ((l / 8) & 3)
+        // -- and MFMA lanes c and c + 8 read the same piece (rows >= 8 are
+        // never stored).  Rows past M repeat row M - 1.
+        const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)M * K * 2);
+        const int r = lane & 7;
+        const uint32_t ao = 2u * ((uint32_t)(r < M ? r : M - 1) * K + 32 * (lane >> 5) + 8 * ((lane >> 3) & 3));
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+            kb = kb < nfull ? kb : nfull - 1;
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(aslot + (i * 2 + p) * 1024), 16,
+                                                         ao + 128u * p, kb * 256, 0, 0);
         }
     }
     if (AM == 4) {
@@ -452,7 +482,7 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    if (AM == 0 || AM == 4) {
+    if (ACOPY) {
         // this wave's activation copies, issued before its weight, scale and
         // zero loads, are done once at most those loads are outstanding (no
         // barrier: only this wave reads its slot)
@@ -555,6 +585,9 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
             if (AM == 0 || AM == 4)
                 a[j] = *reinterpret_cast<const f16x8*>(aslot + (size_t)i * 1024 + arow_m * 256 +
                                                        2 * (32 * j + 8 * kq));
+            else if (AM == 5)
+                a[j] = *reinterpret_cast<const f16x8*>(aslot + (size_t)(i * 2 + (j >> 1)) * 1024 +
+                                                       16 * ((col & 7) + 8 * kq + 32 * (j & 1)));
             else if (AM == 3)
                 a[j] = ar[i][j];
             else if (AM == 2)
@@ -605,7 +638,7 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
     if (G32 && (K & 127) && wave == 0) {
         // trailing 64-k block: two 32-k groups
         f16x8 a[2];
-        const f16* arow_t = (AM == 0 || AM == 3) ? A + (size_t)arow_m * K + 8 * kq : arow;
+        const f16* arow_t = (AM == 0 || AM == 3 || AM == 5) ? A + (size_t)arow_m * K + 8 * kq : arow;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
             a[j] = *reinterpret_cast<const f16x8*>(arow_t + nfull * 128 + 32 * j);
@@ -965,20 +998,23 @@ struct GemvCfg {
     int split = 1;  // k-splits (gridDim.y), each over (K/128)/split blocks
 };
 
-// Workspace of a split-K launch: the strip counters at offset 0 (room for
-// N / 16 of them, whatever the tiles, so calls of any M and split on one
-// workspace find theirs at zero), then the fp32 partials [split][M][N] from a
-// 256-byte boundary.
-constexpr size_t splitk_part_off(int N) { return ((size_t)(N / 16) * 4 + 255) & ~(size_t)255; }
+// Workspace of a split-K launch: the strip counters in a fixed region at
+// offset 0 (one int per strip, kSplitStrips of them whatever N, M, the tiles
+// and the split), then the fp32 partials [split][M][N].  The counter of strip
+// s is then at the same place for every call, and no call's partials reach
+// another's counters, so calls of any shape may share one workspace as long
+// as they do not overlap; every call leaves its counters at zero.
+constexpr int kSplitStrips = 16384;  // N <= 16 * kSplitStrips with a split
+constexpr size_t splitk_part_off(int) { return (size_t)kSplitStrips * 4; }
 constexpr size_t splitk_ws_bytes(int M, int N, int split) {
     return splitk_part_off(N) + (size_t)split * M * N * 4;
 }
 
 constexpr size_t kGemvLdsCap = 96 * 1024;  // activations staged in LDS up to this size
 
-// A split-K launch (split > 1) uses register activations (AM 0 copies for
-// M <= 4, AM 3 / AM 2 above): the whole-row LDS staging of AM 1 would read
-// past the shifted activation base.
+// A split-K launch (split > 1) uses per-wave activations (AM 0 / AM 5 copies
+// up to M = 8, AM 3 / AM 2 above): the whole-row LDS staging of AM 1 would
+// read past the shifted activation base.
 template <int T, int NB, bool G32>
 hipError_t launch_gemv_nb(const f16* A, const uint32_t* Wq, const uint16_t* S, const uint32_t* Z,
                           f16* C, int M, int N, int K, int waves, int split, SplitArgs sp,
@@ -989,6 +1025,9 @@ hipError_t launch_gemv_nb(const f16* A, const uint32_t* Wq, const uint16_t* S, c
     const size_t shared = (((size_t)M * (K + 8) * 2 + 15) & ~(size_t)15);
     if (M <= 4 && own + red <= 160 * 1024)
         hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 0>), grid, block, own + red, stream, A, Wq, S, Z,
+                           C, M, N, K, sp);
+    else if (M <= 8 && 2 * own + red <= 160 * 1024)
+        hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 5>), grid, block, 2 * own + red, stream, A, Wq, S, Z,
                            C, M, N, K, sp);
     else if (NB <= 4)
         hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 3>), grid, block, red, stream, A, Wq, S, Z, C, M,
@@ -1025,8 +1064,14 @@ hipError_t launch_gemv_t4(const f16* A, const uint32_t* Wq, const uint16_t* S, c
                           f16* C, int M, int N, int K, int waves, int split, SplitArgs sp,
                           hipStream_t stream) {
     const size_t red = (size_t)waves * 4 * 256 * sizeof(float);
-    hipLaunchKernelGGL((int4_gemv_nb<4, NB, G32, 3>), dim3(N / 64, split), dim3(64 * waves), red, stream, A,
-                       Wq, S, Z, C, M, N, K, sp);
+    const size_t own = (size_t)waves * NB * 1024;
+    const dim3 grid(N / 64, split), block(64 * waves);
+    if (M <= 8 && 2 * own + red <= 160 * 1024)
+        hipLaunchKernelGGL((int4_gemv_nb<4, NB, G32, 5>), grid, block, 2 * own + red, stream, A, Wq, S, Z,
+                           C, M, N, K, sp);
+    else
+        hipLaunchKernelGGL((int4_gemv_nb<4, NB, G32, 3>), grid, block, red, stream, A, Wq, S, Z, C, M, N,
+                           K, sp);
     return hipGetLastError();
 }
 
@@ -1218,7 +1263,7 @@ bool int4_marlin_abi_gemm(const void* a, const uint32_t* q, const void* scales,
         return int4_gemm_large_m(A, q, static_cast<const f16*>(scales), zeros, Cp, M, N, K, g32,
                                  stream);
     GemvCfg cfg = forced ? *forced : default_gemv_cfg(M, N, K, g32, ws != nullptr);
-    if (cfg.split > 1 && (!ws || !fl_aligned(ws, 256) ||
+    if (cfg.split > 1 && (!ws || !fl_aligned(ws, 256) || N / 16 > kSplitStrips ||
                           ws_bytes < splitk_ws_bytes(M, N, cfg.split))) {
         if (forced) return false;
         cfg = default_gemv_cfg(M, N, K, g32, false);
@@ -1249,34 +1294,38 @@ hipError_t launch_gemv_swiglu(const f16* A, const uint32_t* Wq, const uint16_t* 
     const size_t own = (size_t)waves * NB * 1024;
     const dim3 grid(N / 32), block(64 * waves);
     if (own + red > kMaxLds) return hipErrorInvalidValue;
-    if constexpr (NB > 4) {  // LDS activation copies only (register activations spill)
-        if (M > 4) return hipErrorInvalidValue;
+    // LDS activation copies up to M = 8 (AM 0; AM 5 above four rows while
+    // its 2 KB per block fit), register activations above (NB <= 4: more
+    // blocks per wave spill there)
+    if (M <= 4) {
         hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 0, true>), grid, block, own + red, stream, A, Wq, S,
                            Z, H, M, N, K);
-        return hipGetLastError();
+    } else if constexpr (NB <= 4) {
+        if (M <= 8 && 2 * own + red <= kMaxLds)
+            hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 5, true>), grid, block, 2 * own + red, stream, A,
+                               Wq, S, Z, H, M, N, K);
+        else
+            hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 3, true>), grid, block, red, stream, A, Wq, S, Z,
+                               H, M, N, K);
+    } else {
+        return hipErrorInvalidValue;
     }
-    if (M <= 4)
-        hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 0, true>), grid, block, own + red, stream, A, Wq, S,
-                           Z, H, M, N, K);
-    else
-        hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 3, true>), grid, block, red, stream, A, Wq, S, Z, H,
-                           M, N, K);
     return hipGetLastError();
 }
 
 template <bool G32>
 hipError_t dispatch_swiglu(const f16* A, const uint32_t* Wq, const uint16_t* S, const uint32_t* Z,
                            f16* H, int M, int N, int K, hipStream_t stream) {
-    // the decode config of this shape, with NB <= 4 (register activations);
-    // above M = 4 sixteen waves (NB = 2 at K = 4096): the NB = 4 register-A
-    // instantiation of this kernel needs more than 128 VGPRs and spills
-    // Up to M = 4 (LDS activation copies) six blocks per wave fit the
-    // registers at 16 waves, so K <= 12288 (16 x 6 x 128); above M = 4 four
-    // blocks per wave (K <= 8192).  Larger K is refused (rc 1): the caller
-    // runs the plain GEMV and the standalone SwiGLU.
+    // the decode config of this shape.  Up to M = 8 (LDS activation copies)
+    // eight waves on wide N, and six blocks per wave fit the registers at 16
+    // waves, so K <= 12288 (16 x 6 x 128).  Above M = 8 (register
+    // activations) sixteen waves of at most four blocks (K <= 8192): the NB =
+    // 4 register-A instantiation at eight waves needs more than 128 VGPRs
+    // and spills.  Larger K is refused (rc 1): the caller runs the plain GEMV
+    // and the standalone SwiGLU.
     const int nfull = K / 128 > 0 ? K / 128 : 1;
-    const int cap = (M <= 4 && !G32) ? 6 : 4;
-    int waves = (N >= 16384 && M <= 4) ? 8 : 16;
+    const int cap = (M <= 8 && !G32) ? 6 : 4;
+    int waves = (N >= 16384 && M <= 8) ? 8 : 16;
     while (waves > 1 && nfull < waves) waves /= 2;
     while ((nfull + waves - 1) / waves > 4 && waves < 16) waves *= 2;
     int nb = (nfull + waves - 1) / waves;
@@ -1461,7 +1510,7 @@ size_t fastllm_int4_gemm_ws_bytes(int size_m, int size_n, int size_k, int group_
     if (size_m < 1 || size_m > 16 || size_n <= 0 || size_k <= 0) return 0;
     if (group_size != 32 && group_size != 128) return 0;
     const GemvCfg c = default_gemv_cfg(size_m, size_n, size_k, group_size == 32, true);
-    return c.split > 1 ? splitk_ws_bytes(size_m, size_n, c.split) : 0;
+    return c.split > 1 && size_n / 16 <= kSplitStrips ? splitk_ws_bytes(size_m, size_n, c.split) : 0;
 }
 
 int fastllm_int4_gemm_ws(const void* a, const uint32_t* b_q_weight, const void* b_scales,

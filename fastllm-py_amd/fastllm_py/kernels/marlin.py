@@ -92,12 +92,15 @@ def build_marlin_scales_zeros(scale, zero_int, group_size, xp=np):
 
 
 # Decode GEMVs above four rows split K in two where that pays (long K, or
-# wide N above eight rows); their per-strip counters (size_n // 16 ints from
-# offset 0) and fp32 partials live in the workspace: 128 * size_n bytes plus
-# the counters for up to 16 rows, beside the reference's (size_n // 64) * 16
-# ints.
+# wide N above eight rows); their per-strip counters (a fixed 64 KiB region
+# at offset 0, the same for every shape) and fp32 partials live in the
+# workspace: 128 * size_n bytes for up to 16 rows after the counters, beside
+# the reference's (size_n // 64) * 16 ints.
+_SPLIT_COUNTER_BYTES = 16384 * 4
+
+
 def _workspace_ints(size_n: int) -> int:
-    split_bytes = ((size_n // 16) * 4 + 255) // 256 * 256 + 2 * 16 * size_n * 4
+    split_bytes = _SPLIT_COUNTER_BYTES + 2 * 16 * size_n * 4
     return max(max(1, (size_n // 64) * 16), split_bytes // 4)
 
 

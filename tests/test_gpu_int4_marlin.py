@@ -247,7 +247,7 @@ def test_gemv_split_k(torch_gpu, gs):
     rng = np.random.default_rng(410 + gs)
     W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
     pay, w_hat, _ = _prep(torch, W, gs)
-    ws_bytes = 1024 * N + 4096  # 16 splits x 16 rows x N fp32 + the counters
+    ws_bytes = 1024 * N + 65536  # 16 splits x 16 rows x N fp32 + the counters
     ws = torch.zeros(ws_bytes, dtype=torch.uint8, device="cuda")
     cfgs = [(4, 16, 1, 2), (4, 8, 1, 4), (2, 4, 2, 4), (1, 4, 1, 8), (4, 4, 1, 8), (1, 2, 1, 16)]
 
@@ -274,13 +274,54 @@ def test_gemv_split_k(torch_gpu, gs):
     for (M, cfg), (ad, y) in first.items():
         assert torch.equal(run(ad, M, cfg), y), (M, cfg)
     torch.cuda.synchronize()
-    assert int(ws[:N // 16 * 4].count_nonzero()) == 0  # counters back at zero
+    assert int(ws[:65536].count_nonzero()) == 0  # counters back at zero
     # a forced split with too small a workspace is refused, no launch
     y = torch.empty((8, N), dtype=torch.float16, device="cuda")
     ad = first[(8, None)][0]
     assert lib.fastllm_int4_gemm_ws(ad.data_ptr(), pay["qweight"].data_ptr(), pay["scales"].data_ptr(),
                                     pay["zeros"].data_ptr(), y.data_ptr(), 8, N, K, gs,
                                     ws.data_ptr(), 1024, (ctypes.c_int * 4)(4, 8, 1, 4), None) == 2
+
+
+def test_gemv_split_k_workspace_across_widths(torch_gpu):
+    """One workspace shared by split-K calls of different output widths,
+    interleaved: a narrow call's partials must not land on a wide call's
+    strip counters (they sit in a fixed region whatever N), so every call
+    stays within the oracle's tolerance and bit-identical to its first run."""
+    from fastllm_py import _native
+
+    torch = torch_gpu
+    lib = _native.lib()
+    K, M = 2048, 16
+    rng = np.random.default_rng(433)
+    ws_bytes = 65536 + 2 * M * 4096 * 4
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device="cuda")
+    cases = []
+    for N in (4096, 256, 1024):
+        W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+        pay, w_hat, _ = _prep(torch, W, 128)
+        a = rng.standard_normal((M, K)).astype(np.float16)
+        cases.append((N, pay, torch.from_numpy(a).cuda(), Q.matmul_ref(a.astype(np.float32), w_hat)))
+
+    def run(N, pay, ad):
+        y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+        rc = lib.fastllm_int4_gemm_ws(ad.data_ptr(), pay["qweight"].data_ptr(), pay["scales"].data_ptr(),
+                                      pay["zeros"].data_ptr(), y.data_ptr(), M, N, K, 128, ws.data_ptr(),
+                                      ws_bytes, (ctypes.c_int * 4)(1, 16, 1, 2), None)
+        assert rc == 0, N
+        return y
+
+    first = {}
+    for _ in range(3):
+        for N, pay, ad, ref in cases:
+            y = run(N, pay, ad)
+            torch.cuda.synchronize()
+            assert Q.max_abs_rel(y.float().cpu().numpy(), ref) < TOL, N
+            if N in first:
+                assert torch.equal(y, first[N]), N
+            else:
+                first[N] = y
+    assert int(ws[:65536].count_nonzero()) == 0
 
 
 @pytest.mark.parametrize("name,M", [("down", 5), ("down", 8), ("down", 16), ("gate_up", 16)])
@@ -313,7 +354,8 @@ def test_gemm_split_default_workspace(torch_gpu, name, M):
 
 
 @pytest.mark.parametrize("M,I,K,gs", [(1, 12288, 4096, 128), (4, 1408, 2048, 128), (8, 3072, 1024, 32),
-                                      (16, 512, 4096, 128), (3, 64, 256, 128)])
+                                      (16, 512, 4096, 128), (3, 64, 256, 128), (8, 12288, 4096, 128),
+                                      (6, 1408, 8192, 128), (12, 1024, 4096, 128)])
 def test_gemm_swiglu(torch_gpu, M, I, K, gs):
     """Gate/up GEMV with the SwiGLU epilogue equals the plain GEMV followed by
     swiglu of its fp16 outputs (up to the device exp), and the fp32 oracle."""
