@@ -673,22 +673,20 @@ constexpr size_t kFp8LdsCap = 96 * 1024;
 //   * Workgroup tile 64 (m) x 128 (n), eight waves side by side along n, a
 //     64 x 16 wave tile (4 m-tiles x one n-tile of 16 x 16 fp32).
 //   * Every main-loop load goes global -> LDS (lds_copy: buffer_load ...
-//     lds from inline asm) three 128-k blocks ahead into four 32 KB stages
-//     (one workgroup per CU), one vmcnt wait and one barrier per block.
-//     Per-block timestamps at one block ahead showed every block waiting
-//     1.2-1.4 us for its copies (a 16-block tile: 16 x 1.5 us); deeper rings
-//     had measured no faster only because the builtin copies made the
-//     compiler drain them all before each block's LDS reads.  M = 512,
-//     2048 x 2048 / 10944 x 2048 / 2048 x 10944 (two K splits): 27.1 / 59.2
-//     / 79.4 us with one block ahead, 20.6 / 58.9 / 53.6 with two, 19.7 /
-//     56.4 / 53.6 with three.
-//     A stage holds the 64 x 128 activation tile
-//     fragment-major (the 1 KB of (m-tile, 32-k step j) holds lane l's MFMA A
-//     operand at 16 l) and the strip's 128 weight rows x 128 codes: n-tile s,
-//     half i, lane (c, g) at 2048 s + 1024 i + 16 (c + 16 g) holds codes
-//     [64 i + 16 g, + 16) of row c -- so MFMA lane (c, q) finds its 8 codes of
-//     step j at 16 (c + 16 (2 (j & 1) + q / 2)) + 8 (q & 1) of half j / 2, and
-//     a ds_read_b64 over the wave touches each bank once.
+//     lds from inline asm) D 128-k blocks ahead into D + 1 stages of 32 KB
+//     (D = 1: two workgroups per CU; D = 3: one), one vmcnt wait and one
+//     barrier per block.  With the builtin copies the compiler drained them
+//     all before each block's LDS reads, so no ring held more than one block.
+//   * A stage holds the 64 x 128 activation tile row-major (256 B per row,
+//     the 16-byte k chunks of row r XOR-swizzled by r % 16) and the strip's
+//     128 weight rows x 128 codes row-major (128 B per row, the 16-code
+//     chunks of row r swizzled by r % 8), so every copy moves whole cache
+//     lines: 4 activation rows or 8 code rows.  The kernel is bound by its
+//     copies (a variant without the MFMA loop ran as long as the kernel,
+//     one without the copies half as long), and a copy that reads 16 rows x
+//     64 B (the fragment-major order this replaced) costs a CU as much as
+//     one of 8 full lines: M = 512, 2048 x 2048 / 10944 x 2048 / 2048 x
+//     10944 19.7 / 56.5 / 53.7 -> 13.6 / 35.6 / 43.6 us (ring depths below).
 //   * Codes become fp16/bf16 exactly (v_cvt_scalef32_pk_*_fp8, scale 1); each
 //     block's MFMAs accumulate into a fresh partial that the fp32 block scale
 //     then adds into the accumulator, as the GEMV does.
@@ -701,9 +699,14 @@ constexpr int kF8BM = 64, kF8BN = 128, kF8MinM = 64;
 // per SIMD to hide the LDS and conversion latencies.
 constexpr int kF8NTW = 1, kF8Waves = 8 / kF8NTW;
 constexpr int kF8AF = 16 / kF8Waves;               // A fragments each wave copies per block
-constexpr int kF8Ahead = 3, kF8Stages = kF8Ahead + 1;
+// Blocks in flight ahead of the one computed (the ring holds D + 1 stages
+// of 32 KB).  Grids of more than 256 workgroups take one block ahead, so
+// two workgroups share a CU; smaller grids (at most one per CU) three.  With
+// whole-line copies, M = 512: 10944 x 2048 (688 workgroups) 35.6 us one
+// ahead, 41.3 two, 39.7 three; 2048 x 2048 (128) 15.7 / 14.7 / 13.6;
+// 2048 x 10944 (two K splits, 256) 52.1 / 43.6 / 44.2.
 constexpr int kF8StA = 0, kF8StB = 16384, kF8Stage = kF8StB + 16384;
-constexpr size_t kF8Lds = (size_t)kF8Stages * kF8Stage;
+constexpr size_t fp8_gemm_lds(int ahead) { return (size_t)(ahead + 1) * kF8Stage; }
 
 // Split-K (gridDim.y > 1, grids of fewer than 256 tiles): split y takes 128-k
 // blocks [y kb_per, (y + 1) kb_per); each split stores its fp32 64 x 128
@@ -713,7 +716,7 @@ constexpr size_t kF8Lds = (size_t)kF8Stages * kF8Stage;
 // resets the counter.  Nothing waits on another workgroup.
 constexpr int kF8TileF = kF8BM * kF8BN;  // fp32 partials per tile and split
 
-template <bool BF16>
+template <bool BF16, int D>
 __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict__ A,
                                                      const uint8_t* __restrict__ W,
                                                      const float* __restrict__ Sc,
@@ -721,7 +724,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
                                                      uint16_t* __restrict__ C, int M, int N, int K,
                                                      int nks, int kb_per, float* __restrict__ part,
                                                      int* __restrict__ cnt) {
-    constexpr int D = kF8Ahead, NS = kF8Stages, NTW = kF8NTW, AF = kF8AF;
+    constexpr int NS = D + 1, NTW = kF8NTW, AF = kF8AF;
     constexpr int LPB = AF + 2 * NTW;  // copies per block and wave: A fragments, 2 halves per tile
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
@@ -745,25 +748,32 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
     const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
     // per-lane source offsets; a piece at k >= K (the second half of a
     // trailing 64-wide block) points past the buffer, and the copy reads zeros
+    // Every copy reads whole 128-byte lines: A copy f brings rows 4 f ..
+    // 4 f + 3 (256 B each), lane l row 4 f + l / 16 and its 16-byte k chunk
+    // (l % 16) ^ (row % 16) into LDS position l % 16 of that row; code copy
+    // (tile s, half h) brings rows 8 h .. 8 h + 7 of n-tile s (128 B each),
+    // lane l row 8 h + l / 8 and its 16-code chunk (l % 8) ^ (l / 8).  The
+    // XOR swizzles keep the MFMA reads below off shared banks.
     constexpr uint32_t kOut = 0x80000000u;
     uint32_t ao[AF], bo[NTW][2];
-    int ak[AF], bk[NTW];
+    int ak[AF], bk[NTW][2];
 #pragma unroll
     for (int i = 0; i < AF; ++i) {
-        const int f = wave * AF + i;  // fragment f = 4 m-tile + step
-        int m = m0 + 16 * (f >> 2) + col;
+        const int r = 4 * (wave * AF + i) + (lane >> 4);  // tile row
+        int m = m0 + r;
         m = m < M ? m : M - 1;
-        ak[i] = 32 * (f & 3) + 8 * kq;
+        ak[i] = 8 * ((lane & 15) ^ (r & 15));
         ao[i] = 2u * ((uint32_t)m * K + ak[i]);
     }
 #pragma unroll
-    for (int t = 0; t < NTW; ++t) {
-        int n = (nt_base + wave * NTW + t) * 16 + col;
-        n = n < N ? n : N - 1;
-        bk[t] = 16 * kq;
+    for (int t = 0; t < NTW; ++t)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) bo[t][h] = (uint32_t)n * K + 64 * h + 16 * kq;
-    }
+        for (int h = 0; h < 2; ++h) {
+            int n = (nt_base + wave * NTW + t) * 16 + 8 * h + (lane >> 3);
+            n = n < N ? n : N - 1;
+            bk[t][h] = 16 * ((lane & 7) ^ (lane >> 3));
+            bo[t][h] = (uint32_t)n * K + bk[t][h];
+        }
     auto issue = [&](int kb, int slot) {
         kb = kb_lo + (kb < nkb ? kb : nkb - 1);
         const uint32_t st = lds0 + (uint32_t)slot * kF8Stage;
@@ -775,7 +785,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
 #pragma unroll
             for (int h = 0; h < 2; ++h)
                 lds_copy(rW, st + kF8StB + (wave * NTW + i) * 2048 + h * 1024,
-                           kb * 128 + 64 * h + bk[i] < K ? bo[i][h] + kb * 128 : kOut);
+                         kb * 128 + bk[i][h] < K ? bo[i][h] + kb * 128 : kOut);
     };
     // block-scale rows of this wave's two n-tiles (a 16-row tile lies in one band)
     const float* srow[NTW];
@@ -794,7 +804,11 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
 #pragma unroll
     for (int d = 0; d < D; ++d) issue(d, d);
 
-    const int boff = 16 * col + 8 * (kq & 1);
+    // A operand of (m-tile mt, step j), lane (col, kq): row 16 mt + col, k
+    // chunk 4 j + kq at position (4 j + kq) ^ col; codes of step j for n-tile
+    // row col: chunk 2 j + kq / 2 at position (2 j + kq / 2) ^ (col % 8),
+    // half kq % 2
+    const int arow = col * 256, brow = col * 128 + 8 * (kq & 1);
     for (int kb0 = 0; kb0 < nkb; kb0 += NS) {
 #pragma unroll
         for (int u = 0; u < NS; ++u) {
@@ -814,12 +828,12 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
                 u32x4 a[4];
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
-                    a[mt] = *reinterpret_cast<const u32x4*>(st + kF8StA + (mt * 4 + j) * 1024 + lane * 16);
+                    a[mt] = *reinterpret_cast<const u32x4*>(st + kF8StA + mt * 4096 + arow +
+                                                            16 * ((4 * j + kq) ^ col));
 #pragma unroll
                 for (int t = 0; t < NTW; ++t) {
                     const uint2 w8 = *reinterpret_cast<const uint2*>(
-                        st + kF8StB + (wave * NTW + t) * 2048 + (j >> 1) * 1024 + 256 * (2 * (j & 1) + (kq >> 1)) +
-                        boff);
+                        st + kF8StB + (wave * NTW + t) * 2048 + brow + 16 * ((2 * j + (kq >> 1)) ^ (col & 7)));
                     const u32x4 b = fp8x8_to_16<BF16>(w8.x, w8.y);
 #pragma unroll
                     for (int mt = 0; mt < 4; ++mt) part[mt][t] = mfma16<BF16>(a[mt], b, part[mt][t]);
@@ -975,8 +989,12 @@ hipError_t fp8_gemm(const uint16_t* A, const uint8_t* W, const float* Sc, const 
         const int kb_per = (nkb + s - 1) / s;
         int* cnt = s > 1 ? static_cast<int*>(ws) : nullptr;
         float* part = s > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kF8CntBytes) : nullptr;
-        hipLaunchKernelGGL((fp8_gemm_mfma<BF16>), dim3(tiles, s), dim3(64 * kF8Waves), kF8Lds, st, A, W, Sc, bias, C,
-                           M, N, K, nks, kb_per, part, cnt);
+        if (tiles * s > 256)
+            hipLaunchKernelGGL((fp8_gemm_mfma<BF16, 1>), dim3(tiles, s), dim3(64 * kF8Waves), fp8_gemm_lds(1), st, A,
+                               W, Sc, bias, C, M, N, K, nks, kb_per, part, cnt);
+        else
+            hipLaunchKernelGGL((fp8_gemm_mfma<BF16, 3>), dim3(tiles, s), dim3(64 * kF8Waves), fp8_gemm_lds(3), st, A,
+                               W, Sc, bias, C, M, N, K, nks, kb_per, part, cnt);
         return hipGetLastError();
     }
     // decode-shaped kernel, 16 activation rows per launch
