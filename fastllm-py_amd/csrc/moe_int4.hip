@@ -1946,9 +1946,13 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
 // a stage to all waves.  One block ahead in two stages (two workgroups per
 // CU): config 5 148.8-154.2 us per layer, against 190.9 us two blocks ahead
 // in three stages (one workgroup per CU).  A stage holds
-//   * A (16 KB): 64 rows x 128 k fp16, fragment-major for the row-major k
-//     order of the stacked tile layout -- lane (c, q) of MFMA step j reads
-//     row c, k 32 q + 8 j .. + 7 at 16 (64 (4 mt + j) + c + 16 q);
+//   * A (16 KB): 64 rows x 128 k fp16.  FP8 / MXFP4: row-major (256 B per
+//     row) with the 16-byte k chunks of row r XOR-swizzled by r % 16, so
+//     each copy moves 4 whole rows and the 16 lanes of an MFMA operand read
+//     hit 16 different bank groups -- lane (c, q) of MFMA step j of m-tile
+//     mt reads row 16 mt + c, chunk a_koff(q, j) / 8 at position chunk ^ c.
+//     INT4: fragment-major -- lane (c, q) of MFMA step j reads row c, k
+//     32 q + 8 j .. + 7 at 16 (64 (4 mt + j) + c + 16 q);
 //   * per wave (2.5 KB): its two 1 KB tile blocks and the tiles' 16 x
 //     (128 / gs) scale|zero words.
 // B is dequantized in registers to s * (q - z) in fp16 (lane (c, q)'s 32 k
@@ -1986,6 +1990,11 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
     constexpr int TB = 1024 * BPT;               // tile block bytes
     constexpr int WST = mg_wave_stage(FMT), STG = mg_stage(FMT);
     constexpr int LPB = FPW + 2 * BPT + 2;  // per block and wave: A fragments, B copies, 2 scale rows
+    // FP8 / MXFP4 stage A row-major in whole rows (config 5: FP8 204 -> 198,
+    // MXFP4 150 -> 147 us per layer); INT4 keeps the MFMA fragment order,
+    // whose reads need no per-step lane addressing (its dequantization keeps
+    // the VALU busy: 146 against 160 us with whole rows)
+    constexpr bool ROWA = FMT != kFmtInt4;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, kq = lane >> 4;
@@ -2063,16 +2072,22 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
 
     for (int mc = 0; mc < M; mc += 64) {
         const int mt_live = (M - mc + 15) >> 4;  // m-tiles holding rows of this chunk
-        // A fragments f = FPW wave + i (f = 4 m-tile + j) of this wave
+        // A copies f = FPW wave + i of this wave.  FP8 / MXFP4 (ROWA): chunk
+        // rows 4 f .. 4 f + 3 (m-tile f / 4), each the row's whole 256 bytes
+        // of the block (two full cache lines); lane l takes row 4 f + l / 16
+        // and its 16-byte k chunk (l % 16) ^ (row % 16).  INT4: fragment f =
+        // 4 m-tile + j in MFMA order (16 rows x four 16-byte pieces).
         uint32_t ao[4];
 #pragma unroll
         for (int i = 0; i < FPW; ++i) {
             const int f = wave * FPW + i;
-            int m = mc + 16 * (f >> 2) + col;
+            const int r = ROWA ? 4 * f + (lane >> 4) : 16 * (f >> 2) + col;
+            int m = mc + r;
             m = m < M ? m : M - 1;
             const int row = PHASE == 0 ? (is_shared ? m : clampi(a.tok[row0 + m], 0, a.T - 1))
                                        : row0 + m;
-            ao[i] = 2u * ((uint32_t)row * astride + a_koff<FMT>(kq, f & 3));
+            ao[i] = 2u * ((uint32_t)row * astride +
+                          (ROWA ? 8 * ((lane & 15) ^ (r & 15)) : a_koff<FMT>(kq, f & 3)));
         }
         auto issue = [&](int kb, int stg) {
             kb = kb < nkb ? kb : nkb - 1;
@@ -2117,7 +2132,7 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
                     bl[t].sz = *reinterpret_cast<const uint32_t*>(wst + 2 * TB + t * 256 +
                                                                   (FMT == kFmtMx4 ? 4 * col : 0));
                 }
-                const unsigned char* ab = st + lane * 16;
+                const unsigned char* ab = st + col * 256;  // ROWA (FP8 / MXFP4)
                 f32x4 part[4][2];
 #pragma unroll
                 for (int mt = 0; mt < 4; ++mt)
@@ -2128,7 +2143,7 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
                     f16x8 av[4];
 #pragma unroll
                     for (int mt = 0; mt < 4; ++mt)
-                        av[mt] = *reinterpret_cast<const f16x8*>(ab + (mt * 4 + j) * 1024);
+                        av[mt] = *reinterpret_cast<const f16x8*>(ab + mt * 4096 + 16 * ((a_koff<FMT>(kq, j) >> 3) ^ col));
 #pragma unroll
                     for (int t = 0; t < 2; ++t) {
                         const f16x8 b = wblk_operand(bl[t], j);
@@ -2172,7 +2187,7 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
                 tile_zero_bits(sz_zero(szw), zlo[t], zhi[t]);
                 sc[t] = sz_scale(szw);
             }
-            const unsigned char* ab = st + lane * 16;
+            const unsigned char* ab = st + lane * 16;  // INT4: fragment order
             // group 128: q - z products accumulate in a per-block fp32 partial
             // that takes the column scale once; smaller groups scale B in fp16
             f32x4 part[4][2];
