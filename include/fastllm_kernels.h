@@ -91,7 +91,9 @@ bool fastllm_int4_gemm_config(const void *a, const uint32_t *b_q_weight,
  * (deterministic) and writes c.  workspace: device memory of at least
  * fastllm_int4_gemm_ws_bytes(size_m, size_n, size_k, group_size) bytes,
  * 256-byte aligned, zero-filled once before first use (its counters are left
- * at zero by every call); calls sharing a workspace must not overlap.  A
+ * at zero by every call, in a fixed 64 KiB region whatever the shape, so
+ * calls of different shapes may share one workspace); calls sharing a
+ * workspace must not overlap.  A
  * workspace of 0 bytes (or NULL) runs the unsplit kernels.  cfg (NULL for
  * the built-in choice) forces {tiles, waves, blocks per wave, splits} for
  * tuning; a forced shape the kernels cannot take returns 2.  Returns 0, 1
