@@ -255,8 +255,12 @@ __global__ __launch_bounds__(1024) void int4_tile_mm(
 //         banks).  Against AM 3 it moves the unique 2 KB per block instead
 //         of 16 rows' fragments and holds no VGPRs: Qwen3-8B M = 8 qkv 6.38
 //         -> 5.99, o 5.41 -> 5.00, gate_up 14.8 -> 13.8, down 10.5 -> 9.9 us.
-//         The same copies of 16 rows (4 KB per block) were no faster than
-//         AM 3 at M = 16 (gate_up split 16.1 -> 20.6 us);
+//       AM 6 (8 < M <= 16): the block's 16 rows as whole 256-byte rows,
+//         4 per copy (16-byte k chunks XOR-swizzled by row), 4 KB per block:
+//         Qwen3-8B M = 16 qkv 7.56 -> 6.34, o 6.64 -> 5.27 us.  Copies of
+//         16 rows x 64 B (the MFMA fragment order) were no faster than AM 3:
+//         such a copy costs the CU's vector-cache path four times the
+//         accesses of whole lines;
 //       AM 3 (M > 4, NB <= 4): each lane loads its own MFMA A operands of all
 //         its blocks from global memory into registers (4 x 16 B per block),
 //         first of all, so they arrive ahead of the weights in issue order;
@@ -327,11 +331,11 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
     }
     constexpr bool ALDS = AM == 1;
     // per-wave LDS copies of the wave's own blocks: ACP 1 KB copies per block
-    constexpr bool ACOPY = AM == 0 || AM == 4 || AM == 5;
-    constexpr int ACP = AM == 5 ? 2 : 1;
+    constexpr bool ACOPY = AM == 0 || AM == 4 || AM == 5 || AM == 6;
+    constexpr int ACP = AM == 5 ? 2 : (AM == 6 ? 4 : 1);
     const int lda = K + 8;
     f16* As = reinterpret_cast<f16*>(smem);
-    // AM 0/4/5: wave w's slot of NB blocks x ACP KB at w * NB * ACP KB
+    // AM 0/4/5/6: wave w's slot of NB blocks x ACP KB at w * NB * ACP KB
     const size_t abytes = ACOPY ? (size_t)nwaves * NB * ACP * 1024
                                 : (ALDS ? (((size_t)M * lda * 2 + 15) & ~(size_t)15) : 0);
     float* red = reinterpret_cast<float*>(smem + abytes);
@@ -428,6 +432,26 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
             for (int p = 0; p < 2; ++p)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(aslot + (i * 2 + p) * 1024), 16,
                                                          ao + 128u * p, kb * 256, 0, 0);
+        }
+    }
+    if (AM == 6) {
+        // the block's 16 rows (rows past M repeat row M - 1) as whole 256-byte
+        // rows, 4 per copy: lane l of copy p takes row r = 4 p + l / 16 and
+        // its 16-byte k chunk (l % 16) ^ r into position l % 16 of that row
+        // (16 rows x 64 B per copy, the MFMA fragment order, cost the CU's
+        // vector-cache path four times the accesses)
+        const __amdgpu_buffer_rsrc_t rA = buf_rsrc(A, (uint32_t)M * K * 2);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            int kb = wave + (i < nb ? i : (nb > 0 ? nb - 1 : 0)) * nwaves;
+            kb = kb < nfull ? kb : nfull - 1;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int r = 4 * p + (lane >> 4);
+                const uint32_t ao = 2u * ((uint32_t)(r < M ? r : M - 1) * K + 8 * ((lane & 15) ^ r));
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(aslot + (i * 4 + p) * 1024), 16, ao,
+                                                         kb * 256, 0, 0);
+            }
         }
     }
     if (AM == 4) {
@@ -585,6 +609,9 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
             if (AM == 0 || AM == 4)
                 a[j] = *reinterpret_cast<const f16x8*>(aslot + (size_t)i * 1024 + arow_m * 256 +
                                                        2 * (32 * j + 8 * kq));
+            else if (AM == 6)
+                a[j] = *reinterpret_cast<const f16x8*>(aslot + (size_t)i * 4096 + arow_m * 256 +
+                                                       16 * ((4 * j + kq) ^ arow_m));
             else if (AM == 5)
                 a[j] = *reinterpret_cast<const f16x8*>(aslot + (size_t)(i * 2 + (j >> 1)) * 1024 +
                                                        16 * ((col & 7) + 8 * kq + 32 * (j & 1)));
@@ -638,7 +665,7 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
     if (G32 && (K & 127) && wave == 0) {
         // trailing 64-k block: two 32-k groups
         f16x8 a[2];
-        const f16* arow_t = (AM == 0 || AM == 3 || AM == 5) ? A + (size_t)arow_m * K + 8 * kq : arow;
+        const f16* arow_t = (AM == 0 || AM == 3 || AM == 5 || AM == 6) ? A + (size_t)arow_m * K + 8 * kq : arow;
 #pragma unroll
         for (int j = 0; j < 2; ++j)
             a[j] = *reinterpret_cast<const f16x8*>(arow_t + nfull * 128 + 32 * j);
@@ -1029,6 +1056,9 @@ hipError_t launch_gemv_nb(const f16* A, const uint32_t* Wq, const uint16_t* S, c
     else if (M <= 8 && 2 * own + red <= 160 * 1024)
         hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 5>), grid, block, 2 * own + red, stream, A, Wq, S, Z,
                            C, M, N, K, sp);
+    else if (M > 8 && 4 * own + red <= 160 * 1024)
+        hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 6>), grid, block, 4 * own + red, stream, A, Wq, S, Z,
+                           C, M, N, K, sp);
     else if (NB <= 4)
         hipLaunchKernelGGL((int4_gemv_nb<T, NB, G32, 3>), grid, block, red, stream, A, Wq, S, Z, C, M,
                            N, K, sp);
@@ -1066,6 +1096,8 @@ hipError_t launch_gemv_t4(const f16* A, const uint32_t* Wq, const uint16_t* S, c
     const size_t red = (size_t)waves * 4 * 256 * sizeof(float);
     const size_t own = (size_t)waves * NB * 1024;
     const dim3 grid(N / 64, split), block(64 * waves);
+    // above M = 8 register fragments: AM 6's 4 KB per block leave one
+    // workgroup per CU here (gate_up M = 16, split 2: 16.1 us against 20.1)
     if (M <= 8 && 2 * own + red <= 160 * 1024)
         hipLaunchKernelGGL((int4_gemv_nb<4, NB, G32, 5>), grid, block, 2 * own + red, stream, A, Wq, S, Z,
                            C, M, N, K, sp);
@@ -1294,15 +1326,18 @@ hipError_t launch_gemv_swiglu(const f16* A, const uint32_t* Wq, const uint16_t* 
     const size_t own = (size_t)waves * NB * 1024;
     const dim3 grid(N / 32), block(64 * waves);
     if (own + red > kMaxLds) return hipErrorInvalidValue;
-    // LDS activation copies up to M = 8 (AM 0; AM 5 above four rows while
-    // its 2 KB per block fit), register activations above (NB <= 4: more
-    // blocks per wave spill there)
+    // LDS activation copies (AM 0; AM 5 above four rows, AM 6 above eight,
+    // while their 2 or 4 KB per block fit), register activations otherwise
+    // (NB <= 4: more blocks per wave spill there)
     if (M <= 4) {
         hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 0, true>), grid, block, own + red, stream, A, Wq, S,
                            Z, H, M, N, K);
     } else if constexpr (NB <= 4) {
         if (M <= 8 && 2 * own + red <= kMaxLds)
             hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 5, true>), grid, block, 2 * own + red, stream, A,
+                               Wq, S, Z, H, M, N, K);
+        else if (M > 8 && 4 * own + red <= kMaxLds)
+            hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 6, true>), grid, block, 4 * own + red, stream, A,
                                Wq, S, Z, H, M, N, K);
         else
             hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 3, true>), grid, block, red, stream, A, Wq, S, Z,
