@@ -338,7 +338,14 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
     // AM 0/4/5/6: wave w's slot of NB blocks x ACP KB at w * NB * ACP KB
     const size_t abytes = ACOPY ? (size_t)nwaves * NB * ACP * 1024
                                 : (ALDS ? (((size_t)M * lda * 2 + 15) & ~(size_t)15) : 0);
-    float* red = reinterpret_cast<float*>(smem + abytes);
+    // AM 6 with four tiles: the cross-wave reduction reuses the activation
+    // slots once every wave is past its blocks (a barrier first), so the
+    // launch needs the larger of the two, not their sum -- two workgroups
+    // per CU where the sum allowed one (down M = 16, four tiles, three K
+    // splits: 11.0 us against 11.95 with register fragments).  With one or
+    // two tiles the extra barrier cost more than it saved.
+    constexpr bool RALIAS = AM == 6 && T == 4;
+    float* red = reinterpret_cast<float*>(smem + (RALIAS ? 0 : abytes));
 
     const int nb = wave < nfull ? (nfull - wave + nwaves - 1) / nwaves : 0;
 
@@ -687,6 +694,7 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
     }
 
     // cross-wave reduction in fixed wave order; only rows < M are written
+    if (RALIAS) __syncthreads();  // the activation slots are dead
 #pragma unroll
     for (int t = 0; t < T; ++t)
         *reinterpret_cast<f32x4*>(red + (wave * T + t) * 256 + lane * 4) = acc[t];
@@ -1096,11 +1104,15 @@ hipError_t launch_gemv_t4(const f16* A, const uint32_t* Wq, const uint16_t* S, c
     const size_t red = (size_t)waves * 4 * 256 * sizeof(float);
     const size_t own = (size_t)waves * NB * 1024;
     const dim3 grid(N / 64, split), block(64 * waves);
-    // above M = 8 register fragments: AM 6's 4 KB per block leave one
-    // workgroup per CU here (gate_up M = 16, split 2: 16.1 us against 20.1)
+    // above M = 8: AM 6 with the reduction in the activation slots from two
+    // blocks per wave; one block per wave measured even with register
+    // fragments (gate_up M = 16, split 2: 16.4 against 16.3 us)
     if (M <= 8 && 2 * own + red <= 160 * 1024)
         hipLaunchKernelGGL((int4_gemv_nb<4, NB, G32, 5>), grid, block, 2 * own + red, stream, A, Wq, S, Z,
                            C, M, N, K, sp);
+    else if (M > 8 && NB >= 2 && (4 * own > red ? 4 * own : red) <= 160 * 1024)
+        hipLaunchKernelGGL((int4_gemv_nb<4, NB, G32, 6>), grid, block, 4 * own > red ? 4 * own : red, stream,
+                           A, Wq, S, Z, C, M, N, K, sp);
     else
         hipLaunchKernelGGL((int4_gemv_nb<4, NB, G32, 3>), grid, block, red, stream, A, Wq, S, Z, C, M, N,
                            K, sp);
@@ -1146,6 +1158,16 @@ GemvCfg default_gemv_cfg(int M, int N, int K, bool g32, bool can_split = false) 
         // 4096 x 12288); wide N above M = 8: four tiles, two splits of one
         // block per wave (18.6 -> 16.7 us at 24576 x 4096, M = 16).
         const int nall = K / 128;
+        if (M > 8 && nall >= 64 && nall % 3 == 0 && nall / 3 <= 16 * 2) {
+            // above eight rows: four tiles, three splits of two blocks per
+            // wave, activations copied in whole rows (4096 x 12288, M = 16:
+            // 12.35 -> 11.0 us)
+            c.tiles = 4;
+            c.waves = 16;
+            c.nb = nb_bucket((nall / 3 + 15) / 16);
+            c.split = 3;
+            return c;
+        }
         if (nall >= 64 && nall % 2 == 0 && nall / 2 <= 16 * 8) {
             c.tiles = 2;
             c.waves = 16;
@@ -1337,8 +1359,8 @@ hipError_t launch_gemv_swiglu(const f16* A, const uint32_t* Wq, const uint16_t* 
             hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 5, true>), grid, block, 2 * own + red, stream, A,
                                Wq, S, Z, H, M, N, K);
         else if (M > 8 && 4 * own + red <= kMaxLds)
-            hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 6, true>), grid, block, 4 * own + red, stream, A,
-                               Wq, S, Z, H, M, N, K);
+            hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 6, true>), grid, block, 4 * own + red, stream, A, Wq,
+                               S, Z, H, M, N, K);
         else
             hipLaunchKernelGGL((int4_gemv_nb<2, NB, G32, 3, true>), grid, block, red, stream, A, Wq, S, Z,
                                H, M, N, K);

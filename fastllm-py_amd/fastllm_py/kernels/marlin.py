@@ -91,23 +91,23 @@ def build_marlin_scales_zeros(scale, zero_int, group_size, xp=np):
     return nat.as_output(scales, numpy_in), nat.as_output(zeros, numpy_in)
 
 
-# Decode GEMVs above four rows split K in two where that pays (long K, or
-# wide N above eight rows); their per-strip counters (a fixed 64 KiB region
-# at offset 0, the same for every shape) and fp32 partials live in the
-# workspace: 128 * size_n bytes for up to 16 rows after the counters, beside
-# the reference's (size_n // 64) * 16 ints.
+# Decode GEMVs above four rows split K in two or three where that pays
+# (long K, or wide N above eight rows); their per-strip counters (a fixed
+# 64 KiB region at offset 0, the same for every shape) and fp32 partials live
+# in the workspace: 192 * size_n bytes for up to 3 splits of 16 rows after
+# the counters, beside the reference's (size_n // 64) * 16 ints.
 _SPLIT_COUNTER_BYTES = 16384 * 4
 
 
 def _workspace_ints(size_n: int) -> int:
-    split_bytes = _SPLIT_COUNTER_BYTES + 2 * 16 * size_n * 4
+    split_bytes = _SPLIT_COUNTER_BYTES + 3 * 16 * size_n * 4
     return max(max(1, (size_n // 64) * 16), split_bytes // 4)
 
 
 def make_workspace(size_n, xp=None):
     """Zeroed int32 workspace for one call site (marlin.py:162-167).  Besides
     the reference's max(1, (size_n//64)*16) ints it holds the split-K
-    partials of the decode GEMVs above four rows (128 * size_n bytes); the
+    partials of the decode GEMVs above four rows (192 * size_n bytes); the
     kernels leave its counters at zero."""
     t = nat.torch()
     nat.require_device()

@@ -88,17 +88,20 @@ def test_moe_entry_argument_checks():
 
 def test_int4_split_workspace_sizes():
     """Split-K workspace query (host arithmetic only): above four rows the
-    long-K down shape and (above eight rows) the wide gate_up shape split in
-    two (counters in a fixed 64 KiB region from offset 0 for every shape,
-    then 2 x M x N fp32 partials); qkv / o and four rows or fewer do not
-    split; the Python layer's make_workspace covers every split shape."""
+    long-K down shape splits in two (three above eight rows) and (above eight
+    rows) the wide gate_up shape in two (counters in a fixed 64 KiB region
+    from offset 0 for every shape, then splits x M x N fp32 partials); qkv /
+    o and four rows or fewer do not split; the Python layer's make_workspace
+    covers every split shape."""
     from fastllm_py.kernels.marlin import _workspace_ints
 
     lib = _native.lib()
     part = lambda N: 16384 * 4  # noqa: E731
     down, gate_up = (4096, 12288), (24576, 4096)
-    for M in (5, 8, 16):
+    for M in (5, 8):
         assert lib.fastllm_int4_gemm_ws_bytes(M, *down, 128) == part(4096) + 2 * M * 4096 * 4
+    for M in (9, 16):  # above eight rows: three splits
+        assert lib.fastllm_int4_gemm_ws_bytes(M, *down, 128) == part(4096) + 3 * M * 4096 * 4
     assert lib.fastllm_int4_gemm_ws_bytes(16, *gate_up, 128) == part(24576) + 2 * 16 * 24576 * 4
     assert lib.fastllm_int4_gemm_ws_bytes(8, *gate_up, 128) == 0
     for N, K in ((6144, 4096), (4096, 4096)):
