@@ -472,7 +472,13 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q4(
 //   * Accumulator element e of lane l is A row 4 (l / 16) + e: half
 //     (l / 16) / 2, activation row 4 ((l / 16) % 2) + e; it is a diagonal
 //     element when that half equals the lane's column half.
-template <int NB, bool INLINE, bool BF16, bool ALDS>
+//   * RING (4 < M <= 8, where the slots' 4 KB of activations each do not
+//     fit the LDS): a ring of two LDS slots per wave, each slot's 8 rows x 2
+//     halves as whole 256-byte rows (16-byte k chunks of row-half rh
+//     XOR-swizzled by rh), slots 0 and 1 copied before the weight loads and
+//     slot i + 2 once slot i has been read.  M = 8: 2048 x 10944 10.08 ->
+//     8.37 us, 2048 x 2048 3.56 -> 3.28 us against register fragments.
+template <int NB, bool INLINE, bool BF16, bool ALDS, bool RING = false>
 __global__ __launch_bounds__(1024) void fp8_gemv_q2(
     const uint16_t* __restrict__ A, const uint8_t* __restrict__ W, const float* __restrict__ Sc,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ C, int M, int N, int K, int rs,
@@ -494,7 +500,27 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
     // half col / 8, k 32 kq + {0, 8, 16, 24} of the slot's block
     const int arow = (col & 7) < M ? (col & 7) : M - 1;
     u32x4 ar[NB][4];
-    unsigned char* aslot = smem + (size_t)wave * NB * 2048;
+    unsigned char* aslot = smem + (size_t)wave * (RING ? 2 * 4096 : NB * 2048);
+    const __amdgpu_buffer_rsrc_t rAr = buf_rsrc(A, (uint32_t)M * K * 2);
+    // RING: the four copies of slot i into ring position i & 1 -- copy c
+    // lane l: row-half rh = 4 c + l / 16 (row rh / 2 clamped to M - 1, half
+    // rh % 2), k chunk (l % 16) ^ rh of the half's block, to position l % 16
+    auto ring_copy = [&](int i) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int rh = 4 * c + (lane >> 4);
+            const int m = (rh >> 1) < M ? (rh >> 1) : M - 1;
+            int kb = (rh & 1) * HB + slot_b(i);
+            kb = kb < nfull ? kb : nfull - 1;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rAr, (lptr_t)(aslot + (i & 1) * 4096 + c * 1024), 16,
+                2u * ((uint32_t)m * K + kb * 128 + 8 * ((lane & 15) ^ rh)), 0, 0, 0);
+        }
+    };
+    if (RING) {
+        ring_copy(0);
+        if (NB > 1) ring_copy(1);
+    }
     if (ALDS) {
         // chunk q = ((i M + m) 2 + half) 16 + p (16 B each) lands at 16 q
         const int total = NB * M * 32;
@@ -510,7 +536,7 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rA, (lptr_t)(aslot + c * 1024), 16,
                                                      2u * ((uint32_t)m * K + kb * 128 + pc * 8), 0, 0, 0);
         }
-    } else {
+    } else if (!RING) {
         const uint16_t* ap = A + (size_t)arow * K + 32 * kq;
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
@@ -556,16 +582,33 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
         constexpr int WL = NB * 2;
         wait_vmcnt<(WL < 63 ? WL : 63)>();
     }
+    const int rhl = 2 * arow + h;  // RING: this lane's row-half
 
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         u32x4 lo, hi;
         trade_pieces(ld0[i], ld1[i], up, lo, hi);
+        if (RING) {
+            // slot i's copies are done once at most the loads issued after
+            // them are outstanding: slot 0 -- slot 1's copies and every code
+            // load; slot 1 -- the code loads and slot 2's copies; slot i >= 2
+            // -- slot i + 1's copies
+            if (i == 0)
+                wait_vmcnt<((NB > 1 ? 4 : 0) + 2 * NB < 63 ? (NB > 1 ? 4 : 0) + 2 * NB : 63)>();
+            else if (i == 1)
+                wait_vmcnt<(2 * NB + (NB > 2 ? 4 : 0) < 63 ? 2 * NB + (NB > 2 ? 4 : 0) : 63)>();
+            else if (i + 1 < NB)
+                wait_vmcnt<4>();
+            else
+                wait_vmcnt<0>();
+        }
         u32x4 a[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             a[j] = ALDS ? *reinterpret_cast<const u32x4*>(aslot + (size_t)(((i * M + arow) * 2 + h) * 16 + 4 * kq + j) * 16)
+                 : RING ? *reinterpret_cast<const u32x4*>(aslot + (i & 1) * 4096 + rhl * 256 +
+                                                          16 * ((4 * kq + j) ^ rhl))
                         : ar[i][j];
         f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
         part = mfma16<BF16>(a[0], fp8x8_to_16<BF16>(lo[0], lo[1]), part);
@@ -575,6 +618,12 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(sv[i], part[e], acc[e]);
         __builtin_amdgcn_sched_barrier(0);
+        // slot i has been read (its MFMAs consumed the reads): its ring
+        // position takes slot i + 2
+        if (RING && i + 2 < NB) {
+            ring_copy(i + 2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 
     if (!INLINE && (K & 127) && wave == 0) {
@@ -597,7 +646,8 @@ __global__ __launch_bounds__(1024) void fp8_gemv_q2(
     }
 
     // diagonal elements: half (kq / 2) == h, activation row 4 (kq % 2) + e
-    float* red = reinterpret_cast<float*>(smem + (ALDS ? (size_t)nwaves * NB * 2048 : 0));
+    float* red = reinterpret_cast<float*>(smem + (ALDS ? (size_t)nwaves * NB * 2048
+                                                        : RING ? (size_t)nwaves * 2 * 4096 : 0));
     if ((kq >> 1) == h) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) red[(wave * 16 + col) * 8 + 4 * (kq & 1) + e] = acc[e];
@@ -625,6 +675,9 @@ hipError_t launch_fp8_q2(const uint16_t* A, const uint8_t* W, const float* Sc, c
     if (M <= 4)
         hipLaunchKernelGGL((fp8_gemv_q2<NB, INLINE, BF16, true>), dim3((N + 7) / 8), dim3(64 * waves),
                            (size_t)waves * NB * 2048 + red, st, A, W, Sc, bias, C, M, N, K, rs, nks);
+    else if ((size_t)waves * 2 * 4096 + red <= 160 * 1024)
+        hipLaunchKernelGGL((fp8_gemv_q2<NB, INLINE, BF16, false, true>), dim3((N + 7) / 8), dim3(64 * waves),
+                           (size_t)waves * 2 * 4096 + red, st, A, W, Sc, bias, C, M, N, K, rs, nks);
     else
         hipLaunchKernelGGL((fp8_gemv_q2<NB, INLINE, BF16, false>), dim3((N + 7) / 8), dim3(64 * waves), red, st,
                            A, W, Sc, bias, C, M, N, K, rs, nks);

@@ -70,8 +70,15 @@ def copy_wait_violations(asm: str) -> tuple[list, int]:
         if not copies:
             continue
         checked += 1
+        # the copies issued before the kernel's first other load (a ring's
+        # later refills are waited for by counts of their own, checked by the
+        # kernel's parity tests)
+        others = [i for i, s in enumerate(body) if i > copies[0] and re.match(r"(global|buffer)_(load|atomic)", s)
+                  and not re.search(r"\blds\b", s)]
+        first_other = others[0] if others else len(body)
+        last = max(i for i in copies if i < first_other)
         after, verdict = 0, None
-        for s in body[copies[-1] + 1:]:
+        for s in body[last + 1:]:
             if re.match(r"(global|buffer)_(load|atomic)", s):
                 after += 1
             m = re.match(r"s_waitcnt vmcnt\((\d+)\)", s)
