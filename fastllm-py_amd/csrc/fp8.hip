@@ -751,8 +751,12 @@ constexpr size_t kFp8LdsCap = 96 * 1024;
 
 // Prefill-shaped FP8 GEMM (M > kF8MinM, 128 x 128 block format, K % 128 ==
 // 0) on the matrix cores: the INT4 MFMA GEMM's structure with e4m3 weights.
-//   * Workgroup tile 64 (m) x 128 (n), eight waves side by side along n, a
-//     64 x 16 wave tile (4 m-tiles x one n-tile of 16 x 16 fp32).
+//   * Workgroup tile BM (m) x 128 (n), eight waves side by side along n, a
+//     BM x 16 wave tile (BM / 16 m-tiles x one n-tile of 16 x 16 fp32).
+//     BM = 64, or 32 where the 64-row grid has at most 128 tiles and no K
+//     split (2048 x 2048, M = 512: 13.6 -> 10.0 us; the copies bound the
+//     kernel per CU, and twice the workgroups reach every CU for 1.5x the
+//     lines copied in all).
 //   * Every main-loop load goes global -> LDS (lds_copy: buffer_load ...
 //     lds from inline asm) D 128-k blocks ahead into D + 1 stages of 32 KB
 //     (D = 1: two workgroups per CU; D = 3: one), one vmcnt wait and one
@@ -779,15 +783,14 @@ constexpr int kF8BM = 64, kF8BN = 128, kF8MinM = 64;
 // measured slower at M = 512: 26.7 / 65.0 / 132.4 us, with half the waves
 // per SIMD to hide the LDS and conversion latencies.
 constexpr int kF8NTW = 1, kF8Waves = 8 / kF8NTW;
-constexpr int kF8AF = 16 / kF8Waves;               // A fragments each wave copies per block
 // Blocks in flight ahead of the one computed (the ring holds D + 1 stages
 // of 32 KB).  Grids of more than 256 workgroups take one block ahead, so
 // two workgroups share a CU; smaller grids (at most one per CU) three.  With
 // whole-line copies, M = 512: 10944 x 2048 (688 workgroups) 35.6 us one
 // ahead, 41.3 two, 39.7 three; 2048 x 2048 (128) 15.7 / 14.7 / 13.6;
 // 2048 x 10944 (two K splits, 256) 52.1 / 43.6 / 44.2.
-constexpr int kF8StA = 0, kF8StB = 16384, kF8Stage = kF8StB + 16384;
-constexpr size_t fp8_gemm_lds(int ahead) { return (size_t)(ahead + 1) * kF8Stage; }
+// stage = BM x 128 activations (bf16) + 128 x 128 codes
+constexpr size_t fp8_gemm_lds(int ahead, int bm) { return (size_t)(ahead + 1) * (bm * 256 + 16384); }
 
 // Split-K (gridDim.y > 1, grids of fewer than 256 tiles): split y takes 128-k
 // blocks [y kb_per, (y + 1) kb_per); each split stores its fp32 64 x 128
@@ -797,7 +800,7 @@ constexpr size_t fp8_gemm_lds(int ahead) { return (size_t)(ahead + 1) * kF8Stage
 // resets the counter.  Nothing waits on another workgroup.
 constexpr int kF8TileF = kF8BM * kF8BN;  // fp32 partials per tile and split
 
-template <bool BF16, int D>
+template <bool BF16, int D, int BM = 64>
 __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict__ A,
                                                      const uint8_t* __restrict__ W,
                                                      const float* __restrict__ Sc,
@@ -805,8 +808,13 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
                                                      uint16_t* __restrict__ C, int M, int N, int K,
                                                      int nks, int kb_per, float* __restrict__ part,
                                                      int* __restrict__ cnt) {
-    constexpr int NS = D + 1, NTW = kF8NTW, AF = kF8AF;
-    constexpr int LPB = AF + 2 * NTW;  // copies per block and wave: A fragments, 2 halves per tile
+    static_assert(BM == 32 || BM == 64, "tile height");
+    constexpr int NS = D + 1, NTW = kF8NTW;
+    constexpr int AF = BM / 32;          // A copies (4 rows each) per block and wave
+    constexpr int MT = BM / 16;          // m-tiles each wave computes
+    constexpr int LPB = AF + 2 * NTW;    // copies per block and wave: A rows, 2 halves per code tile
+    constexpr int STB = BM * 256;        // codes after the activation rows
+    constexpr int STG = STB + 16384;     // stage bytes
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -816,12 +824,12 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
     const int nkb = (nkb_all - kb_lo) < kb_per ? (nkb_all - kb_lo) : kb_per;  // this split's blocks
     const int ntiles = (N + 15) >> 4;
 
-    const int nblk = (N + kF8BN - 1) / kF8BN, mblk = (M + kF8BM - 1) / kF8BM;
+    const int nblk = (N + kF8BN - 1) / kF8BN, mblk = (M + BM - 1) / BM;
     const int total = nblk * mblk;
     int lin = blockIdx.x;
     if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);  // XCD-grouped
     const int nb_i = lin / mblk, mb_i = lin - nb_i * mblk;
-    const int m0 = mb_i * kF8BM;
+    const int m0 = mb_i * BM;
     const int nt_base = nb_i * 8;
 
     const i32x4_t rA = raw_rsrc(A, (uint32_t)M * K * 2);
@@ -857,15 +865,15 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
         }
     auto issue = [&](int kb, int slot) {
         kb = kb_lo + (kb < nkb ? kb : nkb - 1);
-        const uint32_t st = lds0 + (uint32_t)slot * kF8Stage;
+        const uint32_t st = lds0 + (uint32_t)slot * STG;
 #pragma unroll
         for (int i = 0; i < AF; ++i)
-            lds_copy(rA, st + kF8StA + (wave * AF + i) * 1024, kb * 128 + ak[i] < K ? ao[i] + kb * 256 : kOut);
+            lds_copy(rA, st + (wave * AF + i) * 1024, kb * 128 + ak[i] < K ? ao[i] + kb * 256 : kOut);
 #pragma unroll
         for (int i = 0; i < NTW; ++i)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
-                lds_copy(rW, st + kF8StB + (wave * NTW + i) * 2048 + h * 1024,
+                lds_copy(rW, st + STB + (wave * NTW + i) * 2048 + h * 1024,
                          kb * 128 + bk[i][h] < K ? bo[i][h] + kb * 128 : kOut);
     };
     // block-scale rows of this wave's two n-tiles (a 16-row tile lies in one band)
@@ -877,9 +885,9 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
         srow[t] = Sc + (size_t)((nt * 16) >> 7) * nks;
     }
 
-    f32x4 acc[4][NTW];
+    f32x4 acc[MT][NTW];
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int t = 0; t < NTW; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -898,33 +906,32 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
             wait_vmcnt<(D - 1) * LPB>();
             asm volatile("s_barrier" ::: "memory");
             issue(kb + D, (u + D) % NS);
-            const unsigned char* st = smem + (size_t)u * kF8Stage;
-            f32x4 part[4][NTW];
+            const unsigned char* st = smem + (size_t)u * STG;
+            f32x4 part[MT][NTW];
 #pragma unroll
-            for (int mt = 0; mt < 4; ++mt)
+            for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int t = 0; t < NTW; ++t) part[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                u32x4 a[4];
+                u32x4 a[MT];
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt)
-                    a[mt] = *reinterpret_cast<const u32x4*>(st + kF8StA + mt * 4096 + arow +
-                                                            16 * ((4 * j + kq) ^ col));
+                for (int mt = 0; mt < MT; ++mt)
+                    a[mt] = *reinterpret_cast<const u32x4*>(st + mt * 4096 + arow + 16 * ((4 * j + kq) ^ col));
 #pragma unroll
                 for (int t = 0; t < NTW; ++t) {
                     const uint2 w8 = *reinterpret_cast<const uint2*>(
-                        st + kF8StB + (wave * NTW + t) * 2048 + brow + 16 * ((2 * j + (kq >> 1)) ^ (col & 7)));
+                        st + STB + (wave * NTW + t) * 2048 + brow + 16 * ((2 * j + (kq >> 1)) ^ (col & 7)));
                     const u32x4 b = fp8x8_to_16<BF16>(w8.x, w8.y);
 #pragma unroll
-                    for (int mt = 0; mt < 4; ++mt) part[mt][t] = mfma16<BF16>(a[mt], b, part[mt][t]);
+                    for (int mt = 0; mt < MT; ++mt) part[mt][t] = mfma16<BF16>(a[mt], b, part[mt][t]);
                 }
             }
 #pragma unroll
             for (int t = 0; t < NTW; ++t) {
                 const float s = live ? srow[t][kb_lo + (kb < nkb ? kb : nkb - 1)] : 0.0f;
 #pragma unroll
-                for (int mt = 0; mt < 4; ++mt)
+                for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) acc[mt][t][e] = __builtin_fmaf(s, part[mt][t][e], acc[mt][t][e]);
             }
@@ -936,14 +943,14 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
         static_assert(NTW == 1, "split-K partials assume one n-tile per wave");
         __shared__ int last;
         const int nsplit = (int)gridDim.y;
-        const size_t tile_off = (size_t)blockIdx.x * kF8TileF;
-        const size_t split_stride = (size_t)gridDim.x * kF8TileF;
+        const size_t tile_off = (size_t)blockIdx.x * (BM * kF8BN);
+        const size_t split_stride = (size_t)gridDim.x * (BM * kF8BN);
         float* mine = part + (size_t)blockIdx.y * split_stride + tile_off;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                __hip_atomic_store(mine + ((wave * 4 + mt) * 4 + e) * 64 + lane, acc[mt][0][e], __ATOMIC_RELAXED,
+                __hip_atomic_store(mine + ((wave * MT + mt) * 4 + e) * 64 + lane, acc[mt][0][e], __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         // this wave's partial stores are complete (device-coherent stores: no
         // cache write-back needed)
@@ -955,10 +962,10 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
         __syncthreads();
         if (!last) return;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const size_t idx = tile_off + ((wave * 4 + mt) * 4 + e) * 64 + lane;
+                const size_t idx = tile_off + ((wave * MT + mt) * 4 + e) * 64 + lane;
                 float v = 0.0f;
                 for (int q = 0; q < nsplit; ++q)
                     v += __hip_atomic_load(part + q * split_stride + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -973,7 +980,7 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
         if (n >= N) continue;
         const float bv = bias ? act_to_f32<BF16>(bias[n]) : 0.0f;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int m = m0 + mt * 16 + 4 * kq + e;
@@ -1073,12 +1080,20 @@ hipError_t fp8_gemm(const uint16_t* A, const uint8_t* W, const float* Sc, const 
         const int kb_per = (nkb + s - 1) / s;
         int* cnt = s > 1 ? static_cast<int*>(ws) : nullptr;
         float* part = s > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + kF8CntBytes) : nullptr;
-        if (tiles * s > 256)
-            hipLaunchKernelGGL((fp8_gemm_mfma<BF16, 1>), dim3(tiles, s), dim3(64 * kF8Waves), fp8_gemm_lds(1), st, A,
-                               W, Sc, bias, C, M, N, K, nks, kb_per, part, cnt);
-        else
-            hipLaunchKernelGGL((fp8_gemm_mfma<BF16, 3>), dim3(tiles, s), dim3(64 * kF8Waves), fp8_gemm_lds(3), st, A,
-                               W, Sc, bias, C, M, N, K, nks, kb_per, part, cnt);
+        if (s == 1 && tiles <= 128) {
+            // at most half the chip with 64-row tiles and no K split: 32-row
+            // tiles, twice the workgroups (1.5x the lines copied in all, but
+            // on every CU)
+            const int t32 = ((N + kF8BN - 1) / kF8BN) * ((M + 31) / 32);
+            hipLaunchKernelGGL((fp8_gemm_mfma<BF16, 3, 32>), dim3(t32, 1), dim3(64 * kF8Waves), fp8_gemm_lds(3, 32),
+                               st, A, W, Sc, bias, C, M, N, K, nks, kb_per, part, cnt);
+        } else if (tiles * s > 256) {
+            hipLaunchKernelGGL((fp8_gemm_mfma<BF16, 1>), dim3(tiles, s), dim3(64 * kF8Waves), fp8_gemm_lds(1, 64), st,
+                               A, W, Sc, bias, C, M, N, K, nks, kb_per, part, cnt);
+        } else {
+            hipLaunchKernelGGL((fp8_gemm_mfma<BF16, 3>), dim3(tiles, s), dim3(64 * kF8Waves), fp8_gemm_lds(3, 64), st,
+                               A, W, Sc, bias, C, M, N, K, nks, kb_per, part, cnt);
+        }
         return hipGetLastError();
     }
     // decode-shaped kernel, 16 activation rows per launch

@@ -164,7 +164,8 @@ def test_fp8_block_gemv_fp16_bias_ragged(torch_gpu, N, K, M):
 # both activation types, bias
 @pytest.mark.parametrize("M,N,K,bf16", [(128, 2048, 2048, True), (200, 1000, 1024, False),
                                         (65, 4096, 512, True), (512, 10944, 2048, True),
-                                        (128, 2048, 10944, True), (96, 256, 320, False)])
+                                        (128, 2048, 10944, True), (96, 256, 320, False),
+                                        (512, 2048, 2048, True)])
 def test_fp8_block_gemm_prefill(torch_gpu, M, N, K, bf16):
     from fastllm_py import quantizer
     from fastllm_py.kernels import fp8
