@@ -1366,9 +1366,9 @@ __global__ void moe_fp8_tile_repack_k(const uint8_t* __restrict__ q, uint8_t* __
     const int nkb = in_f / 128;
     const size_t n = (size_t)rows * in_f / 16;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        // destination piece i: block (t, kb), lane l = c + 16 q, half h
+        // destination piece i: block (t, kb), half h, lane l = c + 16 q
         const size_t blk = i / 128;
-        const int within = (int)(i % 128), l = within >> 1, h = within & 1;
+        const int within = (int)(i % 128), h = within >> 6, l = within & 63;
         const size_t t = blk / nkb;
         const int kb = (int)(blk % nkb), c = l & 15, qq = l >> 4;
         const size_t src = (16 * t + c) * (size_t)in_f + 128 * kb + 32 * qq + 16 * h;
@@ -1495,9 +1495,10 @@ FL_DEV WBlk<FMT> wblk_load(const uint8_t* q, const uint32_t* sz, size_t tile, in
     WBlk<FMT> b;
     const size_t blk = tile * nkb + kb;
     if (FMT == kFmtFp8) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(q + blk * 2048 + lane * 32);
+        // the lane's two 16-byte halves, 1 KB apart: each load reads whole lines
+        const u32x4* p = reinterpret_cast<const u32x4*>(q + blk * 2048 + lane * 16);
         b.w = __builtin_nontemporal_load(p);
-        b.w2 = __builtin_nontemporal_load(p + 1);
+        b.w2 = __builtin_nontemporal_load(p + 64);
         b.sz = sz[(tile >> 3) * nkb + kb];  // fp32 bits of the 128x128 block scale
     } else {
         b.w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(q + blk * 1024 + lane * 16));
@@ -2100,8 +2101,8 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int h = 0; h < BPT; ++h)  // FP8: lane l's 32 bytes at 32 l (two copies)
-                    lds_copy(rq[t], wst + t * TB + h * 1024, BPT == 2 ? lane * 32 + h * 16 : lane * 16, kb * TB);
+                for (int h = 0; h < BPT; ++h)  // FP8: the block's two 1 KB halves
+                    lds_copy(rq[t], wst + t * TB + h * 1024, h * 1024 + lane * 16, kb * TB);
 #pragma unroll
             for (int t = 0; t < 2; ++t) lds_copy<4>(rz[t], wst + 2 * TB + t * 256, zlane, kb * zstep);
         };

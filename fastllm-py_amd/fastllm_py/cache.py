@@ -24,7 +24,7 @@ from . import _native as nat
 
 MARLIN_FORMAT = "fastllm-py_amd/marlin-tile/v1"
 EXPERTS_FORMAT = "fastllm-py_amd/marlin-experts/v1"
-STACKED_FORMAT = "fastllm-py_amd/stacked-tile/v1"
+STACKED_FORMAT = "fastllm-py_amd/stacked-tile/v2"  # v2: FP8 expert blocks as two 1 KB halves
 
 
 def _host(v):

@@ -454,8 +454,10 @@ int fastllm_moe_int4_tile_unpack(const uint8_t *qtile, const uint32_t *sz,
  * in_f % 128 == 0; stacked experts are rows e * out + r):
  *  - FP8: row-major e4m3 codes q u8 [rows, in_f] (fastllm_quantize_fp8_block
  *    with 128x128 blocks, out % 128 == 0 so no block straddles two experts)
- *    -> qtile u8 [rows/16, in_f/128, 2048]: block (t, kb) holds at byte
- *    32*(c + 16*q) the 32 codes of row 16*t + c, k = 128*kb + 32*q .. + 31.
+ *    -> qtile u8 [rows/16, in_f/128, 2048]: half h of block (t, kb) holds
+ *    at byte 1024*h + 16*(c + 16*q) the 16 codes of row 16*t + c,
+ *    k = 128*kb + 32*q + 16*h .. + 15 (each 16-byte load or copy of a lane
+ *    then reads whole cache lines with its wave).
  *    The block scales f32 [rows/128, in_f/128] are used as they are.
  *  - MXFP4: codes u8 [rows, in_f/2] and e8 u8 [rows, in_f/32] from
  *    fastllm_quantize_mxfp4 -> qtile u8 [rows/16, in_f/128, 1024] whose

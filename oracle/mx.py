@@ -101,14 +101,15 @@ def dequantize_mxfp4(packed, e8):
 
 
 def moe_tile_pack_fp8(q):
-    """Row-major e4m3 codes (rows, in) -> (rows/16, in/128, 2048) u8: lane
-    (c, q)'s 32 bytes at 32 (c + 16 q) are row 16 t + c, k = 128 kb + 32 q
-    + 0..31 in order (MFMA step j takes bytes 8 j .. 8 j + 7).  The 128x128
-    block scales of quantize_fp8_block are used as they are."""
+    """Row-major e4m3 codes (rows, in) -> (rows/16, in/128, 2048) u8: half
+    h of block (t, kb) at 1024 h holds at 16 (c + 16 q) the 16 codes of row
+    16 t + c, k = 128 kb + 32 q + 16 h + 0..15 in order (lane (c, q)'s MFMA
+    step j takes codes 8 j .. 8 j + 7 of its 32, halves 0 then 1).  The
+    128x128 block scales of quantize_fp8_block are used as they are."""
     q = np.asarray(q, dtype=np.uint8)
     rows, cols = q.shape
-    x = q.reshape(rows // 16, 16, cols // 128, 4, 32)         # t, c, kb, q, byte
-    return np.ascontiguousarray(x.transpose(0, 2, 3, 1, 4).reshape(rows // 16, cols // 128, 2048))
+    x = q.reshape(rows // 16, 16, cols // 128, 4, 2, 16)      # t, c, kb, q, h, byte
+    return np.ascontiguousarray(x.transpose(0, 2, 4, 3, 1, 5).reshape(rows // 16, cols // 128, 2048))
 
 
 def moe_tile_pack_mxfp4(packed, e8):

@@ -92,8 +92,8 @@ def test_fp8_tile_layout_brute_force():
     for r in range(rows):
         for k in range(cols):
             tt, c, kb, kk = r // 16, r % 16, k // 128, k % 128
-            qq, i = kk // 32, kk % 32
-            assert t[tt, kb, 32 * (c + 16 * qq) + i] == q[r, k]
+            qq, h, i = kk // 32, (kk % 32) // 16, kk % 16
+            assert t[tt, kb, 1024 * h + 16 * (c + 16 * qq) + i] == q[r, k]
 
 
 def test_mxfp4_tile_layout_brute_force():
