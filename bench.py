@@ -23,7 +23,7 @@ exceed 2.2x the 256 MB Infinity Cache, so weights stream from HBM; each leg
 records its `cycle_bytes`.  `--warmup W` untimed replays, and at least 30 ms
 of replays, precede each timed region.
 
-CPU baselines (BASELINE.md's plan): the numpy oracle on the host, 3 warm-up
+CPU baselines: the numpy oracle on the host, 3 warm-up
 runs then the median of 20; figure (i) dequantize-then-fp32-matmul per call
 (the reference's CPU semantics), figure (ii) the fp32 matmul on
 pre-dequantized weights (the BLAS floor); CPU model and BLAS build recorded.

@@ -51,7 +51,7 @@ FL_DEV float rtn_scale(float mn, float mx) {
 // -0.0 (rint of a small negative) stays -0.0 like in numpy.
 FL_DEV float clip015(float v) { return v < 0.0f ? 0.0f : (v > 15.0f ? 15.0f : v); }
 
-// ------------------------------------------------------------ A3: int4 group
+// ---------------------------------------------------------------- int4 group
 // q = clip(rint((g - wmin) / scale), 0, 15); even column in the low nibble;
 // scales = scale (fp32), zeros = wmin (fp32).
 __global__ void quantize_int4_group_k(const float* __restrict__ w, uint8_t* __restrict__ packed,
@@ -101,7 +101,7 @@ __global__ void dequantize_int4_group_k(const uint8_t* __restrict__ packed,
     }
 }
 
-// --------------------------------------------- A9: Marlin-style integer zero
+// ------------------------------------------------- Marlin-style integer zero
 // zero = clip(rint(-wmin / scale), 0, 15); q = clip(rint(g / scale) + zero, 0, 15)
 // (moe.py:40-46).  Outputs unpacked q [N, K] u8, scale [N, G] f32, zero [N, G] i32.
 __global__ void quantize_int4_marlin_k(const float* __restrict__ w, uint8_t* __restrict__ q,
@@ -128,7 +128,7 @@ __global__ void quantize_int4_marlin_k(const float* __restrict__ w, uint8_t* __r
     }
 }
 
-// ------------------------------------------------ A13: row-major int4 format
+// ----------------------------------------------------- row-major int4 format
 // zero = clip(rint(-wmin / scale), 0, 15) (fp32); q = clip(rint(g / scale + zero), 0, 15);
 // scales, zeros stored fp16 (moe_int4.py:24-40, batched :97-113).
 __global__ void quantize_int4_rowmajor_k(const float* __restrict__ w, uint8_t* __restrict__ packed,
@@ -181,7 +181,7 @@ __global__ void dequantize_int4_rowmajor_k(const uint8_t* __restrict__ packed,
     }
 }
 
-// ------------------------------------------------------- A4: GPTQ packing
+// ----------------------------------------------------------- GPTQ packing
 // word [k/8, n] = sum_i q[n, 8(k/8) + i] << 4i  (mod 2^32, marlin.py:113-127).
 __global__ void pack_gptq_k(const uint32_t* __restrict__ q, uint32_t* __restrict__ out, int N,
                             int K) {
@@ -198,7 +198,7 @@ __global__ void pack_gptq_k(const uint32_t* __restrict__ q, uint32_t* __restrict
     }
 }
 
-// ----------------------------------------- A5: Marlin scale/zero permutation
+// --------------------------------------------- Marlin scale/zero permutation
 // scales_out[g, c*64 + 8i + j] = fp16(scale[c*64 + 8j + i, g]);
 // zeros_out[g, c*8 + w] = sum_s zero[c*64 + 8*zpi[s] + w, g] << 4s (mod 2^32),
 // zpi = {0,2,4,6,1,3,5,7}  (marlin.py:41-51,138-159).
@@ -230,7 +230,7 @@ __global__ void marlin_scales_zeros_k(const float* __restrict__ scale, const int
     }
 }
 
-// ----------------------------------------------------------- A1: E4M3 codec
+// --------------------------------------------------------------- E4M3 codec
 __global__ void fp8_encode_k(const float* __restrict__ x, uint8_t* __restrict__ out, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (size_t)gridDim.x * blockDim.x)
@@ -242,7 +242,7 @@ __global__ void fp8_decode_k(const uint8_t* __restrict__ b, float* __restrict__ 
         out[i] = e4m3_decode_exact(b[i]);
 }
 
-// --------------------------------------------------- A2: 128x128 block FP8
+// ------------------------------------------------------- 128x128 block FP8
 // One workgroup per (bs x bs) block: amax over the block (zero padding outside
 // the matrix), scale = amax / 448 (1 if amax == 0), q = encode(w / scale)
 // (quantizer.py:65-85).  Scales [ceil(R/bs), ceil(C/bs)] fp32.

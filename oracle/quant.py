@@ -132,7 +132,7 @@ def dequantize_fp8_inline(packed, cols: int):
     return (e4m3_decode(codes) * scale[:, :, None]).reshape(rows, cols)
 
 
-# -------------------------------------------------------------- INT4 (A3 fmt)
+# ------------------------------------------------ INT4 group format (u8 pairs)
 def _groups(w, gs):
     w = np.asarray(w).astype(F32)
     rows, cols = w.shape
@@ -172,7 +172,7 @@ def dequantize_int4_group(packed, scales, zeros, gs: int = 128):
     return (q * s + z).astype(F32)
 
 
-# ------------------------------------------------- INT4 Marlin-style (A9 fmt)
+# -------------------------------------------------- INT4 Marlin-style format
 def quantize_int4_marlin(w, gs: int = 128):
     """(q (N, K) u8, scale (N, G) f32, zero (N, G) int64)
     (fastllm_py/moe.py:40-46): zero = clip(rint(-min/s)), q = clip(rint(w/s) + zero)."""
@@ -237,7 +237,7 @@ def marlin_dequant(q, scales_fp16_perm, zeros_perm, gs: int):
     return deq.reshape(N, K).astype(F32)
 
 
-# --------------------------------------------- INT4 row-major format (A13 fmt)
+# ----------------------------------------------------- INT4 row-major format
 def quantize_int4_rowmajor(w, gs: int = 128):
     """(packed (.., out, in/2) u8, scales f16, zeros f16)
     (fastllm_py/kernels/moe_int4.py:24-40, batched :97-113):

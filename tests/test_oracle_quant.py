@@ -158,10 +158,11 @@ def test_int4_variants_brute_force_tiny():
                 assert (p13[r, c // 2] >> nib) & 0xF == q13
 
 
-def test_int4_variant_disagreement_counts_match_survey():
+def test_int4_variant_disagreement_counts():
     """Config-1 shape, N(0,0.02) seed 0: the three RTN variants disagree on
-    exactly the element counts measured independently when the path was
-    surveyed (A9 vs A13: 2 fp32 / 359 fp16-cast; A3 vs A9: 773,237 / 773,125)."""
+    exactly the element counts measured independently of this oracle
+    (marlin vs rowmajor codes: 2 for fp32 input / 359 for fp16-cast input;
+    group vs marlin codes: 773,237 / 773,125)."""
     rng = np.random.default_rng(0)
     W = (rng.standard_normal((3072, 1024)) * 0.02).astype(np.float32)
     for w, n913, n39 in ((W, 2, 773237), (W.astype(np.float16), 359, 773125)):
