@@ -179,12 +179,19 @@ def current_stream_handle() -> int:
 
 
 def stream_handle(stream) -> int:
-    """torch.cuda.Stream / raw int handle / None (null stream) -> int."""
+    """Launch-stream handle of a torch.cuda.Stream (``.cuda_stream``), a CuPy
+    stream (``.ptr``, what the reference's callers pass), a raw int handle,
+    or None (the null stream) -> int."""
     if stream is None:
         return 0
     if isinstance(stream, int):
         return stream
-    return int(stream.cuda_stream)
+    h = getattr(stream, "cuda_stream", None)
+    if h is None:
+        h = getattr(stream, "ptr", None)
+    if h is None:
+        raise TypeError(f"not a stream: {type(stream).__name__} has neither .cuda_stream nor .ptr")
+    return int(h)
 
 
 def check_out(buf, numel: int, dtypes, device, name: str = "out"):

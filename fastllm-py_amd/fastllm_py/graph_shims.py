@@ -32,7 +32,7 @@ from . import _native as nat
 
 def _stream_of(cp, stream):
     if stream is not None:
-        return int(getattr(stream, "ptr", stream))
+        return nat.stream_handle(stream)
     return int(cp.cuda.get_current_stream().ptr) if cp is not None else nat.current_stream_handle()
 
 

@@ -93,8 +93,12 @@ def fp8_gemv(x_fp16, weight_fp8_block128, scales=None, out=None, k=None):
 
 
 # one zeroed split-K workspace per device for the prefill GEMM, grown as
-# shapes need it (its tile counters are left at zero by every call)
+# shapes need it (its tile counters are left at zero by every call).  A
+# smaller workspace it replaces is kept alive to the end of the process: a
+# launch on a caller's stream, or a captured graph, may still read it, and
+# freeing it would let the caching allocator hand its block to a new tensor.
 _gemm_ws: dict = {}
+_gemm_ws_retired: list = []
 
 
 def _gemm_workspace(M: int, N: int, K: int):
@@ -105,7 +109,11 @@ def _gemm_workspace(M: int, N: int, K: int):
     dev = t.cuda.current_device()
     ws = _gemm_ws.get(dev)
     if ws is None or ws.numel() < need:
-        ws = t.zeros(need, dtype=t.uint8, device="cuda")
+        if ws is not None:
+            _gemm_ws_retired.append(ws)
+        # round up so a run of growing shapes retires few buffers
+        size = 1 << max(20, (need - 1).bit_length())
+        ws = t.zeros(size, dtype=t.uint8, device="cuda")
         _gemm_ws[dev] = ws
     return ws, ws.numel()
 

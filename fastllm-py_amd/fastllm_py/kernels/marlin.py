@@ -48,9 +48,9 @@ def available() -> bool:
 # weight-prep helpers (GPU kernels; reference does these in numpy)
 # --------------------------------------------------------------------------
 def pack_gptq_qweight(q_int4, xp=np):
-    """int4 weight [size_n, size_k] (values 0..15) -> uint32 [size_k//8, size_n].
-
-    Value k at bits 4*(k%8) of word [k//8, n] (marlin.py:113-127)."""
+    """GPTQ packing (marlin.py:113-127): codes q[n, k] in 0..15, shape
+    (size_n, size_k), become a uint32 array of shape (size_k // 8, size_n)
+    whose word [k // 8, n] holds code k in bits 4 * (k % 8)."""
     t = nat.torch()
     size_n, size_k = q_int4.shape
     assert size_k % 8 == 0, "size_k must be a multiple of 8"
@@ -163,14 +163,13 @@ def get_workspace(size_n: int):
 
 def gemm_fast(a_fp16, qweight, scales, zeros, size_n, size_k, stream=None, workspace=None,
               out=None):
-    """Lean GEMV/GEMM for the decode hot path (marlin.py:205-247).
-
-    Trusts that a_fp16 is a contiguous fp16 device tensor and that
-    qweight/scales/zeros were validated at load time.  stream: a
-    torch.cuda.Stream (or raw handle) to launch on through the stream entry;
-    None launches on the null stream.  Like the reference it does not check
-    the entry's return value.  ``out``: an optional preallocated contiguous
-    (M, size_n) fp16 tensor (persistent buffers for graph capture)."""
+    """C[M, size_n] = A @ W^T for the per-token decode loop (marlin.py:205-247),
+    with no argument checks: the caller hands in an fp16 contiguous A and the
+    payload that load-time code already checked, and the entry's return code
+    is ignored, as the reference does.  ``stream`` (torch stream, CuPy stream
+    or raw handle) selects the stream entry; None runs on the null stream.
+    ``out`` may be a preallocated contiguous (M, size_n) fp16 tensor, which
+    graph-captured callers keep across replays."""
     t = nat.torch()
     lib = nat.lib()
     size_m = a_fp16.shape[0]

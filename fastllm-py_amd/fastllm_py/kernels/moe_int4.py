@@ -548,6 +548,17 @@ def moe_route_forward_noalloc(x, logits, stacked, top_k, E, hidden, inter, *, ro
     if T > 16 or x.numel() != T * hidden or logits.numel() != T * E or out.numel() != T * hidden:
         raise ValueError("moe_route_forward_noalloc: x (T, hidden), logits (T, E) and out "
                          "(T, hidden) with T <= 16")
+    # the optional per-token / per-expert vectors reach the kernel as raw
+    # pointers too: same checks, with their lengths
+    for name, v, n in (("shared_logit", shared_logit, T), ("e_score_bias", e_score_bias, E)):
+        if v is None:
+            continue
+        if not isinstance(v, t.Tensor) or v.dtype != t.float32 or not v.is_cuda \
+                or not v.is_contiguous() or v.numel() != n:
+            raise ValueError(f"moe_route_forward_noalloc: {name} must be a contiguous fp32 "
+                             f"device tensor of {n} elements")
+        if v.device != x.device:
+            raise ValueError(f"moe_route_forward_noalloc: {name} must live on {x.device}")
     for k, (shape, dt) in _route_buffer_shapes(T, E, top_k).items():
         if k == "shared_coef" and shared_logit is None:
             continue

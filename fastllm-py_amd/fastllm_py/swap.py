@@ -13,7 +13,12 @@ Callers of the reference hand CuPy arrays to these functions and expect
 CuPy arrays back (``xp=cupy``).  Every swapped function is wrapped so that
 device arrays exposing ``__cuda_array_interface__`` enter as zero-copy torch
 views (in-place ``out=`` buffers included) and device results leave as
-zero-copy CuPy arrays when the call carried CuPy arrays or ``xp=cupy``.
+zero-copy CuPy arrays when the call carried CuPy arrays, a CuPy stream or
+``xp=cupy``.  A CuPy ``stream=`` argument is passed through untouched (the
+library reads its ``.ptr``), and the call runs with torch's current stream
+set to the launch stream (the given one, else CuPy's current stream), so
+outputs are allocated, and default-stream launches ordered, on the stream
+the caller's CuPy work uses.
 
 ``install`` also rebinds copies a reference module took with ``from X import
 name`` before the swap (``moe.py:18`` binds ``route_topk`` that way).
@@ -75,6 +80,18 @@ def load_as(name: str = "fastllm_amd"):
     return mod
 
 
+def _launch_stream(torch, cp, kwargs):
+    """torch stream context for the call: the caller's ``stream=`` (CuPy
+    ``.ptr``, torch ``.cuda_stream`` or int), else CuPy's current stream."""
+    from . import _native as nat
+
+    s = kwargs.get("stream")
+    h = nat.stream_handle(s) if s is not None else int(cp.cuda.get_current_stream().ptr)
+    if h == 0:
+        return torch.cuda.stream(torch.cuda.default_stream())
+    return torch.cuda.stream(torch.cuda.ExternalStream(h))
+
+
 def _cupy_of(v):
     m = type(v).__module__ or ""
     if m.startswith("cupy"):
@@ -117,14 +134,18 @@ def adapt(fn):
             return fn(*args, **kwargs)
         import torch
 
+        from . import _native as nat
+
         def to_torch(x):
-            return torch.as_tensor(x, device="cuda") if _cupy_of(x) is not None else x
+            # device arrays only: a CuPy stream is passed through as it is
+            return torch.as_tensor(x, device="cuda") if nat.is_device_array(x) else x
 
         def to_cupy(x):
             return cp.asarray(x) if isinstance(x, torch.Tensor) and x.is_cuda else x
         if kwargs.get("xp") is cp:
             kwargs["xp"] = torch  # any non-numpy xp: device results
-        r = fn(*_map(list(args), to_torch), **_map(kwargs, to_torch))
+        with _launch_stream(torch, cp, kwargs):
+            r = fn(*_map(list(args), to_torch), **_map(kwargs, to_torch))
         return _map(r, to_cupy)
 
     wrapper.__wrapped_amd__ = fn

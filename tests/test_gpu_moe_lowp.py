@@ -136,41 +136,71 @@ def test_lowp_moe_parity(torch_gpu, fmt, T, E, K, hidden, inter, sinter):
     assert Q.max_abs_rel(y2.cpu().numpy(), ref) < TOL
 
 
+_C4 = {}  # fmt -> (weights, stacks, per-expert oracle dequantization cache)
+
+
+def _config4_layer(torch, fmt):
+    """Qwen1.5-MoE-A2.7B expert weights in `fmt`, built once per format."""
+    from fastllm_py.kernels import moe_int4
+
+    if fmt not in _C4:
+        E, hidden, inter, sinter = 60, 2048, 1408, 5632
+        rng = np.random.default_rng(1400 + (0 if fmt == "fp8" else 1))
+
+        def w(n, o, i):
+            return (rng.standard_normal((n, o, i), dtype=np.float32) * 0.05
+                    ).astype(np.float16).astype(np.float32)
+        Wr = {"gate": w(E, inter, hidden), "up": w(E, inter, hidden), "down": w(E, hidden, inter)}
+        Ws = {"gate": w(1, sinter, hidden), "up": w(1, sinter, hidden), "down": w(1, hidden, sinter)}
+        st = {"group": moe_int4.LOWP_FORMATS[fmt][1], "format": fmt}
+        sh = dict(st)
+        for p in ("gate", "up", "down"):
+            st.update(moe_int4.stack_lowp(fmt, p, Wr[p]))
+            sh.update(moe_int4.stack_lowp(fmt, p, Ws[p]))
+        sdeq = {p: _oracle_deq(fmt, Ws[p]) for p in Ws}
+        torch.cuda.synchronize()
+        _C4[fmt] = (Wr, st, sh, sdeq, {})
+    return _C4[fmt]
+
+
 @pytest.mark.parametrize("fmt", ["fp8", "mxfp4"])
-def test_lowp_moe_config4_shape(torch_gpu, fmt):
+@pytest.mark.parametrize("T", [1, 6, 16])
+def test_lowp_moe_config4_shape(torch_gpu, fmt, T):
     """Qwen1.5-MoE-A2.7B shapes (60 experts, hidden 2048, inter 1408, shared
-    5632), one token: the oracle dequantizes only the routed experts (the
-    blocks of one expert depend on that expert's weights alone)."""
+    5632) at 1, 6 and 16 tokens -- the launch shapes the decode plan picks
+    there (at 16 tokens: four gate/up tiles and two blocks per wave) -- twice
+    in a row: the oracle dequantizes only the routed experts (the blocks of
+    one expert depend on that expert's weights alone)."""
     from fastllm_py.kernels import moe_int4
 
     torch = torch_gpu
     E, K, hidden, inter, sinter = 60, 4, 2048, 1408, 5632
-    rng = np.random.default_rng(1400 + (0 if fmt == "fp8" else 1))
-    Wr = {"gate": _weights(rng, E, inter, hidden), "up": _weights(rng, E, inter, hidden),
-          "down": _weights(rng, E, hidden, inter)}
-    Ws = {"gate": _weights(rng, 1, sinter, hidden), "up": _weights(rng, 1, sinter, hidden),
-          "down": _weights(rng, 1, hidden, sinter)}
-    st = {"group": moe_int4.LOWP_FORMATS[fmt][1], "format": fmt}
-    sh = dict(st)
-    for p in ("gate", "up", "down"):
-        st.update(moe_int4.stack_lowp(fmt, p, Wr[p]))
-        sh.update(moe_int4.stack_lowp(fmt, p, Ws[p]))
-    x = torch.from_numpy((rng.standard_normal((1, hidden)) * 0.5).astype(np.float32)).cuda()
-    logits = torch.from_numpy(rng.standard_normal((1, E)).astype(np.float16).astype(np.float32)).cuda()
-    sl = torch.from_numpy(rng.standard_normal(1).astype(np.float32)).cuda()
-    r = {}
-    y = moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, shared=sh, shared_inter=sinter,
-                                   shared_logit=sl, route=r)
-    torch.cuda.synchronize()
-    ids, w = r["topk_ids"].cpu().numpy(), r["topk_w"].cpu().numpy()
-    used = sorted(set(ids.reshape(-1).tolist()))
-    deq = {p: np.zeros((E,) + Wr[p].shape[1:], np.float32) for p in Wr}
-    for p in Wr:
-        deq[p][used] = _oracle_deq(fmt, Wr[p][used])
-    sdeq = {p: _oracle_deq(fmt, Ws[p]) for p in Ws}
+    Wr, st, sh, sdeq, cache = _config4_layer(torch, fmt)
+    rng = np.random.default_rng(1410 + T + (0 if fmt == "fp8" else 100))
+    x = torch.from_numpy((rng.standard_normal((T, hidden)) * 0.5).astype(np.float32)).cuda()
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float16).astype(np.float32)).cuda()
+    sl = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).cuda()
     coef = 1.0 / (1.0 + np.exp(-sl.cpu().numpy()))
-    ref = OM.moe_ref(x.cpu().numpy(), deq, ids, w, sdeq, coef)
-    assert Q.max_abs_rel(y.cpu().numpy(), ref) < TOL
+    ref = None
+    for call in range(2):
+        r = {}
+        print(f"lowp config4 {fmt} T={T} call {call}", flush=True)
+        y = moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, shared=sh,
+                                       shared_inter=sinter, shared_logit=sl, route=r)
+        torch.cuda.synchronize()
+        if ref is None:
+            ids, w = r["topk_ids"].cpu().numpy(), r["topk_w"].cpu().numpy()
+            deq = {p: np.zeros((E,) + Wr[p].shape[1:], np.float32) for p in Wr}
+            for e in sorted(set(ids.reshape(-1).tolist())):
+                if e not in cache:
+                    cache[e] = {p: _oracle_deq(fmt, Wr[p][e:e + 1])[0] for p in Wr}
+                for p in Wr:
+                    deq[p][e] = cache[e][p]
+            ref = OM.moe_ref(x.cpu().numpy(), deq, ids, w, sdeq, coef)
+        else:
+            np.testing.assert_array_equal(r["topk_ids"].cpu().numpy(), ids)
+        err = Q.max_abs_rel(y.cpu().numpy(), ref)
+        assert err < TOL, (fmt, T, call, err)
 
 
 @pytest.mark.parametrize("fmt", ["fp8", "mxfp4"])

@@ -95,6 +95,57 @@ def test_adapter_round_trips_device_arrays(torch_gpu, fake_cupy):
     np.testing.assert_array_equal(p["qweight"]._t.cpu().numpy(), ref["qweight"])
 
 
+class _FakeStream:
+    """Stand-in for a cupy.cuda.Stream: CuPy streams expose their handle as
+    ``.ptr`` (not ``.cuda_stream``) and live in module cupy.cuda.stream."""
+
+    __module__ = "cupy.cuda.stream"
+
+    def __init__(self, ptr):
+        self.ptr = int(ptr)
+
+
+def test_adapter_passes_cupy_streams(torch_gpu, fake_cupy):
+    """The reference's hot callers pass stream=<cupy Stream> (graph_decode.py:778,
+    batched.py:161, moe.py:152): the adapted gemm_fast and _expert_ffn_marlin
+    launch on that stream and equal the direct calls bit for bit."""
+    from fastllm_py import swap
+    from fastllm_py.kernels import marlin
+    from fastllm_py.moe import _expert_ffn_marlin, build_marlin_expert_payload
+
+    torch = torch_gpu
+    side = torch.cuda.Stream()
+    fs = _FakeStream(side.cuda_stream)
+    N, K = 768, 2048
+    rng = np.random.default_rng(11)
+    w = {"gate": (rng.standard_normal((N, K)) * 0.02).astype(np.float16),
+         "up": (rng.standard_normal((N, K)) * 0.02).astype(np.float16),
+         "down": (rng.standard_normal((K, N)) * 0.02).astype(np.float16)}
+    pay = {k: torch.from_numpy(np.ascontiguousarray(v)).cuda()
+           for k, v in build_marlin_expert_payload(w).items()}
+    for M in (1, 3):
+        x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float16)).cuda()
+        ws = marlin.make_workspace(N)
+        direct = marlin.gemm_fast(x, pay["gate.qweight"], pay["gate.scales"], pay["gate.zeros"],
+                                  N, K, stream=torch.cuda.current_stream(), workspace=ws)
+        ffn = _expert_ffn_marlin(x, pay)
+        torch.cuda.synchronize()
+        fa = {k: _FakeArray(v) for k, v in pay.items()}
+        ws2 = _FakeArray(marlin.make_workspace(N))
+        out = swap.adapt(marlin.gemm_fast)(_FakeArray(x), fa["gate.qweight"], fa["gate.scales"],
+                                           fa["gate.zeros"], N, K, stream=fs, workspace=ws2)
+        out2 = swap.adapt(_expert_ffn_marlin)(_FakeArray(x), fa, stream=fs)
+        # torch tensors in, only the stream from CuPy: results still leave as CuPy arrays
+        out3 = swap.adapt(marlin.gemm_fast)(x, pay["gate.qweight"], pay["gate.scales"],
+                                            pay["gate.zeros"], N, K, stream=fs,
+                                            workspace=marlin.make_workspace(N))
+        side.synchronize()
+        assert isinstance(out, _FakeArray) and isinstance(out2, _FakeArray)
+        assert isinstance(out3, _FakeArray)
+        assert torch.equal(out._t, direct) and torch.equal(out3._t, direct)
+        assert torch.equal(out2._t, ffn)
+
+
 def test_graph_shims_match_library_paths(torch_gpu, fake_cupy):
     from fastllm_py import graph_shims
     from fastllm_py.expert_router import route_topk_device

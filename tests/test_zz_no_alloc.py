@@ -92,3 +92,33 @@ def test_noalloc_refuses_oversized_workspace(torch_gpu):
         moe_int4.moe_route_forward_noalloc(x, logits, st, K, E, hidden, inter, route=r, out=y,
                                            shared=sh, shared_inter=sinter)
     torch.cuda.synchronize()
+
+
+def test_noalloc_refuses_wrongly_typed_vectors(torch_gpu):
+    """shared_logit (T,) and e_score_bias (E,) reach the kernel as raw
+    pointers: a host tensor, an fp16 tensor or a wrong length is a
+    ValueError before any launch."""
+    from fastllm_py.kernels import moe_int4
+
+    torch = torch_gpu
+    T, E, K, hidden, inter, sinter = 2, 64, 4, 256, 256, 512
+    rng = np.random.default_rng(2)
+    st = moe_int4.build_stacked_experts(_experts(rng, E, hidden, inter), 128)
+    sh = moe_int4.build_stacked_experts(_experts(rng, 1, hidden, sinter), 128)
+    x = torch.zeros((T, hidden), dtype=torch.float32, device="cuda")
+    logits = torch.zeros((T, E), dtype=torch.float32, device="cuda")
+    y = torch.empty_like(x)
+    r = moe_int4.alloc_route_buffers(T, E, K)
+    bad = {"shared_logit": (torch.zeros(T), torch.zeros(T, device="cuda").half(),
+                            torch.zeros(T + 1, device="cuda")),
+           "e_score_bias": (torch.zeros(E), torch.zeros(E, device="cuda").half(),
+                            torch.zeros(E - 1, device="cuda"))}
+    for name, vals in bad.items():
+        for v in vals:
+            kw = {name: v}
+            if name == "e_score_bias":
+                kw["scoring"] = "sigmoid"
+            with pytest.raises(ValueError, match=name):
+                moe_int4.moe_route_forward_noalloc(x, logits, st, K, E, hidden, inter, route=r,
+                                                   out=y, shared=sh, shared_inter=sinter, **kw)
+    torch.cuda.synchronize()
