@@ -13,8 +13,17 @@ Also measured (same JSON line, "breakdown"): M in {1,4,8,16}; FP8-E4M3
 (configs[3]) in us/layer and against its routed-weight-bytes roofline.
 
 Also: config 1 (the INT4 GEMV on quantize_int4_group's format, 3072x1024),
-the row-major INT4 GEMV (dgemv) at the Qwen3-8B shapes, and the prefill
-GEMMs of config 5.
+the row-major INT4 GEMV (dgemv) at the Qwen3-8B shapes, the reference ABI's
+own FP8 GEMV (inline 1x128 format, fastllm_fp8_block128_gemv_fp16), the
+decode MoE at the Qwen3-30B-A3B shape of the reference's one published
+fused-MoE latency, the prefill GEMMs of config 5, and a streaming-read probe
+(fastllm_hbm_read_probe) at every decode GEMV's byte count -- the per-launch
+floor each GEMV is reported against.
+
+The timed region of the headline is exactly --steps layer-steps (four GEMV
+launches each, step i on weight copy i mod the copy count), one replay of a
+HIP graph holding them; the per-GEMV figures come from graphs of >= 96
+launches of one GEMV each.
 
 Every figure is timed with HIP events around HIP-graph replays on the launch
 stream.  Each graph cycles through enough weight copies (and, for the MoE,
@@ -50,6 +59,10 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE / WRITE_SIZE (x2.000 / x1.000 copy-kernel calibration); see
 # profiles/int4_gemv_gate_up_qwen3_8b_m1_traffic.md.  Keyed by (kernel, M).
 MEASURED_TRAFFIC = {("int4_gemv_nb<2,4,false,0>", 1): 52_495_211}
+# Average duration of the roofline kernel in the committed rocprofv3 kernel
+# trace of this bench (profiles/bench_kernel_trace_full.md), beside the
+# graph-timed figure the line computes live.  Keyed by (kernel, M).
+ROCPROF_US = {("int4_gemv_nb<2,4,false,0>", 1): (11.36, "profiles/bench_kernel_trace_full.md")}
 QWEN3_8B = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096),
             ("down", 4096, 12288)]
 FP8_SHAPES = [("2048x2048", 2048, 2048), ("10944x2048", 10944, 2048), ("2048x10944", 2048, 10944)]
@@ -164,20 +177,18 @@ def run_int4(torch, lib, layers, M, steps, stream):
         return go
 
     L = len(layers)
-    rounds = max(1, -(-24 // L))
-    seq = [launcher(layers[c], n, N, K) for _ in range(rounds) for c in range(L)
-           for n, N, K in QWEN3_8B]
-    per_graph = rounds * L
-    reps = max(2, -(-steps // per_graph))
-    ms_step = graph_time(torch, stream, seq, reps) / per_graph
+    # the timed region: exactly `steps` layer-steps (step i on layer copy
+    # i mod L), one replay of a graph that holds them
+    seq = [launcher(layers[i % L], n, N, K) for i in range(steps) for n, N, K in QWEN3_8B]
+    ms_step = graph_time(torch, stream, seq, 1) / steps
     per = {}
     r1 = max(1, -(-96 // L))
     for name, N, K in QWEN3_8B:
         seq1 = [launcher(layers[c], name, N, K) for _ in range(r1) for c in range(L)]
-        per[name] = graph_time(torch, stream, seq1, max(2, reps // 4)) / (r1 * L) * 1e3
+        per[name] = graph_time(torch, stream, seq1, 4) / (r1 * L) * 1e3
     cyc = {name: cycle(L * marlin_bytes(0, N, K)) for name, N, K in QWEN3_8B}
-    cyc["layer"] = cycle(L * sum(marlin_bytes(0, N, K) for _, N, K in QWEN3_8B))
-    return ms_step, per, reps * per_graph, cyc
+    cyc["layer"] = cycle(min(steps, L) * sum(marlin_bytes(0, N, K) for _, N, K in QWEN3_8B))
+    return ms_step, per, steps, cyc
 
 
 def run_swiglu(torch, lib, layers, stream, M_list=(1, 8)):
@@ -446,7 +457,111 @@ def run_fp8_prefill(torch, lib, stream, M=512):
     return res
 
 
+def run_fp8_inline(torch, lib, stream, M_list=(1, 8), shapes=(("2048x2048", 2048, 2048),
+                                                               ("10944x2048", 10944, 2048))):
+    """The reference ABI's own FP8 GEMV, fastllm_fp8_block128_gemv_fp16
+    (native/fastllm_fp8_block128.cu:273-287): the inline 1x128 format (per row
+    [128 e4m3][fp32 scale] x K/128, quantized by fastllm_fp8_block128_quantize),
+    fp16 activations, at the configs[2] shapes the format takes (K % 128 == 0).
+    Launched through its stream entry, which runs the same kernels, so it can
+    be graph-timed (the reference's entry synchronizes after every call)."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3100)
+    res = {}
+    for name, N, K in shapes:
+        W = (torch.randn((N, K), generator=gen, device="cuda") * 0.02).half()
+        per = lib.fastllm_fp8_block128_packed_row_bytes(K)
+        q = torch.empty((N, per), dtype=torch.uint8, device="cuda")
+        h0 = torch.cuda.current_stream().cuda_stream
+        if lib.fastllm_fp8_block128_quantize_stream(W.data_ptr(), q.data_ptr(), N, K, 0, h0):
+            raise RuntimeError("fp8 inline quantize failed")
+        del W
+        n = copies_for(N * per)
+        cps = [q] + [q.clone() for _ in range(n - 1)]
+        for M in M_list:
+            x = torch.randn((M, K), generator=gen, device="cuda").half()
+            y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+            f = lib.fastllm_fp8_block128_gemv_stream
+
+            def mk(w, x=x, y=y, M=M):
+                def go(h):
+                    if f(x.data_ptr(), w.data_ptr(), y.data_ptr(), None, M, K, N, per, 0, h):
+                        raise RuntimeError("fp8 inline gemv failed")
+                return go
+            rounds = max(1, -(-96 // n))
+            seq = [mk(w) for _ in range(rounds) for w in cps]
+            us = graph_time(torch, stream, seq, 4) / len(seq) * 1e3
+            nb = N * per + M * K * 2 + M * N * 2
+            res[f"{name}/M{M}"] = {"us_per_call": round(us, 3), "GB/s": round(nb / us / 1e3, 1),
+                                   "pct_of_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS * 100, 2),
+                                   "bytes": nb, **cycle(n * N * per)}
+        del cps, q
+        torch.cuda.empty_cache()
+    return res
+
+
+def run_stream_probe(torch, lib, stream, sizes):
+    """Per-launch floor of a streaming read of each byte count: the library's
+    HBM read probe (fastllm_hbm_read_probe: every wave load a contiguous 1 KB,
+    non-temporal, all loads issued before the first use, nothing computed or
+    stored), graph-timed like the GEMVs, each launch at its own offset of a
+    buffer larger than 2.2x the MALL so every launch reads HBM.  Best of 4, 8
+    and 16 loads per lane.  `sizes`: name -> bytes."""
+    big = max(sizes.values())
+    stride_of = {k: -(-v // 4096) * 4096 for k, v in sizes.items()}
+    buf_bytes = max(ROTATE_BYTES + big, 2 * big) + 4096
+    buf = torch.empty(buf_bytes, dtype=torch.uint8, device="cuda")
+    buf.random_(0, 256)
+    sink = torch.zeros(1024, dtype=torch.int32, device="cuda")
+    base = buf.data_ptr()
+    res = {}
+    for name, nb in sizes.items():
+        nb16 = -(-nb // 16) * 16
+        st = stride_of[name]
+        slots = max(1, (buf_bytes - nb16) // st + 1)
+        n = min(slots, max(copies_for(nb16), 2))
+        offs = [i * st for i in range(n)]
+        best = None
+        for nl in (4, 8, 16):
+            def mk(off, nl=nl):
+                def go(h):
+                    if lib.fastllm_hbm_read_probe(base + off, nb16, sink.data_ptr(), nl, h):
+                        raise RuntimeError("hbm read probe failed")
+                return go
+            rounds = max(1, -(-96 // n))
+            seq = [mk(o) for _ in range(rounds) for o in offs]
+            us = graph_time(torch, stream, seq, 4) / len(seq) * 1e3
+            if best is None or us < best[0]:
+                best = (us, nl)
+        # the same reads ending in one dependent store per workgroup (as a
+        # GEMV's workgroups end): the part of a GEMV's gap that any kernel
+        # with outputs pays
+        nl = best[1]
+        seq = [(lambda off: (lambda h: lib.fastllm_hbm_read_probe(base + off, nb16, sink.data_ptr(),
+                                                                   nl | 64, h)))(o)
+               for _ in range(max(1, -(-96 // n))) for o in offs]
+        us_st = graph_time(torch, stream, seq, 4) / len(seq) * 1e3
+        res[name] = {"bytes": int(nb16), "us_per_launch": round(best[0], 3),
+                     "GB/s": round(nb16 / best[0] / 1e3, 1),
+                     "pct_of_hbm_peak": round(nb16 / best[0] / 1e3 / HBM_PEAK_GBS * 100, 2),
+                     "loads_per_lane": best[1], "us_per_launch_with_store": round(us_st, 3),
+                     **cycle(n * nb16)}
+    del buf, sink
+    torch.cuda.empty_cache()
+    return res
+
+
 # ------------------------------------------------------------------- MoE
+# Decode MoE layers: Qwen1.5-MoE-A2.7B (BASELINE configs[3]) and the
+# Qwen3-30B-A3B layer of the reference's only published fused-MoE latency
+# (fused_moe_weighted, 36 us/layer at M=1 on an RTX 5090,
+# fastllm_py/kernels/moe_int4.py:179).
+MOE_SHAPES = {
+    "qwen15_a27b": {"E": 60, "hidden": 2048, "inter": 1408, "sinter": 5632, "K": 4, "norm": False},
+    "qwen3_30b_a3b": {"E": 128, "hidden": 2048, "inter": 768, "sinter": 0, "K": 8, "norm": True},
+}
+
+
 def moe_weight_bytes(fmt, out_f, in_f):
     """Packed bytes of one (out, in) expert matrix: INT4 g128 (nibbles + fp16
     scale and zero per group), FP8 (codes + fp32 per 128x128 block), MXFP4
@@ -456,18 +571,20 @@ def moe_weight_bytes(fmt, out_f, in_f):
             "mxfp4": n // 2 + n // 32}[fmt]
 
 
-def run_moe(torch, lib, stream, T_list=(1, 16), fmt="int4"):
-    """Fused Qwen1.5-MoE-A2.7B layer with `fmt` expert weights (INT4 g128,
-    FP8 128x128-block e4m3 or MXFP4): router from fp16 logits ~ N(0,1)
-    (top-4 softmax, no renorm) + routed experts + shared expert (sigmoid gate).
-    Timed unit = one layer: router + gate/up + down launches
-    (moe_route_forward)."""
+def run_moe(torch, lib, stream, T_list=(1, 16), fmt="int4", shape="qwen15_a27b"):
+    """Fused decode MoE layer with `fmt` expert weights (INT4 g128, FP8
+    128x128-block e4m3 or MXFP4) at MOE_SHAPES[shape]: router from fp16
+    logits ~ N(0,1) (top-K softmax; Qwen1.5: no renorm, plus the shared
+    expert with its sigmoid gate; Qwen3-30B-A3B: renormalised top-8, no shared
+    expert) + routed experts.  Timed unit = one layer: every launch of
+    moe_route_forward (router, gate/up, down)."""
     from fastllm_py.expert_router import route_topk_device
     from fastllm_py.kernels import moe_int4
 
-    E, hidden, inter, sinter, K = 60, 2048, 1408, 5632, 4
+    sp = MOE_SHAPES[shape]
+    E, hidden, inter, sinter, K, norm = (sp[k] for k in ("E", "hidden", "inter", "sinter", "K", "norm"))
     gen = torch.Generator(device="cuda")
-    gen.manual_seed(4000)
+    gen.manual_seed(4000 if shape == "qwen15_a27b" else 4100)
 
     def stacked(d, proj, n, out_f, in_f):
         w = (torch.randn((n, out_f, in_f), generator=gen, device="cuda") * 0.02).half()
@@ -480,14 +597,16 @@ def run_moe(torch, lib, stream, T_list=(1, 16), fmt="int4"):
     def layer():
         meta = {"group": 128} if fmt == "int4" else {"group": moe_int4.LOWP_FORMATS[fmt][1],
                                                      "format": fmt}
-        st, sh = dict(meta), dict(meta)
+        st, sh = dict(meta), (dict(meta) if sinter else None)
         for d, n, inn in ((st, E, inter), (sh, 1, sinter)):
+            if d is None:
+                continue
             for proj, (o, i) in (("gate", (inn, hidden)), ("up", (inn, hidden)),
                                  ("down", (hidden, inn))):
                 stacked(d, proj, n, o, i)
         return st, sh
     expert_bytes = 3 * moe_weight_bytes(fmt, inter, hidden)
-    shared_bytes = 3 * moe_weight_bytes(fmt, sinter, hidden)
+    shared_bytes = 3 * moe_weight_bytes(fmt, sinter, hidden) if sinter else 0
     # layer copies: one token's routed set + the shared expert, over 2.2x MALL
     nl = copies_for(K * expert_bytes + shared_bytes)
     layers = [layer() for _ in range(nl)]
@@ -499,11 +618,12 @@ def run_moe(torch, lib, stream, T_list=(1, 16), fmt="int4"):
         n_ent = rounds * nl
         logits = torch.randn((n_ent, T, E), generator=gen, device="cuda").half().float()
         xs = torch.randn((n_ent, T, hidden), generator=gen, device="cuda").half().float()
-        slog = torch.randn((n_ent, T), generator=gen, device="cuda")
+        slog = torch.randn((n_ent, T), generator=gen, device="cuda") if sinter else None
         bufs = {}
         touched, per_layer = set(), []
         for i in range(n_ent):
-            route_topk_device(logits[i], K, shared_logit=slog[i], out=bufs)
+            route_topk_device(logits[i], K, norm_topk_prob=norm,
+                              shared_logit=slog[i] if sinter else None, out=bufs)
             ids = np.unique(bufs["topk_ids"].cpu().numpy())
             per_layer.append(len(ids) * expert_bytes + shared_bytes)
             touched.update((i % nl, int(e)) for e in ids)
@@ -513,8 +633,9 @@ def run_moe(torch, lib, stream, T_list=(1, 16), fmt="int4"):
 
         def mk(i, st, sh, bufs=bufs, y=y, ws=ws, T=T):
             def go(h):
-                moe_int4.moe_route_forward(xs[i], logits[i], st, K, E, hidden, inter, shared=sh,
-                                           shared_inter=sinter, shared_logit=slog[i], route=bufs,
+                moe_int4.moe_route_forward(xs[i], logits[i], st, K, E, hidden, inter,
+                                           norm_topk_prob=norm, shared=sh, shared_inter=sinter,
+                                           shared_logit=slog[i] if sinter else None, route=bufs,
                                            out=y, workspace=ws, stream=h)
             return go
         seq = [mk(i, *layers[i % nl]) for i in range(n_ent)]
@@ -847,7 +968,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--only", default="int4,swiglu,layer,group,rm,fp8,fp8p,moe,moelp,gemm,moelpp")
+    ap.add_argument("--only", default="int4,swiglu,layer,probe,group,rm,fp8,fp8i,fp8p,moe,moelp,"
+                                      "moe30,gemm,moelpp")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy a 64 MiB buffer 5 times (a known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -929,6 +1051,9 @@ def main():
     if "fp8p" in only:
         breakdown["fp8_prefill_gemm_M512"] = run_fp8_prefill(torch, lib, stream)
         log(f"FP8 prefill: {breakdown['fp8_prefill_gemm_M512']}")
+    if "fp8i" in only:
+        breakdown["fp8_inline_1x128_abi_fp16"] = run_fp8_inline(torch, lib, stream)
+        log(f"FP8 inline ABI: {breakdown['fp8_inline_1x128_abi_fp16']}")
     if "moe" in only:
         breakdown["moe_qwen15_a27b_int4"] = run_moe(torch, lib, stream)
         log(f"MoE: {breakdown['moe_qwen15_a27b_int4']}")
@@ -936,6 +1061,46 @@ def main():
         for fmt in ("fp8", "mxfp4"):
             breakdown[f"moe_qwen15_a27b_{fmt}"] = run_moe(torch, lib, stream, fmt=fmt)
             log(f"MoE {fmt}: {breakdown[f'moe_qwen15_a27b_{fmt}']}")
+    if "moe30" in only:
+        for fmt in ("int4", "fp8", "mxfp4"):
+            key = f"moe_decode_qwen3_30b_a3b_{fmt}"
+            breakdown[key] = run_moe(torch, lib, stream, T_list=(1,), fmt=fmt, shape="qwen3_30b_a3b")
+            breakdown[key]["reference_published"] = {
+                "us_per_layer": 36.0, "hardware": "RTX 5090", "kernel": "fused_moe_weighted, INT4 g128",
+                "source": "fastllm_py/kernels/moe_int4.py:179"}
+            log(f"MoE decode Qwen3-30B-A3B {fmt}: {breakdown[key]}")
+    if "probe" in only:
+        # the streaming-read floor at each decode GEMV's byte count, and the
+        # GEMVs as a fraction of it
+        sizes = {f"int4_{n}_M1": marlin_bytes(1, N, K) for n, N, K in QWEN3_8B}
+        sizes.update({f"fp8_{n}_M1": fp8_block_bytes(1, N, K) for n, N, K in FP8_SHAPES})
+        sizes["peak_512MiB"] = 512 * 2 ** 20
+        pr = run_stream_probe(torch, lib, stream, sizes)
+        if 1 in per_m:
+            for n, N, K in QWEN3_8B:
+                g = per_m[1]["us_per_call"][n]
+                pr[f"int4_{n}_M1"]["gemv_us"] = round(g, 3)
+                pr[f"int4_{n}_M1"]["gemv_pct_of_probe"] = round(pr[f"int4_{n}_M1"]["us_per_launch"] / g * 100, 1)
+                pr[f"int4_{n}_M1"]["gemv_minus_probe_us"] = round(g - pr[f"int4_{n}_M1"]["us_per_launch"], 3)
+                pr[f"int4_{n}_M1"]["gemv_minus_probe_with_store_us"] = round(
+                    g - pr[f"int4_{n}_M1"]["us_per_launch_with_store"], 3)
+            lay = sum(pr[f"int4_{n}_M1"]["us_per_launch"] for n, _, _ in QWEN3_8B)
+            pr["int4_layer_M1"] = {"probe_us": round(lay, 3),
+                                   "probe_pct_of_hbm_peak": round(
+                                       sum(marlin_bytes(1, N, K) for _, N, K in QWEN3_8B) / lay / 1e3
+                                       / HBM_PEAK_GBS * 100, 2),
+                                   "gemv_us": round(per_m[1]["ms_per_layer"] * 1e3, 3),
+                                   "gemv_pct_of_probe": round(lay / (per_m[1]["ms_per_layer"] * 1e3) * 100, 1)}
+        if "fp8_b128x128_bf16" in breakdown:
+            for n, N, K in FP8_SHAPES:
+                g = breakdown["fp8_b128x128_bf16"][f"{n}/M1"]["us_per_call"]
+                pr[f"fp8_{n}_M1"]["gemv_us"] = g
+                pr[f"fp8_{n}_M1"]["gemv_pct_of_probe"] = round(pr[f"fp8_{n}_M1"]["us_per_launch"] / g * 100, 1)
+                pr[f"fp8_{n}_M1"]["gemv_minus_probe_us"] = round(g - pr[f"fp8_{n}_M1"]["us_per_launch"], 3)
+                pr[f"fp8_{n}_M1"]["gemv_minus_probe_with_store_us"] = round(
+                    g - pr[f"fp8_{n}_M1"]["us_per_launch_with_store"], 3)
+        breakdown["hbm_read_probe"] = pr
+        log(f"HBM read probe: {pr}")
 
     head = per_m[ms_list[0]]
     M0 = ms_list[0]
@@ -949,7 +1114,18 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": MEASURED_TRAFFIC.get((kname, M0)),
                 "kernel": f"{kname} (gate_up 24576x4096, M={M0})",
-                "bytes_per_launch": int(bpl), "us_per_launch": round(dur_us, 3)}
+                "bytes_per_launch": int(bpl), "us_per_launch": round(dur_us, 3),
+                "us_per_launch_source": "HIP events around graph replays of >= 96 launches on "
+                                        "the launch stream (this run)"}
+    rp = ROCPROF_US.get((kname, M0))
+    if rp is not None:
+        roofline["us_per_launch_rocprof"] = rp[0]
+        roofline["frac_rocprof"] = round(bpl / (rp[0] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+        roofline["rocprof_summary"] = rp[1]
+    if "hbm_read_probe" in breakdown and M0 == 1:
+        pg = breakdown["hbm_read_probe"]["int4_gate_up_M1"]
+        roofline["stream_probe_us"] = pg["us_per_launch"]
+        roofline["frac_of_stream_probe"] = round(pg["us_per_launch"] / dur_us, 4)
 
     cpu = None
     if not args.no_cpu_baseline:

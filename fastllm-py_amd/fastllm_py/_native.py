@@ -74,6 +74,8 @@ SIGNATURES: dict[str, tuple] = {
     "fastllm_moe_int4_routed_noalloc": (_I, [_P, _I, _I, _I, _F, _P, _I, _I, _P] + [_P] * 9 +
                                         [_P, _I, _I, _I, _I, _I] + [_P] * 6 + [_I] + [_P] * 6 +
                                         [_P, _P]),
+    # measurement
+    "fastllm_hbm_read_probe": (_I, [_P, _SZ, _P, _I, _P]),
     "fastllm_quantize_mxfp4": (_I, [_P, _P, _P, ctypes.c_long, _I, _P]),
     "fastllm_dequantize_mxfp4": (_I, [_P, _P, _P, ctypes.c_long, _I, _P]),
     "fastllm_moe_fp8_tile_repack": (_I, [_P, _P, ctypes.c_long, _I, _P]),

@@ -618,6 +618,24 @@ int fastllm_moe_int4_routed_noalloc(const float *logits, int top_k, int scoring,
                                     const uint8_t *sdq, const uint32_t *sdsz,
                                     float *y, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Measurement
+ * ------------------------------------------------------------------------ */
+
+/* HBM streaming-read probe: reads `bytes` (a multiple of 16) from `src`
+ * (16-byte aligned) with the decode GEMVs' access shape (contiguous 1 KB per
+ * wave load, non-temporal), `loads_per_lane` (4, 8 or 16) loads per lane all
+ * in flight, and writes nothing (sink: 1024 words, written only if the
+ * folded data equals a fixed constant).  Its per-launch time at a GEMV's
+ * byte count is the floor that GEMV's launch can reach.  loads_per_lane + 64:
+ * every wave also stores one word once its loads have landed (the dependent
+ * store a GEMV ends with).  0 ok, 1 bad arguments, 2 device /
+ * launch error.
+ * No counterpart in the reference: bench.py's calibration of the GEMV
+ * figures against the device's own streaming rate. */
+int fastllm_hbm_read_probe(const void *src, size_t bytes, uint32_t *sink,
+                           int loads_per_lane, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
