@@ -571,13 +571,14 @@ def moe_weight_bytes(fmt, out_f, in_f):
             "mxfp4": n // 2 + n // 32}[fmt]
 
 
-def run_moe(torch, lib, stream, T_list=(1, 16), fmt="int4", shape="qwen15_a27b"):
+def run_moe(torch, lib, stream, T_list=(1, 16), fmt="int4", shape="qwen15_a27b", deterministic=False):
     """Fused decode MoE layer with `fmt` expert weights (INT4 g128, FP8
     128x128-block e4m3 or MXFP4) at MOE_SHAPES[shape]: router from fp16
     logits ~ N(0,1) (top-K softmax; Qwen1.5: no renorm, plus the shared
     expert with its sigmoid gate; Qwen3-30B-A3B: renormalised top-8, no shared
     expert) + routed experts.  Timed unit = one layer: every launch of
-    moe_route_forward (router, gate/up, down)."""
+    moe_route_forward (router, gate/up, down; with ``deterministic`` also
+    the ordered combine)."""
     from fastllm_py.expert_router import route_topk_device
     from fastllm_py.kernels import moe_int4
 
@@ -628,7 +629,8 @@ def run_moe(torch, lib, stream, T_list=(1, 16), fmt="int4", shape="qwen15_a27b")
             per_layer.append(len(ids) * expert_bytes + shared_bytes)
             touched.update((i % nl, int(e)) for e in ids)
         y = torch.empty((T, hidden), device="cuda")
-        ws = torch.empty((moe_int4.moe_workspace_bytes(T, hidden, inter, sinter, T * K),),
+        ws = torch.empty((moe_int4.moe_workspace_bytes(T, hidden, inter, sinter, T * K,
+                                                       deterministic),),
                          dtype=torch.uint8, device="cuda")
 
         def mk(i, st, sh, bufs=bufs, y=y, ws=ws, T=T):
@@ -636,7 +638,8 @@ def run_moe(torch, lib, stream, T_list=(1, 16), fmt="int4", shape="qwen15_a27b")
                 moe_int4.moe_route_forward(xs[i], logits[i], st, K, E, hidden, inter,
                                            norm_topk_prob=norm, shared=sh, shared_inter=sinter,
                                            shared_logit=slog[i] if sinter else None, route=bufs,
-                                           out=y, workspace=ws, stream=h)
+                                           out=y, workspace=ws, stream=h,
+                                           deterministic=deterministic)
             return go
         seq = [mk(i, *layers[i % nl]) for i in range(n_ent)]
         us = graph_time(torch, stream, seq, 4) / len(seq) * 1e3
@@ -694,7 +697,7 @@ def run_gemm_prefill(torch, lib, stream, M=512, N=8192, K=2048):
             **cycle(n * marlin_bytes(0, N, K))}
 
 
-def run_moe_prefill(torch, lib, stream, T=512, fmt="int4"):
+def run_moe_prefill(torch, lib, stream, T=512, fmt="int4", deterministic=False):
     """Config 5's grouped MoE layer (Qwen3-30B-A3B): 128 experts, hidden 2048,
     inter 768, top-8 softmax with renormalisation from fp16 logits ~ N(0,1),
     M=512 tokens, `fmt` expert weights.  Timed unit = one layer: route +
@@ -730,14 +733,14 @@ def run_moe_prefill(torch, lib, stream, T=512, fmt="int4"):
     torch.cuda.synchronize()
     distinct = len(np.unique(bufs["topk_ids"].cpu().numpy()))
     y = torch.empty((T, hidden), device="cuda")
-    ws = torch.empty((moe_int4.moe_workspace_bytes(T, hidden, inter, 0, T * K),),
+    ws = torch.empty((moe_int4.moe_workspace_bytes(T, hidden, inter, 0, T * K, deterministic),),
                      dtype=torch.uint8, device="cuda")
 
     def mk(st):
         def go(h):
             route_topk_device(logits, K, norm_topk_prob=True, out=bufs, stream=h)
             moe_int4.moe_forward(x, st, E, hidden, inter, bufs, max_slots=E, max_entries=T * K,
-                                 out=y, workspace=ws, stream=h)
+                                 out=y, workspace=ws, stream=h, deterministic=deterministic)
         return go
     rounds = max(1, -(-16 // nl))
     seq = [mk(st) for _ in range(rounds) for st in layers]
@@ -969,7 +972,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ms", default="1,4,8,16")
     ap.add_argument("--only", default="int4,swiglu,layer,probe,group,rm,fp8,fp8i,fp8p,moe,moelp,"
-                                      "moe30,gemm,moelpp")
+                                      "moe30,moedet,gemm,moelpp")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy a 64 MiB buffer 5 times (a known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -1061,6 +1064,14 @@ def main():
         for fmt in ("fp8", "mxfp4"):
             breakdown[f"moe_qwen15_a27b_{fmt}"] = run_moe(torch, lib, stream, fmt=fmt)
             log(f"MoE {fmt}: {breakdown[f'moe_qwen15_a27b_{fmt}']}")
+    if "moedet" in only:
+        # the ordered (bit-reproducible) combine, beside the atomic legs above
+        key = "moe_qwen15_a27b_int4_deterministic"
+        breakdown[key] = run_moe(torch, lib, stream, deterministic=True)
+        log(f"MoE deterministic: {breakdown[key]}")
+        key = "moe_prefill_qwen3_30b_a3b_int4_deterministic"
+        breakdown[key] = run_moe_prefill(torch, lib, stream, deterministic=True)
+        log(f"MoE prefill deterministic: {breakdown[key]}")
     if "moe30" in only:
         for fmt in ("int4", "fp8", "mxfp4"):
             key = f"moe_decode_qwen3_30b_a3b_{fmt}"

@@ -21,6 +21,17 @@ namespace {
 
 constexpr int kProbeThreads = 256;
 
+// XOR of x over the wave: DPP exchanges within each 16-lane row (quad
+// pairs, quads, half-rows), then the four row results read by lane.
+FL_DEV uint32_t wave_xor(uint32_t x) {
+    x ^= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+    x ^= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false);   // quad_perm 2,3,0,1
+    x ^= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    x ^= (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xF, 0xF, false);  // row_mirror
+    return (uint32_t)(__builtin_amdgcn_readlane((int)x, 0) ^ __builtin_amdgcn_readlane((int)x, 16) ^
+                      __builtin_amdgcn_readlane((int)x, 32) ^ __builtin_amdgcn_readlane((int)x, 48));
+}
+
 template <int NL, bool STORE>
 __global__ __launch_bounds__(kProbeThreads) void hbm_read_k(const u32x4* __restrict__ src, size_t n16,
                                                              uint32_t* __restrict__ sink) {
@@ -35,9 +46,15 @@ __global__ __launch_bounds__(kProbeThreads) void hbm_read_k(const u32x4* __restr
     uint32_t x = 0;
 #pragma unroll
     for (int r = 0; r < NL; ++r) x ^= v[r][0] ^ v[r][1] ^ v[r][2] ^ v[r][3];
-    // STORE: lane 0 of every wave writes its value once the wave's loads
-    // have landed (vector stores)
-    if (STORE ? (threadIdx.x & 63) == 0 : x == 0x9E3779B9u) sink[(blockIdx.x * 4 + (threadIdx.x >> 6)) & 1023] = x;
+    if (STORE) {
+        // every lane's loads feed the stored value (folded over the wave
+        // first: a value of lane 0 alone would let the compiler drop the
+        // other lanes' loads), written by lane 0 once the loads have landed
+        x = wave_xor(x);
+        if ((threadIdx.x & 63) == 0) sink[(blockIdx.x * 4 + (threadIdx.x >> 6)) & 1023] = x;
+    } else if (x == 0x9E3779B9u) {
+        sink[blockIdx.x & 1023] = x;
+    }
 }
 
 template <int NL>

@@ -1479,6 +1479,9 @@ struct MoeExperts {
 // Both low-precision codes become fp16 exactly (scale-1 conversions); the
 // block scale multiplies the fp32 MFMA result.
 constexpr int kFmtInt4 = 0, kFmtFp8 = 1, kFmtMx4 = 2;
+// Call flags of the fused MoE entries
+constexpr int kMoeDeterministic = 1;  // ordered combine: bit-identical repeats
+constexpr int kMoeFlags = kMoeDeterministic;
 
 template <int FMT>
 struct WBlk {  // one lane's share of a tile block
@@ -1593,6 +1596,12 @@ struct MoeArgs {
     int fuse_route;
     RouteArgs ra;
     int fmt;  // weight format of both expert stacks (kFmt*)
+    // deterministic combine: the down projections store their terms into
+    // `part` (rows [0, max_entries): list entry p; row max_entries + q T + t:
+    // shared-expert piece q of token t) and moe_combine_k sums them per
+    // token in one fixed order, instead of fp32 atomics into y
+    int det, nq;
+    float* part;
 };
 
 // Fused routing of the one token (T == 1) in a routed gate/up workgroup:
@@ -1923,9 +1932,53 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
         __builtin_amdgcn_sched_barrier(0);
     }
     float* red = reinterpret_cast<float*>(smem);
-    reduce_and_store<TRD>(red, acc, M, wave, nwaves, lane, [&](int m, int t, int c, float v) {
-        unsafeAtomicAdd(&a.y[(size_t)toks[m] * a.hidden + o0 + 16 * t + c], v);
-    });
+    if (a.det) {
+        float* dst = a.part + (size_t)(is_shared ? a.max_entries + (y_slot - a.max_slots) * a.T : row0) * a.hidden + o0;
+        reduce_and_store<TRD>(red, acc, M, wave, nwaves, lane, [&](int m, int t, int c, float v) {
+            dst[(size_t)m * a.hidden + 16 * t + c] = v;
+        });
+    } else {
+        reduce_and_store<TRD>(red, acc, M, wave, nwaves, lane, [&](int m, int t, int c, float v) {
+            unsafeAtomicAdd(&a.y[(size_t)toks[m] * a.hidden + o0 + 16 * t + c], v);
+        });
+    }
+}
+
+// Deterministic combine (MoeArgs::det): y[t, c] = the terms of token t's
+// list entries in ascending entry order (ascending expert), then its shared-
+// expert pieces in order -- one fixed summation order, so repeated calls give
+// bit-identical y.  Grid (hidden / 256 column blocks, T); the workgroup
+// gathers token t's entries from tok[] with ballots (ascending by
+// construction) before any thread sums.
+constexpr int kCombineMaxEnt = 256;  // entries of one token (<= max_slots)
+__global__ __launch_bounds__(256) void moe_combine_k(MoeArgs a) {
+    __shared__ int ents[kCombineMaxEnt];
+    __shared__ int wcount[4];
+    const int t = blockIdx.y;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int na = clampi(*a.n_active, 0, a.max_slots);
+    const int n_ent = clampi(a.offsets[na], 0, a.max_entries);
+    int cnt = 0;
+    for (int base = 0; base < n_ent; base += 256) {
+        const int i = base + tid;
+        const bool hit = i < n_ent && a.tok[i] == t;
+        const unsigned long long bm = __ballot(hit);
+        if (lane == 0) wcount[wave] = __builtin_popcountll(bm);
+        __syncthreads();
+        int off = cnt;
+        for (int w = 0; w < wave; ++w) off += wcount[w];
+        const int pos = off + __builtin_popcountll(bm & ((1ull << lane) - 1ull));
+        if (hit && pos < kCombineMaxEnt) ents[pos] = i;
+        cnt += wcount[0] + wcount[1] + wcount[2] + wcount[3];
+        __syncthreads();
+    }
+    const int c = blockIdx.x * 256 + tid;
+    if (c >= a.hidden) return;
+    const int n = cnt < kCombineMaxEnt ? cnt : kCombineMaxEnt;
+    float sum = 0.f;
+    for (int j = 0; j < n; ++j) sum += a.part[(size_t)ents[j] * a.hidden + c];
+    for (int q = 0; q < a.nq; ++q) sum += a.part[(size_t)(a.max_entries + q * a.T + t) * a.hidden + c];
+    a.y[(size_t)t * a.hidden + c] = sum;
 }
 
 // ------------------------------------------- grouped MoE GEMM (prefill)
@@ -2247,9 +2300,13 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
                 } else {
                     const int tkn = is_shared ? m : clampi(a.tok[row0 + m], 0, a.T - 1);
 #pragma unroll
-                    for (int t = 0; t < 2; ++t)
-                        unsafeAtomicAdd(&a.y[(size_t)tkn * a.hidden + strip * 32 * NW + wave * 32 + t * 16 + col],
-                                        acc[mt][t][i]);
+                    for (int t = 0; t < 2; ++t) {
+                        const int cc = strip * 32 * NW + wave * 32 + t * 16 + col;
+                        if (a.det)  // the shared slot's rows max_entries + t are piece 0's
+                            a.part[(size_t)(row0 + m) * a.hidden + cc] = acc[mt][t][i];
+                        else
+                            unsafeAtomicAdd(&a.y[(size_t)tkn * a.hidden + cc], acc[mt][t][i]);
+                    }
                 }
             }
         asm volatile("s_barrier" ::: "memory");  // the chunk's LDS is reused by the next chunk
@@ -2383,7 +2440,18 @@ struct MoePlan {
     size_t xh_off;  // grouped, or T > 4: workspace offset of the fp16 copy of x (else 0)
     int nb_gu, waves_gu, tr_gu, nb_d, trd, waves_d, pieces, inter_pad;
     size_t lds_gu, lds_d, bytes;
+    size_t part_off;  // deterministic combine: workspace offset of the term rows (else 0)
+    int nq;           // shared-expert pieces of the down projection
 };
+
+// The deterministic combine's term rows after the rest of the workspace:
+// (max_entries + nq T) x hidden fp32, 256-byte aligned.
+void plan_part(MoePlan& p, bool det, int T, int hidden, int max_entries) {
+    p.part_off = 0;
+    if (!det) return;
+    p.part_off = (p.bytes + 255) & ~(size_t)255;
+    p.bytes = p.part_off + (size_t)(max_entries + (size_t)p.nq * T) * hidden * 4;
+}
 
 // 16-row output tiles per down-projection workgroup for NB blocks per wave
 // (Qwen1.5-MoE down, NB = 2: two tiles measured 14.8 / 60.0 us per layer at
@@ -2392,7 +2460,7 @@ constexpr int down_tiles(int nb) { return nb <= 4 ? 2 : 1; }
 
 // false when the shape is outside what the kernels support.
 bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, MoePlan& p,
-              int fmt = kFmtInt4) {
+              int fmt = kFmtInt4, bool det = false) {
     if (T <= 0 || hidden <= 0 || hidden % 128 || inter <= 0 || inter % 128) return false;
     if (shared_inter < 0 || shared_inter % 128 || max_entries <= 0) return false;
     p.grouped = T > 16;
@@ -2403,6 +2471,8 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
         // + the fp16 copy of x, 256-byte aligned after inter_buf
         p.xh_off = (p.bytes + 255) & ~(size_t)255;
         p.bytes = p.xh_off + (size_t)T * hidden * 2;
+        p.nq = shared_inter > 0 ? 1 : 0;  // the shared slot covers all of its K
+        plan_part(p, det, T, hidden, max_entries);
         return hidden % 256 == 0;  // grouped GEMM: 256-column down strips
     }
     const int nfh = hidden / 128;
@@ -2433,6 +2503,8 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
         p.xh_off = (p.bytes + 255) & ~(size_t)255;
         p.bytes = p.xh_off + (size_t)T * hidden * 2;
     }
+    p.nq = p.pieces;
+    plan_part(p, det, T, hidden, max_entries);
     return true;
 }
 
@@ -2462,6 +2534,10 @@ void launch_grouped_pair(const MoeArgs& a, dim3 gu, dim3 dn, hipStream_t st) {
     hipLaunchKernelGGL((moe_gemm_k<1, G128, FMT>), dn, dim3(64 * kMgWaves), mg_lds(FMT), st, a);
 }
 
+void launch_combine(const MoeArgs& a, hipStream_t st) {
+    hipLaunchKernelGGL(moe_combine_k, dim3((a.hidden + 255) / 256, a.T), dim3(256), 0, st, a);
+}
+
 void moe_launch_grouped(const MoeArgs& a, hipStream_t st) {
     const int n8 = a.T * a.hidden / 8;
     hipLaunchKernelGGL(x_to_f16_k, dim3((n8 + 255) / 256 < 1024 ? (n8 + 255) / 256 : 1024), dim3(256), 0,
@@ -2477,6 +2553,7 @@ void moe_launch_grouped(const MoeArgs& a, hipStream_t st) {
         launch_grouped_pair<kFmtInt4, true>(a, gu, dn, st);
     else
         launch_grouped_pair<kFmtInt4, false>(a, gu, dn, st);
+    if (a.det) launch_combine(a, st);
 }
 
 template <int FMT, bool G128>
@@ -2500,6 +2577,7 @@ void moe_launch(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
         case 6: launch_down<FMT, G128, 6>(a, p, st); break;
         default: launch_down<FMT, G128, 8>(a, p, st); break;
     }
+    if (a.det) launch_combine(a, st);
 }
 
 }  // namespace
@@ -2647,6 +2725,16 @@ size_t fastllm_moe_int4_workspace_bytes(int T, int hidden, int inter, int shared
     return moe_plan(T, hidden, inter, shared_inter, max_entries, p) ? p.bytes : 0;
 }
 
+size_t fastllm_moe_workspace_bytes_ex(int T, int hidden, int inter, int shared_inter,
+                                      int max_entries, int flags) {
+    if (flags & ~kMoeFlags) return 0;
+    MoePlan p;
+    return moe_plan(T, hidden, inter, shared_inter, max_entries, p, kFmtInt4,
+                    (flags & kMoeDeterministic) != 0)
+               ? p.bytes
+               : 0;
+}
+
 // The fused MoE entry; launch = false only validates the arguments.
 static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int E, int inter,
                           const uint8_t* gq, const uint32_t* gsz, const uint8_t* uq,
@@ -2658,7 +2746,7 @@ static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int
                           const float* tokw, int max_slots, int max_entries, void* workspace,
                           size_t workspace_bytes, float* y, void* stream, bool launch,
                           const RouteArgs* fuse = nullptr, bool xh_ready = false,
-                          int fmt = kFmtInt4) {
+                          int fmt = kFmtInt4, int flags = 0) {
     if (!x || !y || E <= 0 || !gq || !gsz || !uq || !usz || !dq || !dsz) return 1;
     if (fmt == kFmtInt4 && group_size != 32 && group_size != 64 && group_size != 128) return 1;
     if (fmt == kFmtFp8 && group_size != 128) return 1;
@@ -2667,10 +2755,13 @@ static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int
     if (fmt < kFmtInt4 || fmt > kFmtMx4) return 1;
     if (!n_active || !active || !offsets || !tok || !tokw) return 1;
     if (max_slots <= 0 || max_entries <= 0) return 1;
+    if (flags & ~kMoeFlags) return 1;
+    const bool det = (flags & kMoeDeterministic) != 0;
+    if (det && max_slots > kCombineMaxEnt) return 1;  // a token's entries fit the combine's list
     const bool has_shared = shared_inter > 0;
     if (has_shared && (!sgq || !sgsz || !suq || !susz || !sdq || !sdsz)) return 1;
     MoePlan p;
-    if (!moe_plan(T, hidden, inter, has_shared ? shared_inter : 0, max_entries, p, fmt)) return 1;
+    if (!moe_plan(T, hidden, inter, has_shared ? shared_inter : 0, max_entries, p, fmt, det)) return 1;
     if (!workspace || workspace_bytes < p.bytes || !fl_aligned(workspace, 16)) return 1;
     if (!fl_aligned(x, 16) || !fl_aligned(y, 16)) return 1;
     const bool al = fl_aligned(gq, 16) && fl_aligned(uq, 16) && fl_aligned(dq, 16) &&
@@ -2705,6 +2796,9 @@ static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int
     a.fuse_route = (fuse && T == 1 && !p.grouped) ? 1 : 0;
     if (a.fuse_route) a.ra = *fuse;
     a.fmt = fmt;
+    a.det = det ? 1 : 0;
+    a.nq = p.nq;
+    a.part = det ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.part_off) : nullptr;
     hipStream_t st = (hipStream_t)stream;
     if (p.grouped)
         moe_launch_grouped(a, st);
@@ -2765,7 +2859,7 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
                            const uint8_t* suq, const uint32_t* susz, const uint8_t* sdq,
                            const uint32_t* sdsz, void* workspace, size_t workspace_bytes,
                            float* y, void* stream, void* (*scratch_of)() = nullptr,
-                           int fmt = kFmtInt4) {
+                           int fmt = kFmtInt4, int flags = 0) {
     if (!logits || T <= 0 || T > 16 || E <= 0 || E > 256 || top_k <= 0 || top_k > 16 || top_k > E)
         return 1;
     if (!topk_ids || !topk_w || !n_active || !active || !offsets || !tok || !tokw) return 1;
@@ -2775,7 +2869,8 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
     const int max_entries = T * top_k, max_slots = E < max_entries ? E : max_entries;
     if (scratch_of) {
         MoePlan sp;
-        if (!moe_plan(T, hidden, inter, shared_inter > 0 ? shared_inter : 0, max_entries, sp, fmt))
+        if (!moe_plan(T, hidden, inter, shared_inter > 0 ? shared_inter : 0, max_entries, sp, fmt,
+                      (flags & kMoeDeterministic) != 0))
             return 1;
         if (sp.bytes > workspace_bytes) {
             fprintf(stderr,
@@ -2792,7 +2887,8 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
     const int rc = moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz,
                                   shared_inter, sgq, sgsz, suq, susz, sdq, sdsz, shared_coef,
                                   n_active, active, offsets, tok, tokw, max_slots, max_entries,
-                                  workspace, workspace_bytes, y, stream, false, nullptr, false, fmt);
+                                  workspace, workspace_bytes, y, stream, false, nullptr, false, fmt,
+                                  flags);
     if (rc) return rc;
     const MoeLists lists{n_active, active, offsets, tok, tokw};
     const RouteArgs r{logits, e_score_bias, shared_logit, T, E, top_k, scoring, norm, n_group,
@@ -2802,11 +2898,12 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
                               shared_inter, sgq, sgsz, suq, susz, sdq, sdsz,
                               shared_logit ? shared_coef : nullptr, n_active, active, offsets, tok,
                               tokw, max_slots, max_entries, workspace, workspace_bytes, y, stream,
-                              true, &r, false, fmt);
+                              true, &r, false, fmt, flags);
     // T > 4: the router also writes the fp16 token rows the gate/up kernel
     // stages (the plan was validated above)
     MoePlan p;
-    moe_plan(T, hidden, inter, shared_inter > 0 ? shared_inter : 0, max_entries, p, fmt);
+    moe_plan(T, hidden, inter, shared_inter > 0 ? shared_inter : 0, max_entries, p, fmt,
+             (flags & kMoeDeterministic) != 0);
     RouteArgs rx = r;
     if (p.xh_off) {
         rx.x = x;
@@ -2823,7 +2920,7 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
                           shared_inter, sgq, sgsz, suq, susz, sdq, sdsz,
                           shared_logit ? shared_coef : nullptr, n_active, active, offsets, tok, tokw,
                           max_slots, max_entries, workspace, workspace_bytes, y, stream, true,
-                          nullptr, p.xh_off != 0, fmt);
+                          nullptr, p.xh_off != 0, fmt, flags);
 }
 
 }  // extern "C"
@@ -2922,6 +3019,41 @@ int fastllm_moe_int4_routed_noalloc(const float* logits, int top_k, int scoring,
                            active, offsets, tok, tokw, x, T, hidden, group_size, E, inter, gq, gsz,
                            uq, usz, dq, dsz, shared_inter, sgq, sgsz, suq, susz, sdq, sdsz, nullptr,
                            kMoeScratchBytes, y, stream, moe_scratch_ptr);
+}
+
+int fastllm_moe_fused_ex(int format, int flags, const float* x, int T, int hidden, int group_size,
+                         int E, int inter, const uint8_t* gq, const uint32_t* gsz, const uint8_t* uq,
+                         const uint32_t* usz, const uint8_t* dq, const uint32_t* dsz, int shared_inter,
+                         const uint8_t* sgq, const uint32_t* sgsz, const uint8_t* suq,
+                         const uint32_t* susz, const uint8_t* sdq, const uint32_t* sdsz,
+                         const float* shared_coef, const int* n_active, const int* active,
+                         const int* offsets, const int* tok, const float* tokw, int max_slots,
+                         int max_entries, void* workspace, size_t workspace_bytes, float* y,
+                         void* stream) {
+    if (format < kFmtInt4 || format > kFmtMx4) return 1;
+    return moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz, shared_inter,
+                          sgq, sgsz, suq, susz, sdq, sdsz, shared_coef, n_active, active, offsets,
+                          tok, tokw, max_slots, max_entries, workspace, workspace_bytes, y, stream,
+                          true, nullptr, false, format, flags);
+}
+
+int fastllm_moe_routed_ex(int format, int flags, const float* logits, int top_k, int scoring,
+                          int norm, float routed_scaling, const float* e_score_bias, int n_group,
+                          int topk_group, const float* shared_logit, int* topk_ids, float* topk_w,
+                          float* rw, float* shared_coef, int* n_active, int* active, int* offsets,
+                          int* tok, float* tokw, const float* x, int T, int hidden, int group_size,
+                          int E, int inter, const uint8_t* gq, const uint32_t* gsz,
+                          const uint8_t* uq, const uint32_t* usz, const uint8_t* dq,
+                          const uint32_t* dsz, int shared_inter, const uint8_t* sgq,
+                          const uint32_t* sgsz, const uint8_t* suq, const uint32_t* susz,
+                          const uint8_t* sdq, const uint32_t* sdsz, void* workspace,
+                          size_t workspace_bytes, float* y, void* stream) {
+    if (format < kFmtInt4 || format > kFmtMx4) return 1;
+    return moe_routed_impl(logits, top_k, scoring, norm, routed_scaling, e_score_bias, n_group,
+                           topk_group, shared_logit, topk_ids, topk_w, rw, shared_coef, n_active,
+                           active, offsets, tok, tokw, x, T, hidden, group_size, E, inter, gq, gsz,
+                           uq, usz, dq, dsz, shared_inter, sgq, sgsz, suq, susz, sdq, sdsz,
+                           workspace, workspace_bytes, y, stream, nullptr, format, flags);
 }
 
 }  // extern "C"

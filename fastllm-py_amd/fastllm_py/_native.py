@@ -71,6 +71,12 @@ SIGNATURES: dict[str, tuple] = {
     "fastllm_moe_int4_routed": (_I, [_P, _I, _I, _I, _F, _P, _I, _I, _P] + [_P] * 9 +
                                 [_P, _I, _I, _I, _I, _I] + [_P] * 6 + [_I] + [_P] * 6 +
                                 [_P, _SZ, _P, _P]),
+    "fastllm_moe_workspace_bytes_ex": (_SZ, [_I, _I, _I, _I, _I, _I]),
+    "fastllm_moe_fused_ex": (_I, [_I, _I, _P, _I, _I, _I, _I, _I] + [_P] * 6 + [_I] + [_P] * 6 +
+                             [_P] * 6 + [_I, _I, _P, _SZ, _P, _P]),
+    "fastllm_moe_routed_ex": (_I, [_I, _I, _P, _I, _I, _I, _F, _P, _I, _I, _P] + [_P] * 9 +
+                              [_P, _I, _I, _I, _I, _I] + [_P] * 6 + [_I] + [_P] * 6 +
+                              [_P, _SZ, _P, _P]),
     "fastllm_moe_int4_routed_noalloc": (_I, [_P, _I, _I, _I, _F, _P, _I, _I, _P] + [_P] * 9 +
                                         [_P, _I, _I, _I, _I, _I] + [_P] * 6 + [_I] + [_P] * 6 +
                                         [_P, _P]),

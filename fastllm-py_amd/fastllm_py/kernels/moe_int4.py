@@ -329,11 +329,20 @@ def _stacked_ptrs(st):
     return [nat.ptr(st[f"{p}.{k}"]) for p in ("gate", "up", "down") for k in ("qtile", "sz")]
 
 
+# call flags of the fused MoE entries (fastllm_moe_fused_ex / _routed_ex)
+MOE_DETERMINISTIC = 1
+
+
 def moe_workspace_bytes(T: int, hidden: int, inter: int, shared_inter: int,
-                        max_entries: int) -> int:
-    """Device workspace (bytes) of one fused MoE call of this shape."""
-    n = nat.lib().fastllm_moe_int4_workspace_bytes(T, hidden, inter, shared_inter or 0,
-                                                   max_entries)
+                        max_entries: int, deterministic: bool = False) -> int:
+    """Device workspace (bytes) of one fused MoE call of this shape (with the
+    deterministic combine's term rows when ``deterministic``)."""
+    if deterministic:
+        n = nat.lib().fastllm_moe_workspace_bytes_ex(T, hidden, inter, shared_inter or 0,
+                                                     max_entries, MOE_DETERMINISTIC)
+    else:
+        n = nat.lib().fastllm_moe_int4_workspace_bytes(T, hidden, inter, shared_inter or 0,
+                                                       max_entries)
     if n == 0:
         raise ValueError(f"unsupported fused MoE shape T={T} hidden={hidden} inter={inter} "
                          f"shared_inter={shared_inter}")
@@ -385,7 +394,7 @@ def build_lists(T: int, E: int, *, rw=None, slot_coef=None, cand=None, out=None,
 
 def moe_forward(x, stacked, E, hidden, inter, lists, *, max_slots=None, max_entries=None,
                 shared=None, shared_inter=0, shared_coef=None, out=None, workspace=None,
-                stream=None):
+                stream=None, deterministic=False):
     """Fused selective INT4 MoE FFN (x (T, hidden) fp32):
 
     y[t] = sum_{entries p of t} tokw[p] * down_e(silu(gate_e x_t) * up_e x_t)
@@ -395,7 +404,10 @@ def moe_forward(x, stacked, E, hidden, inter, lists, *, max_slots=None, max_entr
     ``build_lists``).  Gate/up run only over the tokens routed to each
     expert; the down projection adds each expert's term into y with fp32
     atomics, as the reference's moew_down does, so the last bits depend on
-    arrival order.  Up to 16 tokens take the decode kernels (weights split
+    arrival order -- unless ``deterministic``: then the terms go to the
+    workspace and one more launch sums each token's terms in a fixed order
+    (ascending expert, then the shared expert), so repeated calls give
+    bit-identical y.  Up to 16 tokens take the decode kernels (weights split
     over the waves along k); more tokens take the grouped GEMM kernels (each
     slot's entries in 64-row chunks on the matrix cores), the prefill form of
     MoELayer._run_gpu_experts (fastllm_py/moe.py:135-159).  ``workspace``
@@ -409,7 +421,7 @@ def moe_forward(x, stacked, E, hidden, inter, lists, *, max_slots=None, max_entr
     if max_slots is None:
         max_slots = min(lists["active"].numel(), max_entries)
     sint = int(shared_inter or 0) if shared is not None else 0
-    need = moe_workspace_bytes(T, hidden, inter, sint, max_entries)
+    need = moe_workspace_bytes(T, hidden, inter, sint, max_entries, deterministic)
     ws = workspace
     if ws is None or ws.numel() * ws.element_size() < need or not ws.is_contiguous():
         ws = t.empty((need,), dtype=t.uint8, device=xd.device)
@@ -422,7 +434,10 @@ def moe_forward(x, stacked, E, hidden, inter, lists, *, max_slots=None, max_entr
             nat.ptr(lists["n_active"]), nat.ptr(lists["active"]), nat.ptr(lists["offsets"]),
             nat.ptr(lists["tok"]), nat.ptr(lists["tokw"]), int(max_slots), int(max_entries),
             nat.ptr(ws), ws.numel() * ws.element_size(), nat.ptr(y), h]
-    if code:
+    if deterministic:
+        nat.check_rc(nat.lib().fastllm_moe_fused_ex(code, MOE_DETERMINISTIC, *args),
+                     "fastllm_moe_fused_ex")
+    elif code:
         nat.check_rc(nat.lib().fastllm_moe_lowp_fused(code, *args), "fastllm_moe_lowp_fused")
     else:
         nat.check_rc(nat.lib().fastllm_moe_int4_fused(*args), "fastllm_moe_int4_fused")
@@ -432,14 +447,15 @@ def moe_forward(x, stacked, E, hidden, inter, lists, *, max_slots=None, max_entr
 def moe_route_forward(x, logits, stacked, top_k, E, hidden, inter, *, norm_topk_prob=False,
                       scoring="softmax", routed_scaling=1.0, e_score_bias=None, n_group=0,
                       topk_group=0, shared=None, shared_inter=0, shared_logit=None, route=None,
-                      out=None, workspace=None, stream=None):
+                      out=None, workspace=None, stream=None, deterministic=False):
     """Router + fused MoE of T <= 16 tokens in one native call: routes
     ``logits`` (T, E) exactly like ``route_topk_device`` (same keyword
     meaning, same outputs, which land in ``route``: topk_ids, topk_w, rw,
     lists, shared_coef) and returns y (T, hidden) fp32 = moe_forward over
     those lists (graph_decode._moe_branch, graph_decode.py:669-700).
     ``route`` / ``workspace`` / ``out`` may carry persistent buffers for
-    graph capture."""
+    graph capture.  ``deterministic``: the ordered combine of moe_forward
+    (bit-identical repeats, one more launch)."""
     t = nat.torch()
     xd = nat.to_device(x, t.float32)
     x2 = xd.reshape(-1, hidden).contiguous()
@@ -475,7 +491,7 @@ def moe_route_forward(x, logits, stacked, top_k, E, hidden, inter, *, norm_topk_
         sl = nat.to_device(shared_logit, t.float32).reshape(-1)
         sc = buf("shared_coef", (T,), t.float32)
     sint = int(shared_inter or 0) if shared is not None else 0
-    need = moe_workspace_bytes(T, hidden, inter, sint, T * top_k)
+    need = moe_workspace_bytes(T, hidden, inter, sint, T * top_k, deterministic)
     ws = workspace
     if ws is None or ws.numel() * ws.element_size() < need or not ws.is_contiguous():
         ws = t.empty((need,), dtype=t.uint8, device=dev)
@@ -484,7 +500,11 @@ def moe_route_forward(x, logits, stacked, top_k, E, hidden, inter, *, norm_topk_
     args = _routed_args(s, top_k, scoring, norm_topk_prob, routed_scaling, bias, n_group,
                         topk_group, sl, o, x2, T, hidden, stacked, E, inter, shared, sint)
     code = _format_code(stacked, shared)
-    if code:
+    if deterministic:
+        rc = nat.lib().fastllm_moe_routed_ex(code, MOE_DETERMINISTIC, *args, nat.ptr(ws),
+                                             ws.numel() * ws.element_size(), nat.ptr(y), h)
+        nat.check_rc(rc, "fastllm_moe_routed_ex")
+    elif code:
         rc = nat.lib().fastllm_moe_lowp_routed(code, *args, nat.ptr(ws), ws.numel() * ws.element_size(),
                                                nat.ptr(y), h)
         nat.check_rc(rc, "fastllm_moe_lowp_routed")

@@ -586,6 +586,54 @@ int fastllm_moe_lowp_routed(int format, const float *logits, int top_k,
                             void *workspace, size_t workspace_bytes, float *y,
                             void *stream);
 
+/* The fused MoE entries with a weight format (0 INT4, FASTLLM_MOE_FP8,
+ * FASTLLM_MOE_MXFP4) and call flags.  FASTLLM_MOE_DETERMINISTIC: the down
+ * projections store each term into the workspace instead of adding it into
+ * y with fp32 atomics, and one more launch sums every token's terms in a
+ * fixed order (its list entries in ascending entry order, i.e. ascending
+ * expert, then the shared expert's pieces), so repeated calls on the same
+ * inputs give bit-identical y; it needs max_slots <= 256 and the workspace
+ * of fastllm_moe_workspace_bytes_ex with the same flags (more than without:
+ * (max_entries + pieces*T) x hidden fp32 term rows).  flags 0 is exactly the
+ * entries above.  Unknown flags or formats return 1 (0 bytes).
+ * No reference counterpart: the reference's moew_down adds with atomicAdd
+ * (fastllm_py/kernels/moe_int4.py:250), whose order varies between calls. */
+#define FASTLLM_MOE_DETERMINISTIC 1
+size_t fastllm_moe_workspace_bytes_ex(int T, int hidden, int inter,
+                                      int shared_inter, int max_entries,
+                                      int flags);
+int fastllm_moe_fused_ex(int format, int flags, const float *x, int T,
+                         int hidden, int group_size, int E, int inter,
+                         const uint8_t *gq, const uint32_t *gsz,
+                         const uint8_t *uq, const uint32_t *usz,
+                         const uint8_t *dq, const uint32_t *dsz,
+                         int shared_inter, const uint8_t *sgq,
+                         const uint32_t *sgsz, const uint8_t *suq,
+                         const uint32_t *susz, const uint8_t *sdq,
+                         const uint32_t *sdsz, const float *shared_coef,
+                         const int *n_active, const int *active,
+                         const int *offsets, const int *tok,
+                         const float *tokw, int max_slots, int max_entries,
+                         void *workspace, size_t workspace_bytes, float *y,
+                         void *stream);
+int fastllm_moe_routed_ex(int format, int flags, const float *logits,
+                          int top_k, int scoring, int norm,
+                          float routed_scaling, const float *e_score_bias,
+                          int n_group, int topk_group,
+                          const float *shared_logit, int *topk_ids,
+                          float *topk_w, float *rw, float *shared_coef,
+                          int *n_active, int *active, int *offsets, int *tok,
+                          float *tokw, const float *x, int T, int hidden,
+                          int group_size, int E, int inter, const uint8_t *gq,
+                          const uint32_t *gsz, const uint8_t *uq,
+                          const uint32_t *usz, const uint8_t *dq,
+                          const uint32_t *dsz, int shared_inter,
+                          const uint8_t *sgq, const uint32_t *sgsz,
+                          const uint8_t *suq, const uint32_t *susz,
+                          const uint8_t *sdq, const uint32_t *sdsz,
+                          void *workspace, size_t workspace_bytes, float *y,
+                          void *stream);
+
 /* fastllm_moe_int4_routed without the workspace argument: the workspace is a
  * static device array of the library, FASTLLM_MOE_SCRATCH_BYTES (16 MiB) per
  * GPU, held until the process ends, so the call allocates nothing (no

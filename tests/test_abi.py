@@ -58,9 +58,27 @@ def test_moe_entry_argument_checks():
         return lib.fastllm_moe_int4_fused(p, T, hidden, gs, 60, inter, *([p] * 6), sinter, *sh,
                                           None, p, p, p, p, p, slots, entries, p, ws_bytes, p, None)
 
+    # the deterministic combine's term rows: (max_entries + pieces T) x hidden fp32 more
+    wsd = lib.fastllm_moe_workspace_bytes_ex(1, 2048, 1408, 5632, 4, 1)
+    assert lib.fastllm_moe_workspace_bytes_ex(1, 2048, 1408, 5632, 4, 0) == ws
+    assert wsd >= ws + (4 + 4 * 1) * 2048 * 4
+    assert lib.fastllm_moe_workspace_bytes_ex(1, 2048, 1408, 5632, 4, 2) == 0  # unknown flag
+    assert lib.fastllm_moe_workspace_bytes_ex(512, 2048, 768, 0, 4096, 1) >= \
+        lib.fastllm_moe_int4_workspace_bytes(512, 2048, 768, 0, 4096) + 4096 * 2048 * 4
+
+    def fused_ex(flags=1, fmt=0, ws_bytes=wsd, slots=4):
+        return lib.fastllm_moe_fused_ex(fmt, flags, p, 1, 2048, 128, 60, 1408, *([p] * 6), 5632,
+                                        *([p] * 6), None, p, p, p, p, p, slots, 4, p, ws_bytes, p,
+                                        None)
+    assert fused_ex(ws_bytes=ws) == 1     # the plain workspace is too small for the term rows
+    assert fused_ex(flags=4) == 1         # unknown flag
+    assert fused_ex(fmt=3) == 1           # unknown format
+    assert fused_ex(slots=300) == 1       # more slots than the combine's per-token list
+
     import torch
     if not torch.cuda.is_available():
         assert fused() == 2
+        assert fused_ex() == 2
     assert fused(gs=96) == 1
     assert fused(hidden=2000) == 1
     assert fused(ws_bytes=ws - 1) == 1
