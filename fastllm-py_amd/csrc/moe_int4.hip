@@ -1944,6 +1944,214 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
     }
 }
 
+// Weight loads of the column-split down kernel: compiler-visible buffer
+// loads, so the compiler tracks their destination registers and places the
+// waits itself (loads issued from inline asm are invisible to it, and it may
+// then copy a destination register before the data has landed).  The
+// descriptor (a whole matrix, in SGPRs) is built once; a block adds a scalar
+// tile offset to a lane offset, so a load costs no 64-bit vector address
+// arithmetic.  Offsets past the descriptor's size read 0.
+typedef __amdgpu_buffer_rsrc_t wb_rsrc_t;
+FL_DEV wb_rsrc_t wb_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+FL_DEV u32x4 wb_ld16(wb_rsrc_t r, uint32_t voff, uint32_t soff = 0) {  // non-temporal
+    return bitcast<u32x4>(__builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 2));
+}
+FL_DEV uint32_t wb_ld4(wb_rsrc_t r, uint32_t voff, uint32_t soff = 0) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, (int)soff, 0);
+}
+
+// A lane's byte offsets into one tile for 128-k block kb: the weight bytes
+// of the block and the lane's scale word.
+struct BlkOff {
+    uint32_t w, s;
+};
+template <int FMT>
+FL_DEV BlkOff blk_offsets(int kb, int g, int lane, int col) {
+    BlkOff o;
+    o.w = (uint32_t)kb * (FMT == kFmtFp8 ? 2048u : 1024u) + 16u * lane;
+    o.s = FMT == kFmtFp8 ? 0u : 4u * (16u * (uint32_t)(FMT == kFmtMx4 ? kb : g) + col);
+    return o;
+}
+
+// Block kb of tile `tile` of the matrix (rq, scales rs), with a fixed number
+// of vector loads: the 16-byte weight load and, INT4 / MXFP4, the lane's
+// scale word; FP8 the second 16-byte half and the block scale (the same
+// word in every lane).
+template <int FMT>
+FL_DEV WBlk<FMT> wb_blk(wb_rsrc_t rq, wb_rsrc_t rs, uint32_t tile, int nkb, int kb, int G, BlkOff o) {
+    constexpr uint32_t TB = FMT == kFmtFp8 ? 2048u : 1024u;
+    WBlk<FMT> b;
+    const uint32_t tw = tile * (uint32_t)nkb * TB;
+    b.w = wb_ld16(rq, o.w, tw);
+    if (FMT == kFmtFp8) {
+        b.w2 = wb_ld16(rq, o.w + 1024u, tw);
+        b.sz = wb_ld4(rs, 0u, ((tile >> 3) * (uint32_t)nkb + (uint32_t)kb) * 4u);
+    } else {
+        b.sz = wb_ld4(rs, o.s, tile * (uint32_t)(FMT == kFmtMx4 ? nkb : G) * 64u);
+    }
+    return b;
+}
+
+// ---- down projection for 4 < T <= 16 tokens, output columns split over waves
+// One workgroup per (slot or shared-expert piece, kDnWaves * kDnTPW output
+// tiles); each wave owns kDnTPW output tiles and streams the slot's whole k
+// range itself (kDnCH blocks per chunk, dn_depth chunks in flight), so there
+// is no cross-wave reduction and no barrier after the start.  The slot's
+// activation rows (inter_buf, row0 .. row0 + M) over the k range are copied
+// into LDS once per workgroup.  Against the split-k kernel (moe_down_k) this
+// runs twice the waves, each with fewer bytes in flight, and the live
+// workgroups of a 16-token batch fit in one generation.  Weight loads are
+// compiler-visible buffer loads in straight-line code (the chunk loop is
+// unrolled), so the compiler's waits leave the later chunks in flight.
+constexpr int kDnWaves = 8;  // waves per workgroup
+constexpr int kDnTPW = 1;    // 16-column output tiles per wave
+constexpr int kDnCH = 2;     // 128-k blocks per chunk
+// chunks in flight: three, two for FP8 (its 2 KB blocks take twice the registers)
+constexpr int dn_depth(int fmt) { return fmt == kFmtFp8 ? 2 : 3; }
+constexpr int kDnMaxCh = 8;  // chunks per slot (k range <= 16 blocks)
+
+// pieces of the shared expert's k range for this kernel (NCH chunks each)
+constexpr int dn_kp(int nch) { return nch * kDnCH; }
+
+// Descriptors of expert e's down matrix and its scales (hidden / 16 tiles,
+// a multiple of 16: at most hidden x inter bytes each, so 32-bit sizes and
+// offsets hold for any expert count).
+struct DnRs {
+    wb_rsrc_t q, s;
+};
+template <int FMT>
+FL_DEV DnRs dn_rsrcs(const MoeExperts& ex, int e, int hidden, int nkb, int G) {
+    const uint32_t tiles = (uint32_t)(hidden / 16);
+    const uint32_t wb = tiles * (uint32_t)nkb * (FMT == kFmtFp8 ? 2048u : 1024u);
+    const uint32_t sw = FMT == kFmtFp8 ? (tiles >> 3) * (uint32_t)nkb : tiles * (uint32_t)(FMT == kFmtMx4 ? nkb : G) * 16u;
+    return DnRs{wb_rsrc(ex.dq + (size_t)e * wb, wb), wb_rsrc(ex.dsz + (size_t)e * sw, sw * 4u)};
+}
+
+template <int FMT, bool G128, int NCH>
+__global__ __launch_bounds__(64 * kDnWaves, 4) void moe_down_ns(MoeArgs a) {  // 4 waves per SIMD: two workgroups per CU
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int toks[16];
+    constexpr int KP = dn_kp(NCH);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, kq = lane >> 4;
+    const int npc = a.has_shared ? a.pieces : 0;  // shared-expert pieces first
+    const int yb = (int)blockIdx.y;
+    const bool is_shared = yb < npc;
+    int e = 0, row0, M, kb0, KR;
+    const MoeExperts* ex;
+    if (!is_shared) {
+        if (!moe_slot(a, yb - npc, e, row0, M)) return;
+        ex = &a.routed;
+        kb0 = 0;
+        KR = ex->inter >> 7;
+    } else {
+        row0 = a.max_entries;
+        M = a.T;
+        ex = &a.shared;
+        kb0 = yb * KP;
+        const int left = (ex->inter >> 7) - kb0;
+        KR = left < KP ? left : KP;
+    }
+    if (M <= 0 || KR <= 0) return;
+    const int nkb = ex->inter >> 7;
+    const int G = ex->inter / a.gs;
+    // the entries' tokens: loaded first, stored to LDS once the weights are
+    // in flight (the store waits for the load)
+    const int tok_ld = is_shared ? 0 : a.tok[row0 + (lane < M ? lane : 0)];
+    // activation rows -> LDS [M][KR blocks][256 B]: 256-byte pieces, four per
+    // wave copy (lane l: 16 bytes l % 16 of piece 4 i + l / 16); a tail past
+    // M KR pieces repeats the last one into the slack
+    const int npieces = M * KR;
+    {
+        const i32x4_t rA = raw_rsrc(a.inter_buf, (uint32_t)(a.max_entries + a.T) * (uint32_t)a.inter_pad * 2u);
+        const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+        for (int p0 = 4 * wave; p0 < npieces; p0 += 4 * kDnWaves) {
+            int p = p0 + (lane >> 4);
+            p = p < npieces ? p : npieces - 1;
+            const int m = p / KR, kl = p - m * KR;
+            lds_copy(rA, lds0 + (uint32_t)p0 * 256u,
+                     2u * ((uint32_t)(row0 + m) * (uint32_t)a.inter_pad + (uint32_t)(kb0 + kl) * 128u) +
+                         16u * (uint32_t)(lane & 15));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const DnRs rs = dn_rsrcs<FMT>(*ex, e, a.hidden, nkb, G);
+    const uint32_t tile0 = blockIdx.x * (kDnWaves * kDnTPW) + wave * kDnTPW;  // within expert e
+    // block i of chunk c: k block kb0 + min(c kDnCH + i, KR - 1) (a block past
+    // KR repeats the last one and counts zero)
+    auto issue = [&](WBlk<FMT> (&w)[kDnCH][kDnTPW], int c) {
+#pragma unroll
+        for (int i = 0; i < kDnCH; ++i) {
+            const int kl = c * kDnCH + i < KR ? c * kDnCH + i : KR - 1;
+            const int kb = kb0 + kl;
+            const BlkOff o = blk_offsets<FMT>(kb, (kb * 128 + 32 * kq) / a.gs, lane, col);
+#pragma unroll
+            for (int t = 0; t < kDnTPW; ++t) w[i][t] = wb_blk<FMT>(rs.q, rs.s, tile0 + t, nkb, kb, G, o);
+        }
+    };
+    constexpr int kDnD = dn_depth(FMT);
+    WBlk<FMT> wb[kDnD][kDnCH][kDnTPW];
+#pragma unroll
+    for (int c = 0; c < kDnD && c < NCH; ++c) {
+        issue(wb[c], c);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (threadIdx.x < 16) toks[threadIdx.x] = is_shared ? threadIdx.x : clampi(tok_ld, 0, a.T - 1);
+    // the copies were issued before every weight load: once the first weight
+    // word has landed (the asm names it, so the compiler waits for it) they
+    // have too; the barrier then publishes every wave's pieces and toks
+    asm volatile("" : : "v"(wb[0][0][0].w) : "memory");
+    lds_barrier();
+    const int mrow = col < M ? col : M - 1;
+    const unsigned char* arow = smem + (size_t)mrow * KR * 256;
+    f32x4 acc[kDnTPW];
+#pragma unroll
+    for (int t = 0; t < kDnTPW; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+        for (int i = 0; i < kDnCH; ++i) {
+            const int kl = c * kDnCH + i < KR ? c * kDnCH + i : KR - 1;
+            const float live = c * kDnCH + i < KR ? 1.0f : 0.0f;
+            u32x4 av[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                av[j] = *reinterpret_cast<const u32x4*>(arow + (size_t)kl * 256 + 2 * a_koff<FMT>(kq, j));
+#pragma unroll
+            for (int t = 0; t < kDnTPW; ++t) {
+                wblk_mma<FMT, G128>(acc[t], av, wb[c % kDnD][i][t], live);
+                // keeps the scaled add here: the compiler otherwise sinks every
+                // block's add to the epilogue and keeps each block's partial
+                // MFMA result live until then
+                asm volatile("" : "+v"(acc[t]));
+            }
+            __builtin_amdgcn_sched_barrier(0);  // one block's operands live at a time
+        }
+        if (c + kDnD < NCH) issue(wb[c % kDnD], c + kDnD);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // lane: rows 4 (lane / 16) + r of tile t, column lane % 16
+    const uint32_t c0 = (blockIdx.x * (kDnWaves * kDnTPW) + wave * kDnTPW) * 16u + (uint32_t)col;
+#pragma unroll
+    for (int t = 0; t < kDnTPW; ++t) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int m = 4 * kq + r;
+            if (m < M) {
+                if (a.det) {
+                    const size_t prow = is_shared ? (size_t)a.max_entries + (size_t)yb * a.T + m : (size_t)row0 + m;
+                    a.part[prow * a.hidden + c0 + 16 * t] = acc[t][r];
+                } else {
+                    unsafeAtomicAdd(&a.y[(size_t)toks[m] * a.hidden + c0 + 16 * t], acc[t][r]);
+                }
+            }
+        }
+    }
+}
+
 // Deterministic combine (MoeArgs::det): y[t, c] = the terms of token t's
 // list entries in ascending entry order (ascending expert), then its shared-
 // expert pieces in order -- one fixed summation order, so repeated calls give
@@ -2442,6 +2650,9 @@ struct MoePlan {
     size_t lds_gu, lds_d, bytes;
     size_t part_off;  // deterministic combine: workspace offset of the term rows (else 0)
     int nq;           // shared-expert pieces of the down projection
+    bool dn_ns;       // down by the column-split kernel (moe_down_ns), nch chunks
+    int nch;
+    size_t lds_dn;
 };
 
 // The deterministic combine's term rows after the rest of the workspace:
@@ -2503,6 +2714,17 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
         p.xh_off = (p.bytes + 255) & ~(size_t)255;
         p.bytes = p.xh_off + (size_t)T * hidden * 2;
     }
+    // 5..16 tokens: the column-split down kernel when a slot's k range fits
+    // its chunks (the shared expert then splits into pieces of that size)
+    const int nch = (nfr + kDnCH - 1) / kDnCH;
+    p.dn_ns = T > kGuOwnT && nch <= kDnMaxCh && hidden % (16 * kDnWaves * kDnTPW) == 0;
+    p.nch = nch;
+    p.lds_dn = 0;
+    if (p.dn_ns) {
+        const int kp = dn_kp(nch);
+        p.pieces = shared_inter > 0 ? (shared_inter / 128 + kp - 1) / kp : 0;
+        p.lds_dn = (size_t)T * kp * 256 + 768;
+    }
     p.nq = p.pieces;
     plan_part(p, det, T, hidden, max_entries);
     return true;
@@ -2526,6 +2748,19 @@ void launch_down(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
     const dim3 grid(a.hidden / (16 * down_tiles(NB)), a.max_slots + (a.has_shared ? p.pieces : 0));
     hipLaunchKernelGGL((moe_down_k<FMT, G128, NB, down_tiles(NB)>), grid, dim3(64 * p.waves_d), p.lds_d,
                        st, a);
+}
+
+template <int FMT, bool G128>
+void launch_down_ns(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
+    const dim3 grid(a.hidden / (16 * kDnWaves * kDnTPW), a.max_slots + (a.has_shared ? p.pieces : 0));
+    const dim3 blk(64 * kDnWaves);
+    switch (p.nch) {
+#define DN_CASE(n) \
+    case n: hipLaunchKernelGGL((moe_down_ns<FMT, G128, n>), grid, blk, p.lds_dn, st, a); break;
+        DN_CASE(1) DN_CASE(2) DN_CASE(3) DN_CASE(4) DN_CASE(5) DN_CASE(6) DN_CASE(7)
+        default: hipLaunchKernelGGL((moe_down_ns<FMT, G128, 8>), grid, blk, p.lds_dn, st, a); break;
+#undef DN_CASE
+    }
 }
 
 template <int FMT, bool G128>
@@ -2569,13 +2804,17 @@ void moe_launch(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
         case 3: launch_gate_up<FMT, G128, 3>(a, p, st); break;
         default: launch_gate_up<FMT, G128, 4>(a, p, st); break;
     }
-    switch (p.nb_d) {
-        case 1: launch_down<FMT, G128, 1>(a, p, st); break;
-        case 2: launch_down<FMT, G128, 2>(a, p, st); break;
-        case 3: launch_down<FMT, G128, 3>(a, p, st); break;
-        case 4: launch_down<FMT, G128, 4>(a, p, st); break;
-        case 6: launch_down<FMT, G128, 6>(a, p, st); break;
-        default: launch_down<FMT, G128, 8>(a, p, st); break;
+    if (p.dn_ns) {
+        launch_down_ns<FMT, G128>(a, p, st);
+    } else {
+        switch (p.nb_d) {
+            case 1: launch_down<FMT, G128, 1>(a, p, st); break;
+            case 2: launch_down<FMT, G128, 2>(a, p, st); break;
+            case 3: launch_down<FMT, G128, 3>(a, p, st); break;
+            case 4: launch_down<FMT, G128, 4>(a, p, st); break;
+            case 6: launch_down<FMT, G128, 6>(a, p, st); break;
+            default: launch_down<FMT, G128, 8>(a, p, st); break;
+        }
     }
     if (a.det) launch_combine(a, st);
 }

@@ -495,6 +495,9 @@ def test_moe_branch_graph_capture(torch_gpu):
     (2, 4, 2, 4096, 640, 2560, 128),      # hidden 4096: 4 gate/up blocks per wave
     (1, 2, 1, 1024, 8192, 0, 128),        # inter 8192: 8 down blocks per wave
     (5, 6, 3, 384, 384, 3200, 32),        # group 32, shared in 9 pieces
+    # 5..16 tokens, hidden a multiple of 256: the column-split down kernel
+    (8, 12, 4, 512, 2048, 2560, 128),     # 16 k blocks (8 chunks), shared in 2 pieces
+    (7, 10, 3, 768, 640, 1152, 64),       # 5 k blocks (a chunk half past the end), shared 6 + 3
 ])
 def test_fused_moe_shapes(torch_gpu, T, E, K, hidden, inter, sinter, gs):
     """Router lists + fused MoE over the launch-plan variants, vs the fp32
