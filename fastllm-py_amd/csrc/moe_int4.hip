@@ -1952,9 +1952,6 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
 // tile offset to a lane offset, so a load costs no 64-bit vector address
 // arithmetic.  Offsets past the descriptor's size read 0.
 typedef __amdgpu_buffer_rsrc_t wb_rsrc_t;
-FL_DEV wb_rsrc_t wb_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
 FL_DEV u32x4 wb_ld16(wb_rsrc_t r, uint32_t voff, uint32_t soff = 0) {  // non-temporal
     return bitcast<u32x4>(__builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 2));
 }
@@ -2026,7 +2023,7 @@ FL_DEV DnRs dn_rsrcs(const MoeExperts& ex, int e, int hidden, int nkb, int G) {
     const uint32_t tiles = (uint32_t)(hidden / 16);
     const uint32_t wb = tiles * (uint32_t)nkb * (FMT == kFmtFp8 ? 2048u : 1024u);
     const uint32_t sw = FMT == kFmtFp8 ? (tiles >> 3) * (uint32_t)nkb : tiles * (uint32_t)(FMT == kFmtMx4 ? nkb : G) * 16u;
-    return DnRs{wb_rsrc(ex.dq + (size_t)e * wb, wb), wb_rsrc(ex.dsz + (size_t)e * sw, sw * 4u)};
+    return DnRs{buf_rsrc(ex.dq + (size_t)e * wb, wb), buf_rsrc(ex.dsz + (size_t)e * sw, sw * 4u)};
 }
 
 template <int FMT, bool G128, int NCH>
@@ -2148,6 +2145,145 @@ __global__ __launch_bounds__(64 * kDnWaves, 4) void moe_down_ns(MoeArgs a) {  //
                     unsafeAtomicAdd(&a.y[(size_t)toks[m] * a.hidden + c0 + 16 * t], acc[t][r]);
                 }
             }
+        }
+    }
+}
+
+// ---- gate/up for 4 < T <= 16 tokens (hidden <= 2048), columns split over waves
+// The same split as moe_down_ns: one workgroup per (shared-expert or slot
+// column group of 16 kDnWaves intermediate columns); each wave owns one gate
+// and one up tile and streams all hidden / 128 k blocks of both itself, so
+// h = silu(g) u w is formed in registers with no cross-wave reduction.  The
+// T token rows of the fp16 copy of x (all of them: they do not depend on the
+// lists) are copied into LDS at the start, before the weights.
+template <int FMT>
+FL_DEV DnRs gu_rsrcs(const uint8_t* q, const uint32_t* sz, int e, int inter, int nkb, int G) {
+    const uint32_t tiles = (uint32_t)(inter / 16);  // a multiple of 8
+    const uint32_t wb = tiles * (uint32_t)nkb * (FMT == kFmtFp8 ? 2048u : 1024u);
+    const uint32_t sw = FMT == kFmtFp8 ? (tiles >> 3) * (uint32_t)nkb : tiles * (uint32_t)(FMT == kFmtMx4 ? nkb : G) * 16u;
+    return DnRs{buf_rsrc(q + (size_t)e * wb, wb), buf_rsrc(sz + (size_t)e * sw, sw * 4u)};
+}
+
+template <int FMT, bool G128, int NCH>
+__global__ __launch_bounds__(64 * kDnWaves, 4) void moe_gate_up_ns(MoeArgs a) {  // two workgroups per CU
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, kq = lane >> 4;
+    const int K = a.hidden, KB = K >> 7, T = a.T;
+    constexpr int GW = 16 * kDnWaves;  // intermediate columns per workgroup
+    // grid: shared-expert groups first (they need no lists), then (slot, group)
+    const int n_sh = a.has_shared ? a.shared.inter / GW : 0;
+    const int groups_r = a.routed.inter / GW;
+    const int b = (int)blockIdx.x;
+    // y zeroed for the down kernel's accumulation, spread over the whole grid
+    // before any workgroup can leave (these stores are older than every
+    // weight load, so the waits below do not count them)
+    for (int i = b * 64 * kDnWaves + (int)threadIdx.x; i < T * K / 4; i += (int)gridDim.x * 64 * kDnWaves)
+        reinterpret_cast<f32x4*>(a.y)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const bool routed = b >= n_sh;
+    int e = 0, row0, M, grp;
+    const MoeExperts* ex;
+    if (routed) {
+        const int slot = (b - n_sh) / groups_r;
+        grp = b - n_sh - slot * groups_r;
+        if (!moe_slot(a, slot, e, row0, M)) return;
+        ex = &a.routed;
+    } else {
+        grp = b;
+        row0 = a.max_entries;
+        M = T;
+        ex = &a.shared;
+    }
+    if (M <= 0) return;
+    // token rows -> LDS [T][KB][256 B]: 256-byte pieces, four per wave copy
+    // (lane l: 16 bytes l % 16 of piece 4 i + l / 16); a tail repeats the
+    // last piece into the slack
+    const int npieces = T * KB;
+    {
+        const i32x4_t rX = raw_rsrc(a.xh, (uint32_t)T * (uint32_t)K * 2u);
+        const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+        for (int p0 = 4 * wave; p0 < npieces; p0 += 4 * kDnWaves) {
+            int p = p0 + (lane >> 4);
+            p = p < npieces ? p : npieces - 1;
+            lds_copy(rX, lds0 + (uint32_t)p0 * 256u, 2u * (uint32_t)p * 128u + 16u * (uint32_t)(lane & 15));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the lane's MFMA row: entry jr of the unit (token tok_ld) and its weight
+    // (unconditional loads: values not used are replaced after the barrier)
+    const int jr = col < M ? col : M - 1;
+    const int tok_ld = a.tok[routed ? row0 + jr : 0];
+    const float w_ld = *(routed ? a.tokw + row0 + jr : (a.scoef ? a.scoef + jr : a.tokw));
+    const int G = K / a.gs;
+    const int inter = ex->inter;
+    const DnRs rg = gu_rsrcs<FMT>(ex->gq, ex->gsz, e, inter, KB, G);
+    const DnRs ru = gu_rsrcs<FMT>(ex->uq, ex->usz, e, inter, KB, G);
+    const uint32_t tile = (uint32_t)(grp * kDnWaves + wave);  // within expert e
+    auto issue = [&](WBlk<FMT> (&w)[kDnCH][2], int c) {
+#pragma unroll
+        for (int i = 0; i < kDnCH; ++i) {
+            const int kb = c * kDnCH + i < KB ? c * kDnCH + i : KB - 1;
+            const BlkOff o = blk_offsets<FMT>(kb, (kb * 128 + 32 * kq) / a.gs, lane, col);
+            w[i][0] = wb_blk<FMT>(rg.q, rg.s, tile, KB, kb, G, o);
+            w[i][1] = wb_blk<FMT>(ru.q, ru.s, tile, KB, kb, G, o);
+        }
+    };
+    // each chunk holds gate and up: one chunk fewer in flight than the down
+    constexpr int kD = dn_depth(FMT) > 2 ? dn_depth(FMT) - 1 : 2;
+    WBlk<FMT> wb[kD][kDnCH][2];
+#pragma unroll
+    for (int c = 0; c < kD && c < NCH; ++c) {
+        issue(wb[c], c);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // the copies were issued before every weight load: once the first weight
+    // word has landed (the asm names it, so the compiler waits for it) they
+    // have too; the barrier publishes every wave's pieces
+    asm volatile("" : : "v"(wb[0][0][0].w) : "memory");
+    lds_barrier();
+    // first uses of the token and weight words only here (through the asm),
+    // so their wait does not move above the weight loads
+    int tk = tok_ld;
+    float wl = w_ld;
+    asm volatile("" : "+v"(tk), "+v"(wl));
+    tk = routed ? tk : jr;
+    wl = (routed || a.scoef) ? wl : 1.0f;
+    const unsigned char* arow = smem + (size_t)clampi(tk, 0, T - 1) * KB * 256;
+    f32x4 acc[2];
+    acc[0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+        for (int i = 0; i < kDnCH; ++i) {
+            const int kb = c * kDnCH + i < KB ? c * kDnCH + i : KB - 1;
+            const float live = c * kDnCH + i < KB ? 1.0f : 0.0f;
+            u32x4 av[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                av[j] = *reinterpret_cast<const u32x4*>(arow + (size_t)kb * 256 + 2 * a_koff<FMT>(kq, j));
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                wblk_mma<FMT, G128>(acc[t], av, wb[c % kD][i][t], live);
+                asm volatile("" : "+v"(acc[t]));  // keeps the scaled add here (see moe_down_ns)
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (c + kD < NCH) issue(wb[c % kD], c + kD);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // lane: rows 4 (lane / 16) + r, column lane % 16; entry m's weight from
+    // lane m (its MFMA row was entry m)
+    const uint32_t c0 = (uint32_t)(grp * GW + wave * 16 + col);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int m = 4 * kq + r;
+        const float wm = __shfl(wl, m);
+        if (m < M) {
+            const float g = acc[0][r], u = acc[1][r];
+            const float h = (g / (1.0f + expf(-g))) * u * wm;
+            a.inter_buf[(size_t)(row0 + m) * a.inter_pad + c0] = bitcast<uint16_t>((f16)h);
         }
     }
 }
@@ -2653,6 +2789,9 @@ struct MoePlan {
     bool dn_ns;       // down by the column-split kernel (moe_down_ns), nch chunks
     int nch;
     size_t lds_dn;
+    bool gu_ns;       // gate/up by the column-split kernel (moe_gate_up_ns), nch_gu chunks
+    int nch_gu;
+    size_t lds_gun;
 };
 
 // The deterministic combine's term rows after the rest of the workspace:
@@ -2727,6 +2866,11 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
     }
     p.nq = p.pieces;
     plan_part(p, det, T, hidden, max_entries);
+    // 5..16 tokens, hidden <= 2048: the column-split gate/up
+    p.nch_gu = (nfh + kDnCH - 1) / kDnCH;
+    p.gu_ns = T > kGuOwnT && p.nch_gu <= kDnMaxCh && inter % (16 * kDnWaves) == 0 &&
+              shared_inter % (16 * kDnWaves) == 0;
+    p.lds_gun = (size_t)T * nfh * 256 + 768;
     return true;
 }
 
@@ -2748,6 +2892,20 @@ void launch_down(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
     const dim3 grid(a.hidden / (16 * down_tiles(NB)), a.max_slots + (a.has_shared ? p.pieces : 0));
     hipLaunchKernelGGL((moe_down_k<FMT, G128, NB, down_tiles(NB)>), grid, dim3(64 * p.waves_d), p.lds_d,
                        st, a);
+}
+
+template <int FMT, bool G128>
+void launch_gate_up_ns(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
+    const int gw = 16 * kDnWaves;
+    const dim3 grid(a.max_slots * (a.routed.inter / gw) + (a.has_shared ? a.shared.inter / gw : 0));
+    const dim3 blk(64 * kDnWaves);
+    switch (p.nch_gu) {
+#define GU_CASE(n) \
+    case n: hipLaunchKernelGGL((moe_gate_up_ns<FMT, G128, n>), grid, blk, p.lds_gun, st, a); break;
+        GU_CASE(1) GU_CASE(2) GU_CASE(3) GU_CASE(4) GU_CASE(5) GU_CASE(6) GU_CASE(7)
+        default: hipLaunchKernelGGL((moe_gate_up_ns<FMT, G128, 8>), grid, blk, p.lds_gun, st, a); break;
+#undef GU_CASE
+    }
 }
 
 template <int FMT, bool G128>
@@ -2798,11 +2956,15 @@ void moe_launch(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
         hipLaunchKernelGGL(x_to_f16_k, dim3((n8 + 255) / 256), dim3(256), 0, st, a.x,
                            const_cast<uint16_t*>(a.xh), n8);
     }
-    switch (p.nb_gu) {
-        case 1: launch_gate_up<FMT, G128, 1>(a, p, st); break;
-        case 2: launch_gate_up<FMT, G128, 2>(a, p, st); break;
-        case 3: launch_gate_up<FMT, G128, 3>(a, p, st); break;
-        default: launch_gate_up<FMT, G128, 4>(a, p, st); break;
+    if (p.gu_ns) {
+        launch_gate_up_ns<FMT, G128>(a, p, st);
+    } else {
+        switch (p.nb_gu) {
+            case 1: launch_gate_up<FMT, G128, 1>(a, p, st); break;
+            case 2: launch_gate_up<FMT, G128, 2>(a, p, st); break;
+            case 3: launch_gate_up<FMT, G128, 3>(a, p, st); break;
+            default: launch_gate_up<FMT, G128, 4>(a, p, st); break;
+        }
     }
     if (p.dn_ns) {
         launch_down_ns<FMT, G128>(a, p, st);
