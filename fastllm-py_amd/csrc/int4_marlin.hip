@@ -776,6 +776,137 @@ __global__ __launch_bounds__(1024) void int4_gemv_norm(NormArgs nrm, const uint3
     int4_gemv_body<T, NB, G32, 4, SWI>(nullptr, Wq, S, Z, C, 1, N, K, nrm);
 }
 
+// Column-split GEMV for wide outputs (N / 16 >= kCsMinTiles), 5..16 rows,
+// group 128: each wave owns one 16-column n-tile and streams all K / 128
+// blocks of it itself, so there is no cross-wave reduction, no split and
+// no barrier after the start, and one generation of workgroups covers the
+// matrix (gate_up 24576 x 4096: 1536 tiles, 192 workgroups of 8 waves;
+// 6 waves on all 256 CUs, two-block chunks, or more chunks in flight each
+// measured slower).
+// The MR activation rows (rows past M repeat row M - 1) are copied whole
+// into LDS first, as activation mode 6 does per block: [block][row][256 B],
+// the 16-byte k chunks of row r XOR-swizzled by r.  Weights, scales and zero
+// words are compiler-visible buffer loads (scalar block offsets, lane
+// offsets fixed per wave), kCsCH blocks per chunk, kCsD chunks in flight; the
+// chunk loop's first pass only issues, so each buffer is written in one
+// place and the compiler's waits leave the later chunks in flight.
+constexpr int kCsWaves = 8;       // waves (n-tiles) per workgroup
+constexpr int kCsCH = 1;          // 128-k blocks per chunk
+constexpr int kCsD = 4;           // chunks in flight
+constexpr int kCsMinTiles = 1024;  // narrower outputs keep the split-k GEMV
+
+struct CsBlk {
+    u32x4 w;
+    uint32_t z;
+    uint16_t s;
+};
+
+template <int MR>
+__global__ __launch_bounds__(64 * kCsWaves) void int4_gemv_cs(const f16* __restrict__ A,
+                                                              const uint32_t* __restrict__ Wq,
+                                                              const uint16_t* __restrict__ S,
+                                                              const uint32_t* __restrict__ Z,
+                                                              f16* __restrict__ C, int M, int N, int K) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, kq = lane >> 4;
+    const int nkb = K >> 7, ntiles = N >> 4, zwords = N >> 3;
+    const int tb = xcd_block() * kCsWaves + wave;  // this wave's n-tile
+    const bool tlive = tb < ntiles;
+    const int nt = tlive ? tb : ntiles - 1;
+    // activation rows into LDS: one copy = 4 rows x 256 B of one block
+    {
+        const i32x4_t rA = raw_rsrc(A, (uint32_t)M * (uint32_t)K * 2u);
+        const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+        const int ncp = nkb * (MR / 4);
+        for (int c = wave; c < ncp; c += kCsWaves) {
+            const int kb = c / (MR / 4), p = c - kb * (MR / 4);
+            const int r = 4 * p + (lane >> 4);
+            const int m = r < M ? r : M - 1;
+            lds_copy(rA, lds0 + (uint32_t)(kb * MR + 4 * p) * 256u,
+                     2u * ((uint32_t)m * (uint32_t)K + (uint32_t)kb * 128u + 8u * (uint32_t)((lane & 15) ^ r)));
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int n = nt * 16 + col;
+    const uint32_t voS = 2u * (uint32_t)marlin_scale_pos(n);
+    const int cl = n & 63;
+    const uint32_t voZ = 4u * (uint32_t)(((n >> 6) << 3) + (cl & 7));
+    const int zsh = 4 * slot_of(cl >> 3);
+    const __amdgpu_buffer_rsrc_t rW = buf_rsrc(Wq, (uint32_t)((size_t)N * K / 2));
+    const __amdgpu_buffer_rsrc_t rS = buf_rsrc(S, (uint32_t)nkb * (uint32_t)N * 2u);
+    const __amdgpu_buffer_rsrc_t rZ = buf_rsrc(Z, (uint32_t)nkb * (uint32_t)zwords * 4u);
+    const uint32_t wt = (uint32_t)nt * 8u * (uint32_t)K;  // the tile's bytes
+    const int nch = (nkb + kCsCH - 1) / kCsCH;
+    // block i of chunk c: min(c kCsCH + i, nkb - 1); a block past the end
+    // repeats the last one and counts zero
+    auto issue = [&](CsBlk (&b)[kCsCH], int c) {
+        c = c < nch ? c : nch - 1;
+#pragma unroll
+        for (int i = 0; i < kCsCH; ++i) {
+            const int kb = c * kCsCH + i < nkb ? c * kCsCH + i : nkb - 1;
+            b[i].w = bitcast<u32x4>(__builtin_amdgcn_raw_buffer_load_b128(rW, (int)(16u * lane),
+                                                                          (int)(wt + 1024u * kb), 2));
+            b[i].s = __builtin_amdgcn_raw_buffer_load_b16(rS, (int)voS, (int)(2u * (uint32_t)N * kb), 0);
+            b[i].z = __builtin_amdgcn_raw_buffer_load_b32(rZ, (int)voZ, (int)(4u * (uint32_t)zwords * kb), 0);
+        }
+    };
+    const uint32_t mlo = 0x64006400u, mhi = 0x54005400u;
+    const int arow = col < M ? col : M - 1;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    CsBlk buf[kCsD][kCsCH];
+    const int passes = (nch + kCsD - 1) / kCsD + 1;
+    for (int it = 0; it < passes; ++it) {
+#pragma unroll
+        for (int d = 0; d < kCsD; ++d) {
+            const int c = (it - 1) * kCsD + d;  // the chunk computed here
+            if (it == 1 && d == 0) {
+                // the copies went out before every weight load: once the
+                // first weight word has landed (the asm names it, so the
+                // compiler waits for it) they have too; the barrier publishes
+                // every wave's rows
+                asm volatile("" : : "v"(buf[0][0].w) : "memory");
+                lds_barrier();
+            }
+            if (it > 0 && c < nch) {
+#pragma unroll
+                for (int i = 0; i < kCsCH; ++i) {
+                    const int kr = c * kCsCH + i;
+                    const int kb = kr < nkb ? kr : nkb - 1;
+                    const unsigned char* ab = smem + ((size_t)kb * MR + arow) * 256;
+                    f16x8 a[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) a[j] = *reinterpret_cast<const f16x8*>(ab + 16 * ((4 * j + kq) ^ arow));
+                    uint32_t zlo, zhi;
+                    zero_bits((buf[d][i].z >> zsh) & 0xFu, zlo, zhi);
+                    f32x4 part = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        part = mfma_f16(a[j], dequant_word_fast(buf[d][i].w[j], zlo, zhi, mlo, mhi), part);
+                    const float sc = kr < nkb ? (float)bitcast<f16>(buf[d][i].s) : 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(sc, part[e], acc[e]);
+                    // keeps the scaled add here: the compiler would otherwise
+                    // sink every block's add to the end and keep each block's
+                    // partial MFMA result live until then
+                    asm volatile("" : "+v"(acc));
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            issue(buf[d], it * kCsD + d);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if (tlive) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int m = 4 * kq + e;
+            if (m < M) C[(size_t)m * N + nt * 16 + col] = (f16)acc[e];
+        }
+    }
+}
+
 // Prefill-shaped GEMM (M > 64, K % 128 == 0) on the matrix cores.
 //
 // Workgroup tile 64 (m) x 256 (n): eight waves side by side along n, each
@@ -1316,6 +1447,20 @@ bool int4_marlin_abi_gemm(const void* a, const uint32_t* q, const void* scales,
     if (M > 16)
         return int4_gemm_large_m(A, q, static_cast<const f16*>(scales), zeros, Cp, M, N, K, g32,
                                  stream);
+    if (!forced && !g32 && M > 4 && K % 128 == 0 && N / 16 >= kCsMinTiles && (size_t)N * K / 2 < (1ull << 31)) {
+        // wide output, 5..16 rows: the column-split GEMV, all rows in LDS
+        const int mr = M > 8 ? 16 : 8;
+        const size_t lds = (size_t)(K / 128) * mr * 256;
+        if (lds <= 128 * 1024) {
+            const dim3 grid((N / 16 + kCsWaves - 1) / kCsWaves), block(64 * kCsWaves);
+            const uint16_t* S = static_cast<const uint16_t*>(scales);
+            if (mr == 16)
+                hipLaunchKernelGGL(int4_gemv_cs<16>, grid, block, lds, stream, A, q, S, zeros, Cp, M, N, K);
+            else
+                hipLaunchKernelGGL(int4_gemv_cs<8>, grid, block, lds, stream, A, q, S, zeros, Cp, M, N, K);
+            return report(hipGetLastError(), "FastllmCudaMarlinHalfInt4Gemm");
+        }
+    }
     GemvCfg cfg = forced ? *forced : default_gemv_cfg(M, N, K, g32, ws != nullptr);
     if (cfg.split > 1 && (!ws || !fl_aligned(ws, 256) || N / 16 > kSplitStrips ||
                           ws_bytes < splitk_ws_bytes(M, N, cfg.split))) {

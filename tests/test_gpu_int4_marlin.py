@@ -232,6 +232,29 @@ def test_gemv_four_tiles(torch_gpu, M, gs):
         assert Q.max_abs_rel(y.float().cpu().numpy(), ref) < TOL, (tiles, waves, nb)
 
 
+@pytest.mark.parametrize("M,N,K", [(5, 16448, 1152), (13, 16448, 4096), (16, 24576, 384), (8, 16384, 8192)])
+def test_gemv_column_split(torch_gpu, M, N, K):
+    """Wide outputs (N / 16 >= 1024) at 5..16 rows, group 128: the
+    column-split GEMV (one n-tile per wave over all of K). 1028 tiles leave
+    the last workgroup with two live waves; 9 and 3 blocks end half way
+    through a two-block chunk; M = 8 at K = 8192 stages 8 rows (64 KB)."""
+    from fastllm_py.kernels import marlin
+
+    torch = torch_gpu
+    rng = np.random.default_rng(400 + M + K)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    a = rng.standard_normal((M, K)).astype(np.float16)
+    pay, w_hat, _ = _prep(torch, W, 128)
+    ref = Q.matmul_ref(a.astype(np.float32), w_hat)
+    ad = torch.from_numpy(a).cuda()
+    out = marlin.marlin_gemm_int4(ad, pay["qweight"], pay["scales"], pay["zeros"])
+    out2 = marlin.marlin_gemm_int4(ad, pay["qweight"], pay["scales"], pay["zeros"])
+    torch.cuda.synchronize()
+    assert Q.max_abs_rel(out.float().cpu().numpy(), ref) < TOL
+    # no atomics or splits: a repeat is bit-identical
+    assert torch.equal(out, out2)
+
+
 @pytest.mark.parametrize("gs", [128, 32])
 def test_gemv_split_k(torch_gpu, gs):
     """Split-K decode GEMV through fastllm_int4_gemm_ws: every forced
