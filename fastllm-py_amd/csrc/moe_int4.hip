@@ -855,7 +855,7 @@ FL_DEV void net_argsort(float (&kf)[4], int (&ix)[4], int maxN, int lane) {
             const int d = m >> 1;
             net_step(kf, ix, nsl, [&](int c, int& pc, int& pl, bool& mx) {
                 const int R = 8 * c + (lane >> 3);
-                const bool hi = (R % m) >= d;
+                const bool hi = (R & (m - 1)) >= d;  // m: a power of two
                 const int R2 = hi ? R - d : R + d;
                 mx = hi;
                 pc = R2 >> 3;
@@ -891,11 +891,16 @@ FL_DEV int net_load_sort(const float (&v)[4], int n, int lane, float (&kf)[4], i
 // topk_ids/topk_w (and scoef, rw).
 // Values sit one per lane in nc <= 4 slots (expert lane + 64 c); slots past
 // nc are skipped by uniform branches.  Everything stays in registers except
-// the exp row of the softmax sum.
+// the exp row of the softmax sum.  NC = route_slots(E): 1 (E <= 64) and 2
+// (E <= 128) fix nc at compile time, which removes the per-slot branches and
+// the E-dependent sum paths of the general (NC = 4) body.
+__host__ __device__ constexpr int route_slots(int E) { return E <= 64 ? 1 : (E <= 128 ? 2 : 4); }
+
+template <int NC>
 FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw, int* sids,
                         float* sws, int& my_id, float& my_w, bool store = true) {
     const int E = a.E, K = a.K;
-    const int nc = (E + 63) >> 6;
+    const int nc = NC < 4 ? NC : (E + 63) >> 6;
     float sel[4], p[4];
     const float* s = a.logits + (size_t)t * E;
     // the logit (and bias) loads go out together, indices clamped
@@ -927,9 +932,9 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        const float z = E <= 64    ? np_sum_wave64(exw, E, lane, p[0])
-                        : E <= 128 ? np_sum_wave128(exw, E, lane, p[0], p[1])
-                                   : np_sum_wave(exw, E, lane);
+        const float z = NC == 1   ? np_sum_wave64(exw, E, lane, p[0])
+                        : NC == 2 ? np_sum_wave128(exw, E, lane, p[0], p[1])
+                                  : np_sum_wave(exw, E, lane);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int e = lane + 64 * c;
@@ -1011,7 +1016,7 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
     my_id = 0;
     my_w = 0.f;
     bool tie = false;  // some round's maximum held by more than one expert
-    if (nc == 1) {
+    if (NC == 1) {
         // one expert per lane (E <= 64): the same rounds without slot loops
         uint32_t k0 = key[0];
         for (int i = 0; i < K; ++i) {
@@ -1153,6 +1158,7 @@ FL_DEV void one_token_lists(const RouteArgs& a, int lane, int my_id, float my_w)
 // (one wave each), so T = 512 routes on 128 CUs instead of 32 (16.5 us on 32
 // workgroups of 16 waves).
 constexpr int kRouteTpb = 4;
+template <int NC>
 __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
     __shared__ float ex[16][256];
     __shared__ int sids[16 * kMaxTopK];
@@ -1162,7 +1168,6 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
     __shared__ unsigned selm[256];
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nw = blockDim.x >> 6;
     const int rb = gridDim.x - a.xh_blocks;  // routing workgroups
     if ((int)blockIdx.x >= rb) {
         // fp16 copy of the token rows, beside the routing
@@ -1183,10 +1188,14 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
     int my_id = 0;
     float my_w = 0.f;
     const int tpb = rb > 1 ? kRouteTpb : 16;  // tokens per routing workgroup
-    for (int tl = wv; tl < tpb; tl += nw) {
+    // every launch has a wave per token of its workgroup (tpb <= waves), so
+    // a wave routes at most one token: no loop, whose preheader would take
+    // every loop-invariant piece of the routing (group sizes, the tie
+    // network's lane constants) ahead of the first load
+    {
+        const int tl = wv;
         const int t = blockIdx.x * tpb + tl;
-        if (t >= a.T) break;
-        route_token(a, t, tl, lane, ex[wv], sids, sws, my_id, my_w);
+        if (tl < tpb && t < a.T) route_token<NC>(a, t, tl, lane, ex[wv], sids, sws, my_id, my_w);
     }
     if (rb == 1 && a.lists.n_active) {
         if (a.T == 1) {
@@ -1195,6 +1204,14 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
         }
         __syncthreads();
         build_lists(sids, sws, a.T, a.K, a.E, a.lists, cnt, base, selm);
+    }
+}
+
+void launch_route(const RouteArgs& a, int grid, int threads, hipStream_t st) {
+    switch (route_slots(a.E)) {
+        case 1: hipLaunchKernelGGL(route_k<1>, dim3(grid), dim3(threads), 0, st, a); break;
+        case 2: hipLaunchKernelGGL(route_k<2>, dim3(grid), dim3(threads), 0, st, a); break;
+        default: hipLaunchKernelGGL(route_k<4>, dim3(grid), dim3(threads), 0, st, a); break;
     }
 }
 
@@ -1618,7 +1635,11 @@ FL_DEV void fused_route_slot(const RouteArgs& r, int slot, bool store, int& e, f
         const int lane = threadIdx.x;
         int my_id = 0;
         float my_w = 0.f;
-        route_token(r, 0, 0, lane, exw, sids, sws, my_id, my_w, store);
+        switch (route_slots(r.E)) {
+            case 1: route_token<1>(r, 0, 0, lane, exw, sids, sws, my_id, my_w, store); break;
+            case 2: route_token<2>(r, 0, 0, lane, exw, sids, sws, my_id, my_w, store); break;
+            default: route_token<4>(r, 0, 0, lane, exw, sids, sws, my_id, my_w, store); break;
+        }
         const int rank = one_token_rank(r.K, my_id);
         if (lane < r.K && rank == slot) {
             s_e = my_id;
@@ -3041,7 +3062,7 @@ int fastllm_route_topk(const float* logits, int T, int E, int top_k, int scoring
     hipStream_t st = (hipStream_t)stream;
     const int wpb = T <= 16 ? T : kRouteTpb;
     const int grid = T <= 16 ? 1 : (T + kRouteTpb - 1) / kRouteTpb;
-    hipLaunchKernelGGL(route_k, dim3(grid), dim3(64 * wpb), 0, st, a);
+    launch_route(a, grid, 64 * wpb, st);
     int rc = finish("fastllm_route_topk");
     if (rc) return rc;
     if (grid > 1 && n_active) {
@@ -3314,7 +3335,7 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
         rx.xh_blocks = (n8 + per - 1) / per;
     }
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(route_k, dim3(1 + rx.xh_blocks), dim3(64 * T), 0, st, rx);
+    launch_route(rx, 1 + rx.xh_blocks, 64 * T, st);
     const int rr = finish("fastllm_moe_int4_routed");
     if (rr) return rr;
     return moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz,
