@@ -961,16 +961,27 @@ __global__ __launch_bounds__(512) void fp8_gemm_mfma(const uint16_t* __restrict_
                    nsplit - 1;
         __syncthreads();
         if (!last) return;
+        // splits outermost: each pass issues the tile's loads together (one
+        // memory round trip per split, not per element and split); every
+        // element still sums its partials in split order
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const size_t idx = tile_off + ((wave * MT + mt) * 4 + e) * 64 + lane;
-                float v = 0.0f;
-                for (int q = 0; q < nsplit; ++q)
-                    v += __hip_atomic_load(part + q * split_stride + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                acc[mt][0][e] = v;
-            }
+            for (int e = 0; e < 4; ++e) acc[mt][0][e] = 0.0f;
+        for (int q = 0; q < nsplit; ++q) {
+            float pv[MT][4];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    pv[mt][e] = __hip_atomic_load(part + q * split_stride + tile_off +
+                                                      ((wave * MT + mt) * 4 + e) * 64 + lane,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[mt][0][e] += pv[mt][e];
+        }
         if (threadIdx.x == 0) __hip_atomic_store(cnt + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 

@@ -302,6 +302,42 @@ struct SplitArgs {
     int* cnt = nullptr;
 };
 
+// Sum of the nsplit (<= 16) partials p[0], p[stride], ... in split order,
+// read with agent-coherent loads that all issue before the first add (a
+// loop of dependent loads costs one memory round trip per split).
+constexpr int kMaxSplits = 16;
+template <int NS>
+FL_DEV float split_sum_n(const float* p, size_t stride) {
+    float pv[NS];
+#pragma unroll
+    for (int q = 0; q < NS; ++q) pv[q] = __hip_atomic_load(p + q * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float v = 0.f;
+#pragma unroll
+    for (int q = 0; q < NS; ++q) v += pv[q];
+    return v;
+}
+
+FL_DEV float split_sum(const float* p, size_t stride, int nsplit) {
+    switch (nsplit) {
+        case 1: return split_sum_n<1>(p, stride);
+        case 2: return split_sum_n<2>(p, stride);
+        case 3: return split_sum_n<3>(p, stride);
+        case 4: return split_sum_n<4>(p, stride);
+        case 5: return split_sum_n<5>(p, stride);
+        case 6: return split_sum_n<6>(p, stride);
+        case 7: return split_sum_n<7>(p, stride);
+        case 8: return split_sum_n<8>(p, stride);
+        case 9: return split_sum_n<9>(p, stride);
+        case 10: return split_sum_n<10>(p, stride);
+        case 11: return split_sum_n<11>(p, stride);
+        case 12: return split_sum_n<12>(p, stride);
+        case 13: return split_sum_n<13>(p, stride);
+        case 14: return split_sum_n<14>(p, stride);
+        case 15: return split_sum_n<15>(p, stride);
+        default: return split_sum_n<16>(p, stride);
+    }
+}
+
 template <int T, int NB, bool G32, int AM, bool SWI>
 __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const uint32_t* __restrict__ Wq,
                                                const uint16_t* __restrict__ S, const uint32_t* __restrict__ Z,
@@ -750,10 +786,7 @@ __device__ __forceinline__ void int4_gemv_body(const f16* __restrict__ A, const 
         const int m = 4 * (l >> 4) + e;
         if (m >= M) continue;
         const size_t n = (size_t)(strip * T + t) * 16 + (l & 15);
-        float v = 0.f;
-        for (int q = 0; q < nsplit; ++q)
-            v += __hip_atomic_load(sp.ws + ((size_t)q * M + m) * N + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        C[(size_t)m * N + n] = (f16)v;
+        C[(size_t)m * N + n] = (f16)split_sum(sp.ws + (size_t)m * N + n, (size_t)M * N, nsplit);
     }
     if (threadIdx.x == 0) __hip_atomic_store(sp.cnt + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1339,7 +1372,7 @@ bool gemv_cfg_ok(const GemvCfg& c, int M, int N, int K, bool g32) {
     if (c.tiles == 4 && c.nb > 4) return false;
     if (c.waves < 1 || c.waves > 16) return false;
     if (N % (16 * c.tiles)) return false;
-    if (c.split < 1 || c.split > 16) return false;
+    if (c.split < 1 || c.split > kMaxSplits) return false;
     if (c.split > 1 && (K % 128 || (K / 128) % c.split)) return false;  // whole blocks per split
     const int nfull = K / 128 / c.split;
     if (nfull < 1 && !(g32 && K == 64)) return false;
