@@ -2678,6 +2678,216 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
     }
 }
 
+// INT4 grouped MoE GEMM with the weights streamed into registers.  The same
+// units, tiles and epilogue as moe_gemm_k, but only the activation tile (the
+// operand all waves share) goes through the LDS ring; each wave's two tile
+// blocks and their scale|zero words (its own, read back by no other wave)
+// are compiler-visible buffer loads into a register ring kMrD blocks deep.
+// The LDS then holds kMrD + 1 activation stages (16 KB each), so two
+// workgroups per CU keep kMrD blocks of weights in flight where the shared
+// stages of moe_gemm_k (36 KB each) allow one.  B is s * (q - z) rounded to
+// fp16 (the Marlin operand) and the MFMAs accumulate in fp32.
+// Hand-off per block c: the compiler waits for the wave's first weight word
+// of c (named by an empty asm), and the activation copies of c went out just
+// before it, so they have landed too; one barrier then publishes every
+// wave's copies and retires the stage of block c - 1, which the copies of
+// block c + kMrD (issued after the barrier) overwrite.
+constexpr int kMrD = 3;              // blocks in flight ahead
+constexpr int kMrStages = kMrD + 1;  // activation stages
+constexpr size_t kMrLds = (size_t)kMrStages * kMgABytes;
+
+template <int V>
+struct IntC {
+    static constexpr int value = V;
+};
+
+struct MrBlk {
+    u32x4 w[2];      // the two tiles' 1 KB blocks, this lane's 16 bytes
+    uint32_t sz[2];  // this lane's scale|zero word of each tile
+};
+
+template <int PHASE, bool G128>
+__global__ __launch_bounds__(64 * kMgWaves, 2) void moe_gemm_rk(MoeArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int D = kMrD, NS = kMrStages, NW = kMgWaves, FPW = 16 / NW;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, kq = lane >> 4;
+    const int slot = blockIdx.y, strip = blockIdx.x;
+    if (PHASE == 0) {
+        // every workgroup zeroes its share of y for the down phase's atomics
+        const int nwg = gridDim.x * gridDim.y;
+        const int wg = blockIdx.y * gridDim.x + blockIdx.x;
+        const int n4 = a.T * a.hidden / 4;
+        for (int i = wg * 64 * NW + threadIdx.x; i < n4; i += nwg * 64 * NW)
+            reinterpret_cast<f32x4*>(a.y)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const bool is_shared = slot >= a.max_slots;
+    if (is_shared && !a.has_shared) return;
+    int e = 0, row0, M;
+    const MoeExperts* ex;
+    if (!is_shared) {
+        if (!moe_slot(a, slot, e, row0, M)) return;
+        const int r1 = clampi(__builtin_amdgcn_readfirstlane(a.offsets[slot + 1]), row0, a.max_entries);
+        M = r1 - row0;
+        ex = &a.routed;
+    } else {
+        row0 = a.max_entries;
+        M = a.T;
+        ex = &a.shared;
+    }
+    const int inter = ex->inter;
+    const int K = PHASE == 0 ? a.hidden : inter;
+    const int Nrows = PHASE == 0 ? inter : a.hidden;
+    const int ncols = PHASE == 0 ? 16 * NW : 32 * NW;
+    if (M <= 0 || strip * ncols >= Nrows) return;
+    const int nkb = K >> 7;
+    const int G = K / a.gs;
+    const int spb = 128 / a.gs;  // groups per 128-k block
+
+    // this wave's two weight tiles: blocks and scale|zero words
+    __amdgpu_buffer_rsrc_t rq[2], rz[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        size_t tile;
+        const uint8_t* tq;
+        const uint32_t* tsz;
+        if (PHASE == 0) {
+            tile = (size_t)e * (inter / 16) + strip * NW + wave;
+            tq = t == 0 ? ex->gq : ex->uq;
+            tsz = t == 0 ? ex->gsz : ex->usz;
+        } else {
+            tile = (size_t)e * (a.hidden / 16) + strip * 2 * NW + wave * 2 + t;
+            tq = ex->dq;
+            tsz = ex->dsz;
+        }
+        rq[t] = buf_rsrc(tq + tile * nkb * 1024, (uint32_t)nkb * 1024u);
+        rz[t] = buf_rsrc(tsz + tile * G * 16, (uint32_t)G * 64u);
+    }
+    const uint32_t zoff = 4u * (uint32_t)((kq * 32 / a.gs) * 16 + col);  // this lane's word in a block
+    const uint32_t zstep = (uint32_t)spb * 64u;                           // scale bytes per block
+    // A rows: PHASE 0 token rows of xh, PHASE 1 the slot's inter_buf rows
+    const uint16_t* abase = PHASE == 0 ? a.xh : a.inter_buf;
+    const int astride = PHASE == 0 ? a.hidden : a.inter_pad;  // halves
+    const int arows = PHASE == 0 ? a.T : a.max_entries + a.T;
+    const i32x4_t rA = raw_rsrc(abase, (uint32_t)arows * astride * 2);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+
+    for (int mc = 0; mc < M; mc += 64) {
+        const int mt_live = (M - mc + 15) >> 4;  // m-tiles holding rows of this chunk
+        // A copies f = FPW wave + i of this wave: fragment f = 4 m-tile + j in
+        // MFMA order (16 rows x four 16-byte pieces)
+        uint32_t ao[FPW];
+#pragma unroll
+        for (int i = 0; i < FPW; ++i) {
+            const int f = wave * FPW + i;
+            int m = mc + 16 * (f >> 2) + col;
+            m = m < M ? m : M - 1;
+            const int row = PHASE == 0 ? (is_shared ? m : clampi(a.tok[row0 + m], 0, a.T - 1)) : row0 + m;
+            ao[i] = 2u * ((uint32_t)row * astride + a_koff<kFmtInt4>(kq, f & 3));
+        }
+        // block b (clamped: blocks past the end repeat the last one, whose
+        // stage and registers nobody reads): activation copies into stage
+        // b % NS, then the wave's weight and scale loads into r
+        auto issue = [&](MrBlk& r, int b) {
+            const int kb = b < nkb ? b : nkb - 1;
+            const uint32_t st = lds0 + (uint32_t)(b % NS) * kMgABytes;
+#pragma unroll
+            for (int i = 0; i < FPW; ++i)
+                if (wave * FPW + i < 4 * mt_live)  // dead m-tiles: no copy
+                    lds_copy(rA, st + (wave * FPW + i) * 1024, ao[i], kb * 256);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                r.w[t] = bitcast<u32x4>(__builtin_amdgcn_raw_buffer_load_b128(rq[t], (int)(16u * lane),
+                                                                              (int)(1024u * kb), 2));
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                r.sz[t] = __builtin_amdgcn_raw_buffer_load_b32(rz[t], (int)zoff, (int)(zstep * kb), 0);
+        };
+
+        f32x4 acc[4][2];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        // the block loop for ML live m-tiles (a compile-time count: no
+        // per-MFMA branches, no activation reads of dead m-tiles)
+        auto run = [&](auto mlc) {
+            constexpr int ML = decltype(mlc)::value;
+            MrBlk ring[D];
+            const int passes = (nkb + D - 1) / D + 1;
+            for (int it = 0; it < passes; ++it) {
+#pragma unroll
+                for (int d = 0; d < D; ++d) {
+                    const int c = (it - 1) * D + d;  // the block computed here
+                    if (it > 0 && c < nkb) {
+                        asm volatile("" : : "v"(ring[d].w[0]) : "memory");
+                        asm volatile("s_barrier" ::: "memory");
+                        const unsigned char* ab = smem + (size_t)(c % NS) * kMgABytes + lane * 16;
+                        uint32_t zlo[2], zhi[2];
+#pragma unroll
+                        for (int t = 0; t < 2; ++t) tile_zero_bits(sz_zero(ring[d].sz[t]), zlo[t], zhi[t]);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            f16x8 av[ML];
+#pragma unroll
+                            for (int mt = 0; mt < ML; ++mt)
+                                av[mt] = *reinterpret_cast<const f16x8*>(ab + (mt * 4 + j) * 1024);
+#pragma unroll
+                            for (int t = 0; t < 2; ++t) {
+                                const f16x8 b = bitcast<f16x8>(scale_f16x8(
+                                    bitcast<u32x4>(dequant_word_fast(ring[d].w[t][j], zlo[t], zhi[t], 0x64006400u,
+                                                                     0x54005400u)),
+                                    sz_scale(ring[d].sz[t])));
+#pragma unroll
+                                for (int mt = 0; mt < ML; ++mt) acc[mt][t] = mfma_f16(av[mt], b, acc[mt][t]);
+                            }
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    issue(ring[d], it * D + d);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        };
+        switch (mt_live) {
+            case 1: run(IntC<1>{}); break;
+            case 2: run(IntC<2>{}); break;
+            case 3: run(IntC<3>{}); break;
+            default: run(IntC<4>{}); break;
+        }
+        wait_vmcnt<0>();
+
+        // epilogue: rows mc + 16 mt + 4 kq + i of the chunk
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = mc + 16 * mt + 4 * kq + i;
+                if (m >= M) continue;
+                if (PHASE == 0) {
+                    const float g = acc[mt][0][i], u = acc[mt][1][i];
+                    const float w = !is_shared ? a.tokw[row0 + m] : (a.scoef ? a.scoef[m] : 1.0f);
+                    const float h = (g / (1.0f + expf(-g))) * u * w;
+                    a.inter_buf[(size_t)(row0 + m) * a.inter_pad + strip * 16 * NW + wave * 16 + col] =
+                        bitcast<uint16_t>((f16)h);
+                } else {
+                    const int tkn = is_shared ? m : clampi(a.tok[row0 + m], 0, a.T - 1);
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const int cc = strip * 32 * NW + wave * 32 + t * 16 + col;
+                        if (a.det)
+                            a.part[(size_t)(row0 + m) * a.hidden + cc] = acc[mt][t][i];
+                        else
+                            unsafeAtomicAdd(&a.y[(size_t)tkn * a.hidden + cc], acc[mt][t][i]);
+                    }
+                }
+            }
+        asm volatile("s_barrier" ::: "memory");  // the chunk's LDS is reused by the next chunk
+    }
+}
+
 int finish(const char* what) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
@@ -2944,8 +3154,13 @@ void launch_down_ns(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
 
 template <int FMT, bool G128>
 void launch_grouped_pair(const MoeArgs& a, dim3 gu, dim3 dn, hipStream_t st) {
-    hipLaunchKernelGGL((moe_gemm_k<0, G128, FMT>), gu, dim3(64 * kMgWaves), mg_lds(FMT), st, a);
-    hipLaunchKernelGGL((moe_gemm_k<1, G128, FMT>), dn, dim3(64 * kMgWaves), mg_lds(FMT), st, a);
+    if constexpr (FMT == kFmtInt4) {
+        hipLaunchKernelGGL((moe_gemm_rk<0, G128>), gu, dim3(64 * kMgWaves), kMrLds, st, a);
+        hipLaunchKernelGGL((moe_gemm_rk<1, G128>), dn, dim3(64 * kMgWaves), kMrLds, st, a);
+    } else {
+        hipLaunchKernelGGL((moe_gemm_k<0, G128, FMT>), gu, dim3(64 * kMgWaves), mg_lds(FMT), st, a);
+        hipLaunchKernelGGL((moe_gemm_k<1, G128, FMT>), dn, dim3(64 * kMgWaves), mg_lds(FMT), st, a);
+    }
 }
 
 void launch_combine(const MoeArgs& a, hipStream_t st) {
