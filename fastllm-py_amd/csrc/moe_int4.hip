@@ -2417,7 +2417,10 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, kq = lane >> 4;
-    const int slot = blockIdx.y, strip = blockIdx.x;
+    // XCD-grouped units, as in moe_gemm_rk
+    const int lin = blockIdx.y * gridDim.x + blockIdx.x, units = gridDim.x * gridDim.y;
+    const int unit = (units & 7) ? lin : (lin & 7) * (units >> 3) + (lin >> 3);
+    const int slot = unit / gridDim.x, strip = unit - slot * gridDim.x;
     if (PHASE == 0) {
         // every workgroup zeroes its share of y for the down phase's atomics
         const int nwg = gridDim.x * gridDim.y;
@@ -2713,7 +2716,13 @@ __global__ __launch_bounds__(64 * kMgWaves, 2) void moe_gemm_rk(MoeArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, kq = lane >> 4;
-    const int slot = blockIdx.y, strip = blockIdx.x;
+    // XCD-grouped units: the hardware deals workgroup L (linear index) to XCD
+    // L % 8, so with the unit count a multiple of 8 XCD x takes the
+    // contiguous units [x U/8, (x+1) U/8): whole slots, whose strips then
+    // share the slot's activation rows in one L2
+    const int lin = blockIdx.y * gridDim.x + blockIdx.x, units = gridDim.x * gridDim.y;
+    const int unit = (units & 7) ? lin : (lin & 7) * (units >> 3) + (lin >> 3);
+    const int slot = unit / gridDim.x, strip = unit - slot * gridDim.x;
     if (PHASE == 0) {
         // every workgroup zeroes its share of y for the down phase's atomics
         const int nwg = gridDim.x * gridDim.y;
