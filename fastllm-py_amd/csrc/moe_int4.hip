@@ -2784,34 +2784,41 @@ __global__ __launch_bounds__(64 * kMgWaves, 2) void moe_gemm_rk(MoeArgs a) {
 
     for (int mc = 0; mc < M; mc += 64) {
         const int mt_live = (M - mc + 15) >> 4;  // m-tiles holding rows of this chunk
+        // lane l holds row mc + l's token and combine weight (rows past M
+        // repeat row M - 1), read once per chunk and handed out by shuffles
+        const int ml = mc + lane < M ? mc + lane : M - 1;
+        const int ltok = is_shared ? ml : clampi(a.tok[row0 + ml], 0, a.T - 1);
+        const float lw = PHASE != 0 ? 0.0f : (!is_shared ? a.tokw[row0 + ml] : (a.scoef ? a.scoef[ml] : 1.0f));
         // A copies f = FPW wave + i of this wave: fragment f = 4 m-tile + j in
         // MFMA order (16 rows x four 16-byte pieces)
         uint32_t ao[FPW];
 #pragma unroll
         for (int i = 0; i < FPW; ++i) {
             const int f = wave * FPW + i;
-            int m = mc + 16 * (f >> 2) + col;
-            m = m < M ? m : M - 1;
-            const int row = PHASE == 0 ? (is_shared ? m : clampi(a.tok[row0 + m], 0, a.T - 1)) : row0 + m;
+            const int r = 16 * (f >> 2) + col;  // chunk row
+            const int row = PHASE == 0 ? __shfl(ltok, r, 64) : row0 + (mc + r < M ? mc + r : M - 1);
             ao[i] = 2u * ((uint32_t)row * astride + a_koff<kFmtInt4>(kq, f & 3));
         }
-        // block b (clamped: blocks past the end repeat the last one, whose
-        // stage and registers nobody reads): activation copies into stage
-        // b % NS, then the wave's weight and scale loads into r
+        // block b: activation copies into stage b % NS, then the wave's weight
+        // and scale loads into r.  Blocks past the end keep the load count
+        // (so the compiler's waits stay exact) with lane offsets past every
+        // buffer's range: the loads return zeros without touching memory,
+        // into a retired stage and a ring slot nobody reads.
         auto issue = [&](MrBlk& r, int b) {
             const int kb = b < nkb ? b : nkb - 1;
+            const uint32_t oob = b < nkb ? 0u : 0x80000000u;
             const uint32_t st = lds0 + (uint32_t)(b % NS) * kMgABytes;
 #pragma unroll
             for (int i = 0; i < FPW; ++i)
                 if (wave * FPW + i < 4 * mt_live)  // dead m-tiles: no copy
-                    lds_copy(rA, st + (wave * FPW + i) * 1024, ao[i], kb * 256);
+                    lds_copy(rA, st + (wave * FPW + i) * 1024, ao[i] | oob, kb * 256);
 #pragma unroll
             for (int t = 0; t < 2; ++t)
-                r.w[t] = bitcast<u32x4>(__builtin_amdgcn_raw_buffer_load_b128(rq[t], (int)(16u * lane),
+                r.w[t] = bitcast<u32x4>(__builtin_amdgcn_raw_buffer_load_b128(rq[t], (int)(16u * lane | oob),
                                                                               (int)(1024u * kb), 2));
 #pragma unroll
             for (int t = 0; t < 2; ++t)
-                r.sz[t] = __builtin_amdgcn_raw_buffer_load_b32(rz[t], (int)zoff, (int)(zstep * kb), 0);
+                r.sz[t] = __builtin_amdgcn_raw_buffer_load_b32(rz[t], (int)(zoff | oob), (int)(zstep * kb), 0);
         };
 
         f32x4 acc[4][2];
@@ -2874,15 +2881,17 @@ __global__ __launch_bounds__(64 * kMgWaves, 2) void moe_gemm_rk(MoeArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = mc + 16 * mt + 4 * kq + i;
+                // shuffles with every lane active (a lane whose row is past M
+                // may hold the row another lane reads)
+                const float w = __shfl(lw, 16 * mt + 4 * kq + i, 64);
+                const int tkn = __shfl(ltok, 16 * mt + 4 * kq + i, 64);
                 if (m >= M) continue;
                 if (PHASE == 0) {
                     const float g = acc[mt][0][i], u = acc[mt][1][i];
-                    const float w = !is_shared ? a.tokw[row0 + m] : (a.scoef ? a.scoef[m] : 1.0f);
                     const float h = (g / (1.0f + expf(-g))) * u * w;
                     a.inter_buf[(size_t)(row0 + m) * a.inter_pad + strip * 16 * NW + wave * 16 + col] =
                         bitcast<uint16_t>((f16)h);
                 } else {
-                    const int tkn = is_shared ? m : clampi(a.tok[row0 + m], 0, a.T - 1);
 #pragma unroll
                     for (int t = 0; t < 2; ++t) {
                         const int cc = strip * 32 * NW + wave * 32 + t * 16 + col;
