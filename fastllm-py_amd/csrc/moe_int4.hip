@@ -2499,6 +2499,11 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
         // of the block (two full cache lines); lane l takes row 4 f + l / 16
         // and its 16-byte k chunk (l % 16) ^ (row % 16).  INT4: fragment f =
         // 4 m-tile + j in MFMA order (16 rows x four 16-byte pieces).
+        // lane l holds row mc + l's token and combine weight (rows past M
+        // repeat row M - 1), read once per chunk and handed out by shuffles
+        const int ml = mc + lane < M ? mc + lane : M - 1;
+        const int ltok = is_shared ? ml : clampi(a.tok[row0 + ml], 0, a.T - 1);
+        const float lw = PHASE != 0 ? 0.0f : (!is_shared ? a.tokw[row0 + ml] : (a.scoef ? a.scoef[ml] : 1.0f));
         uint32_t ao[4];
 #pragma unroll
         for (int i = 0; i < FPW; ++i) {
@@ -2506,26 +2511,28 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
             const int r = ROWA ? 4 * f + (lane >> 4) : 16 * (f >> 2) + col;
             int m = mc + r;
             m = m < M ? m : M - 1;
-            const int row = PHASE == 0 ? (is_shared ? m : clampi(a.tok[row0 + m], 0, a.T - 1))
-                                       : row0 + m;
+            const int row = PHASE == 0 ? __shfl(ltok, m - mc, 64) : row0 + m;
             ao[i] = 2u * ((uint32_t)row * astride +
                           (ROWA ? 8 * ((lane & 15) ^ (r & 15)) : a_koff<FMT>(kq, f & 3)));
         }
+        // blocks past the end keep the copy count with lane offsets past
+        // every buffer's range: they read zeros without touching memory
         auto issue = [&](int kb, int stg) {
+            const uint32_t oob = kb < nkb ? 0u : 0x80000000u;
             kb = kb < nkb ? kb : nkb - 1;
             const uint32_t st = lds0 + (uint32_t)stg * STG;
 #pragma unroll
             for (int i = 0; i < FPW; ++i)
                 if (kMgAhead > 1 || wave * FPW + i < 4 * mt_live)  // dead m-tiles: no copy
-                    lds_copy(rA, st + (wave * FPW + i) * 1024, ao[i], kb * 256);
+                    lds_copy(rA, st + (wave * FPW + i) * 1024, ao[i] | oob, kb * 256);
             const uint32_t wst = st + kMgABytes + wave * WST;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int h = 0; h < BPT; ++h)  // FP8: the block's two 1 KB halves
-                    lds_copy(rq[t], wst + t * TB + h * 1024, h * 1024 + lane * 16, kb * TB);
+                    lds_copy(rq[t], wst + t * TB + h * 1024, (h * 1024 + lane * 16) | oob, kb * TB);
 #pragma unroll
-            for (int t = 0; t < 2; ++t) lds_copy<4>(rz[t], wst + 2 * TB + t * 256, zlane, kb * zstep);
+            for (int t = 0; t < 2; ++t) lds_copy<4>(rz[t], wst + 2 * TB + t * 256, zlane | oob, kb * zstep);
         };
 
         f32x4 acc[4][2];
@@ -2658,15 +2665,17 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int m = mc + 16 * mt + 4 * kq + i;
+                // shuffles with every lane active (a lane whose row is past M
+                // may hold the row another lane reads)
+                const float w = __shfl(lw, 16 * mt + 4 * kq + i, 64);
+                const int tkn = __shfl(ltok, 16 * mt + 4 * kq + i, 64);
                 if (m >= M) continue;
                 if (PHASE == 0) {
                     const float g = acc[mt][0][i], u = acc[mt][1][i];
-                    const float w = !is_shared ? a.tokw[row0 + m] : (a.scoef ? a.scoef[m] : 1.0f);
                     const float h = (g / (1.0f + expf(-g))) * u * w;
                     a.inter_buf[(size_t)(row0 + m) * a.inter_pad + strip * 16 * NW + wave * 16 + col] =
                         bitcast<uint16_t>((f16)h);
                 } else {
-                    const int tkn = is_shared ? m : clampi(a.tok[row0 + m], 0, a.T - 1);
 #pragma unroll
                     for (int t = 0; t < 2; ++t) {
                         const int cc = strip * 32 * NW + wave * 32 + t * 16 + col;
