@@ -697,12 +697,14 @@ def run_gemm_prefill(torch, lib, stream, M=512, N=8192, K=2048):
             **cycle(n * marlin_bytes(0, N, K))}
 
 
-def run_moe_prefill(torch, lib, stream, T=512, fmt="int4", deterministic=False):
+def run_moe_prefill(torch, lib, stream, T=512, fmt="int4", deterministic=False, routed=True):
     """Config 5's grouped MoE layer (Qwen3-30B-A3B): 128 experts, hidden 2048,
     inter 768, top-8 softmax with renormalisation from fp16 logits ~ N(0,1),
-    M=512 tokens, `fmt` expert weights.  Timed unit = one layer: route +
-    gate/up + down launches; HBM-bound on the routed experts' packed
-    weights."""
+    M=512 tokens, `fmt` expert weights.  Timed unit = one layer: router +
+    gate/up + down launches (``routed``: moe_route_forward, one native call
+    whose router also builds the lists and the fp16 copy of x; else
+    route_topk_device + moe_forward, five launches); HBM-bound on the routed
+    experts' packed weights."""
     from fastllm_py.expert_router import route_topk_device
     from fastllm_py.kernels import moe_int4
 
@@ -733,11 +735,16 @@ def run_moe_prefill(torch, lib, stream, T=512, fmt="int4", deterministic=False):
     torch.cuda.synchronize()
     distinct = len(np.unique(bufs["topk_ids"].cpu().numpy()))
     y = torch.empty((T, hidden), device="cuda")
-    ws = torch.empty((moe_int4.moe_workspace_bytes(T, hidden, inter, 0, T * K, deterministic),),
-                     dtype=torch.uint8, device="cuda")
+    ws = torch.zeros((moe_int4.moe_workspace_bytes(T, hidden, inter, 0, T * K, deterministic),),
+                     dtype=torch.uint8, device="cuda")  # zero-filled: the router's counter
 
     def mk(st):
         def go(h):
+            if routed:
+                moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, norm_topk_prob=True,
+                                           route=bufs, out=y, workspace=ws, stream=h,
+                                           deterministic=deterministic)
+                return
             route_topk_device(logits, K, norm_topk_prob=True, out=bufs, stream=h)
             moe_int4.moe_forward(x, st, E, hidden, inter, bufs, max_slots=E, max_entries=T * K,
                                  out=y, workspace=ws, stream=h, deterministic=deterministic)
@@ -750,6 +757,7 @@ def run_moe_prefill(torch, lib, stream, T=512, fmt="int4", deterministic=False):
     del layers
     torch.cuda.empty_cache()
     return {"T": T, "us_per_layer": round(us, 3), "distinct_experts": distinct,
+            "entry": "moe_route_forward" if routed else "route_topk_device + moe_forward",
             "routed_weight_bytes": routed, "weight_GB/s": round(routed / us / 1e3, 1),
             "pct_of_hbm_peak": round(routed / us / 1e3 / HBM_PEAK_GBS * 100, 2),
             "TFLOP/s": round(flops / (us * 1e-6) / 1e12, 1), **cycle(nl * routed)}

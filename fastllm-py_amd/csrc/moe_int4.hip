@@ -595,6 +595,10 @@ struct RouteArgs {
     const float* x;
     uint16_t* xh;
     int hidden, xh_blocks;
+    // batches of several routing workgroups: an arrival counter (zero before
+    // the launch, left at zero) -- the last routing workgroup builds the
+    // lists from every workgroup's picks (nullptr: route_lists_k does)
+    int* arrive;
 };
 
 // Inclusive prefix sum over the wave: shifts by 1, 2, 4, 8 inside each
@@ -1104,9 +1108,11 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
     }
     my_w = my_w * a.scale;
     if (lane < K) {
-        if (store) {
-            a.topk_ids[(size_t)t * K + lane] = my_id;
-            a.topk_w[(size_t)t * K + lane] = my_w;
+        if (store) {  // agent-coherent: the lists may be built on another XCD
+            __hip_atomic_store(a.topk_ids + (size_t)t * K + lane, my_id, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.topk_w + (size_t)t * K + lane, my_w, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         }
         sids[tl * K + lane] = my_id;
         sws[tl * K + lane] = my_w;
@@ -1149,6 +1155,119 @@ FL_DEV void one_token_lists(const RouteArgs& a, int lane, int my_id, float my_w)
         if (lane == 0) {
             a.lists.offsets[K] = K;
             *a.lists.n_active = K;
+        }
+    }
+}
+
+// MoE lists for batches routed by several workgroups (entries read from the
+// router's topk_ids / topk_w), one workgroup of 1024 threads.  Entries of an
+// expert are its tokens in ascending order (a token's K experts are
+// distinct), so entry (t, k) of expert e sits at
+//   base[e] + #{t' < t : t' chose e},
+// and that count is a popcount over a token bitmap sel[e] of the expert:
+//   1. every thread loads its entries, counts experts (LDS atomics) and sets
+//      the token bits of sel;
+//   2. the first wave scans the expert counts (slot offsets, active list)
+//      while the others form pc[e][w], the bits of sel[e] below word w;
+//   3. every entry writes itself at base[e] + pc[e][t/32] + the popcount
+//      of sel[e][t/32] below bit t%32 -- no serial walk anywhere.
+// Limits: T * K <= kListIds, E * ceil(T / 32) <= kListSel.
+constexpr int kListIds = 4096;
+constexpr int kListSel = 4096;
+// The placement of route_lists_k by NT threads of one workgroup; COHERENT:
+// the picks are read with agent-coherent loads (written by other workgroups
+// of the same launch, possibly on other XCDs).
+template <int NT, bool COHERENT>
+FL_DEV void lists_multi(const int* __restrict__ ids, const float* __restrict__ tw, int T, int K, int E,
+                        MoeLists L) {
+    constexpr int R = kListIds / NT;  // entries per thread
+    __shared__ int cnt[256];
+    __shared__ int base[256];
+    __shared__ uint32_t sel[kListSel];
+    __shared__ int pc[kListSel];
+    const int TK = T * K;
+    const int tw32 = (T + 31) >> 5;  // bitmap words per expert
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += NT) cnt[e] = 0;
+    for (int i = tid; i < E * tw32; i += NT) sel[i] = 0u;
+    int ev[R], tv[R];
+    float wv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int i = tid + NT * r;
+        const int ic = i < TK ? i : TK - 1;
+        if (COHERENT) {
+            ev[r] = __hip_atomic_load(ids + ic, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            wv[r] = __hip_atomic_load(tw + ic, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            ev[r] = ids[ic];
+            wv[r] = tw[ic];
+        }
+        tv[r] = (int)(((float)ic + 0.5f) * (1.0f / (float)K));  // ic / K (exact: ic < 2^12)
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (tid + NT * r < TK) {
+            atomicAdd(&cnt[ev[r]], 1);
+            atomicOr(&sel[ev[r] * tw32 + (tv[r] >> 5)], 1u << (tv[r] & 31));
+        }
+    }
+    __syncthreads();
+    if (tid < 64) {
+        int c[4], tot = 0, act = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * tid + q;
+            c[q] = e < E ? cnt[e] : 0;
+            tot += c[q];
+            act += c[q] > 0 ? 1 : 0;
+        }
+        int it = tot, ia = act;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int vt = __shfl_up(it, o, 64), va = __shfl_up(ia, o, 64);
+            if (tid >= o) {
+                it += vt;
+                ia += va;
+            }
+        }
+        int off = it - tot, na = ia - act;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int e = 4 * tid + q;
+            if (e < E) {
+                base[e] = off;
+                if (c[q] > 0) {
+                    L.active[na] = e;
+                    L.offsets[na] = off;
+                    ++na;
+                }
+                off += c[q];
+            }
+        }
+        if (tid == 63) {
+            L.offsets[ia] = it;
+            *L.n_active = ia;
+        }
+    } else {
+        // pc[e][w] = popcount of sel[e][0..w): one expert per thread
+        for (int e = tid - 64; e < E; e += NT - 64) {
+            int run = 0;
+            for (int w = 0; w < tw32; ++w) {
+                pc[e * tw32 + w] = run;
+                run += __popc(sel[e * tw32 + w]);
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (tid + NT * r < TK) {
+            const int e = ev[r], t = tv[r], w = e * tw32 + (t >> 5);
+            const int p = base[e] + pc[w] + __popc(sel[w] & ((1u << (t & 31)) - 1u));
+            L.tok[p] = t;
+            L.tokw[p] = wv[r];
         }
     }
 }
@@ -1197,6 +1316,20 @@ __global__ __launch_bounds__(1024) void route_k(RouteArgs a) {
         const int t = blockIdx.x * tpb + tl;
         if (tl < tpb && t < a.T) route_token<NC>(a, t, tl, lane, ex[wv], sids, sws, my_id, my_w);
     }
+    if (rb > 1 && a.arrive && a.lists.n_active) {
+        // the last routing workgroup to arrive builds the lists: each wave's
+        // pick stores are complete (agent-coherent), then one counter bump
+        __shared__ int s_last;
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (threadIdx.x == 0)
+            s_last = __hip_atomic_fetch_add(a.arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == rb - 1;
+        __syncthreads();
+        if (!s_last) return;
+        lists_multi<64 * kRouteTpb, true>(a.topk_ids, a.topk_w, a.T, a.K, a.E, a.lists);
+        if (threadIdx.x == 0) __hip_atomic_store(a.arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     if (rb == 1 && a.lists.n_active) {
         if (a.T == 1) {
             one_token_lists(a, lane, my_id, my_w);
@@ -1215,109 +1348,11 @@ void launch_route(const RouteArgs& a, int grid, int threads, hipStream_t st) {
     }
 }
 
-// MoE lists for batches routed by several workgroups (entries read from the
-// router's topk_ids / topk_w), one workgroup of 1024 threads.  Entries of an
-// expert are its tokens in ascending order (a token's K experts are
-// distinct), so entry (t, k) of expert e sits at
-//   base[e] + #{t' < t : t' chose e},
-// and that count is a popcount over a token bitmap sel[e] of the expert:
-//   1. every thread loads its entries, counts experts (LDS atomics) and sets
-//      the token bits of sel;
-//   2. the first wave scans the expert counts (slot offsets, active list)
-//      while the others form pc[e][w], the bits of sel[e] below word w;
-//   3. every entry writes itself at base[e] + pc[e][t/32] + the popcount
-//      of sel[e][t/32] below bit t%32 -- no serial walk anywhere.
-// Limits: T * K <= kListIds, E * ceil(T / 32) <= kListSel.
-constexpr int kListIds = 4096;
-constexpr int kListSel = 4096;
+// The lists of a batch routed by several workgroups, one launch after the router.
 __global__ __launch_bounds__(1024) void route_lists_k(const int* __restrict__ ids,
                                                       const float* __restrict__ tw, int T, int K,
                                                       int E, MoeLists L) {
-    constexpr int R = kListIds / 1024;  // entries per thread
-    __shared__ int cnt[256];
-    __shared__ int base[256];
-    __shared__ uint32_t sel[kListSel];
-    __shared__ int pc[kListSel];
-    const int TK = T * K;
-    const int tw32 = (T + 31) >> 5;  // bitmap words per expert
-    const int tid = threadIdx.x;
-    for (int e = tid; e < E; e += 1024) cnt[e] = 0;
-    for (int i = tid; i < E * tw32; i += 1024) sel[i] = 0u;
-    int ev[R], tv[R];
-    float wv[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int i = tid + 1024 * r;
-        const int ic = i < TK ? i : TK - 1;
-        ev[r] = ids[ic];
-        wv[r] = tw[ic];
-        tv[r] = ic / K;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if (tid + 1024 * r < TK) {
-            atomicAdd(&cnt[ev[r]], 1);
-            atomicOr(&sel[ev[r] * tw32 + (tv[r] >> 5)], 1u << (tv[r] & 31));
-        }
-    }
-    __syncthreads();
-    if (tid < 64) {
-        int c[4], tot = 0, act = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int e = 4 * tid + q;
-            c[q] = e < E ? cnt[e] : 0;
-            tot += c[q];
-            act += c[q] > 0 ? 1 : 0;
-        }
-        int it = tot, ia = act;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int vt = __shfl_up(it, o, 64), va = __shfl_up(ia, o, 64);
-            if (tid >= o) {
-                it += vt;
-                ia += va;
-            }
-        }
-        int off = it - tot, na = ia - act;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int e = 4 * tid + q;
-            if (e < E) {
-                base[e] = off;
-                if (c[q] > 0) {
-                    L.active[na] = e;
-                    L.offsets[na] = off;
-                    ++na;
-                }
-                off += c[q];
-            }
-        }
-        if (tid == 63) {
-            L.offsets[ia] = it;
-            *L.n_active = ia;
-        }
-    } else {
-        // pc[e][w] = popcount of sel[e][0..w): one expert per thread
-        for (int e = tid - 64; e < E; e += 1024 - 64) {
-            int run = 0;
-            for (int w = 0; w < tw32; ++w) {
-                pc[e * tw32 + w] = run;
-                run += __popc(sel[e * tw32 + w]);
-            }
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if (tid + 1024 * r < TK) {
-            const int e = ev[r], t = tv[r], w = e * tw32 + (t >> 5);
-            const int p = base[e] + pc[w] + __popc(sel[w] & ((1u << (t & 31)) - 1u));
-            L.tok[p] = t;
-            L.tokw[p] = wv[r];
-        }
-    }
+    lists_multi<1024, false>(ids, tw, T, K, E, L);
 }
 
 // MoE lists from an explicit slot list: slot s is expert cand[s] (or s when
@@ -3050,7 +3085,15 @@ struct MoePlan {
     bool gu_ns;       // gate/up by the column-split kernel (moe_gate_up_ns), nch_gu chunks
     int nch_gu;
     size_t lds_gun;
+    size_t inter_off;   // workspace offset of inter_buf (after the counter region)
 };
+
+// The first kMoeCounterBytes of every fused-MoE workspace hold the routed
+// entry's arrival counter (batches above 16 tokens).  Every plan leaves them
+// out, so a workspace shared by calls of any shape keeps them as the last
+// call left them: zero, once the workspace was zero-filled before its first
+// use.
+constexpr size_t kMoeCounterBytes = 256;
 
 // The deterministic combine's term rows after the rest of the workspace:
 // (max_entries + nq T) x hidden fp32, 256-byte aligned.
@@ -3074,7 +3117,8 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
     p.grouped = T > 16;
     p.xh_off = 0;
     p.inter_pad = inter > shared_inter ? inter : shared_inter;
-    p.bytes = (size_t)(max_entries + T) * p.inter_pad * 2;
+    p.inter_off = kMoeCounterBytes;
+    p.bytes = p.inter_off + (size_t)(max_entries + T) * p.inter_pad * 2;
     if (p.grouped) {
         // + the fp16 copy of x, 256-byte aligned after inter_buf
         p.xh_off = (p.bytes + 255) & ~(size_t)255;
@@ -3106,7 +3150,7 @@ bool moe_plan(int T, int hidden, int inter, int shared_inter, int max_entries, M
     p.pieces = shared_inter > 0 ? (shared_inter / 128 + span - 1) / span : 0;
     p.lds_d = (size_t)p.waves_d * p.trd * 1024;
     p.inter_pad = inter > shared_inter ? inter : shared_inter;
-    p.bytes = (size_t)(max_entries + T) * p.inter_pad * 2;
+    p.bytes = p.inter_off + (size_t)(max_entries + T) * p.inter_pad * 2;
     if (T > kGuOwnT) {  // + the fp16 copy of x the gate/up kernel stages from
         p.xh_off = (p.bytes + 255) & ~(size_t)255;
         p.bytes = p.xh_off + (size_t)T * hidden * 2;
@@ -3196,8 +3240,9 @@ void launch_combine(const MoeArgs& a, hipStream_t st) {
 
 void moe_launch_grouped(const MoeArgs& a, hipStream_t st) {
     const int n8 = a.T * a.hidden / 8;
-    hipLaunchKernelGGL(x_to_f16_k, dim3((n8 + 255) / 256 < 1024 ? (n8 + 255) / 256 : 1024), dim3(256), 0,
-                       st, a.x, const_cast<uint16_t*>(a.xh), n8);
+    if (!a.xh_ready)
+        hipLaunchKernelGGL(x_to_f16_k, dim3((n8 + 255) / 256 < 1024 ? (n8 + 255) / 256 : 1024), dim3(256), 0,
+                           st, a.x, const_cast<uint16_t*>(a.xh), n8);
     const int slots = a.max_slots + (a.has_shared ? 1 : 0);
     const int inter_max = a.routed.inter > a.shared.inter ? a.routed.inter : a.shared.inter;
     const dim3 gu(inter_max / (16 * kMgWaves), slots), dn(a.hidden / (32 * kMgWaves), slots);
@@ -3452,7 +3497,7 @@ static int moe_fused_impl(const float* x, int T, int hidden, int group_size, int
     a.max_slots = max_slots;
     a.max_entries = max_entries;
     a.inter_pad = p.inter_pad;
-    a.inter_buf = static_cast<uint16_t*>(workspace);
+    a.inter_buf = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + p.inter_off);
     a.xh = p.xh_off ? reinterpret_cast<const uint16_t*>(static_cast<char*>(workspace) + p.xh_off)
                     : nullptr;
     a.xh_ready = xh_ready ? 1 : 0;
@@ -3508,8 +3553,11 @@ int fastllm_moe_lowp_fused(int format, const float* x, int T, int hidden, int gr
                           true, nullptr, false, format);
 }
 
-// Router + fused MoE of T <= 16 tokens (body of fastllm_moe_int4_routed and
-// of its static-scratch variant).  `scratch_of`, when given, supplies the
+// Router + fused MoE (body of fastllm_moe_int4_routed and of its
+// static-scratch variant): up to 16 tokens the decode kernels, above that
+// the grouped GEMMs, the router's spare workgroups writing the fp16 copy of
+// x and its last routing workgroup the lists (a counter in the workspace,
+// which must be zero-filled once; every call leaves it at zero).  `scratch_of`, when given, supplies the
 // workspace once every argument has been validated (nullptr -> rc 2).
 static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm,
                            float routed_scaling, const float* e_score_bias, int n_group,
@@ -3524,8 +3572,9 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
                            const uint32_t* sdsz, void* workspace, size_t workspace_bytes,
                            float* y, void* stream, void* (*scratch_of)() = nullptr,
                            int fmt = kFmtInt4, int flags = 0) {
-    if (!logits || T <= 0 || T > 16 || E <= 0 || E > 256 || top_k <= 0 || top_k > 16 || top_k > E)
-        return 1;
+    if (!logits || T <= 0 || E <= 0 || E > 256 || top_k <= 0 || top_k > 16 || top_k > E) return 1;
+    // above 16 tokens the router's last workgroup builds the lists in LDS
+    if (T > 16 && ((long)T * top_k > kListIds || (long)E * ((T + 31) / 32) > kListSel)) return 1;
     if (!topk_ids || !topk_w || !n_active || !active || !offsets || !tok || !tokw) return 1;
     if (scoring != 0 && scoring != 1) return 1;
     if (n_group > 1 && (E % n_group || n_group > 64)) return 1;
@@ -3569,15 +3618,20 @@ static int moe_routed_impl(const float* logits, int top_k, int scoring, int norm
     moe_plan(T, hidden, inter, shared_inter > 0 ? shared_inter : 0, max_entries, p, fmt,
              (flags & kMoeDeterministic) != 0);
     RouteArgs rx = r;
+    // routing workgroups: one of T waves (T <= 16), else kRouteTpb tokens
+    // each, the last to finish building the lists
+    const int tpw = T <= 16 ? T : kRouteTpb;
+    const int rgrid = T <= 16 ? 1 : (T + kRouteTpb - 1) / kRouteTpb;
+    if (T > 16) rx.arrive = static_cast<int*>(workspace);  // the counter region
     if (p.xh_off) {
         rx.x = x;
         rx.xh = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + p.xh_off);
         rx.hidden = hidden;
-        const int n8 = T * hidden / 8, per = 64 * T;
+        const int n8 = T * hidden / 8, per = 64 * tpw;
         rx.xh_blocks = (n8 + per - 1) / per;
     }
     hipStream_t st = (hipStream_t)stream;
-    launch_route(rx, 1 + rx.xh_blocks, 64 * T, st);
+    launch_route(rx, rgrid + rx.xh_blocks, 64 * tpw, st);
     const int rr = finish("fastllm_moe_int4_routed");
     if (rr) return rr;
     return moe_fused_impl(x, T, hidden, group_size, E, inter, gq, gsz, uq, usz, dq, dsz,

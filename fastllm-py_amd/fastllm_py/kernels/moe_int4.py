@@ -448,11 +448,15 @@ def moe_route_forward(x, logits, stacked, top_k, E, hidden, inter, *, norm_topk_
                       scoring="softmax", routed_scaling=1.0, e_score_bias=None, n_group=0,
                       topk_group=0, shared=None, shared_inter=0, shared_logit=None, route=None,
                       out=None, workspace=None, stream=None, deterministic=False):
-    """Router + fused MoE of T <= 16 tokens in one native call: routes
-    ``logits`` (T, E) exactly like ``route_topk_device`` (same keyword
-    meaning, same outputs, which land in ``route``: topk_ids, topk_w, rw,
-    lists, shared_coef) and returns y (T, hidden) fp32 = moe_forward over
-    those lists (graph_decode._moe_branch, graph_decode.py:669-700).
+    """Router + fused MoE in one native call: routes ``logits`` (T, E)
+    exactly like ``route_topk_device`` (same keyword meaning, same outputs,
+    which land in ``route``: topk_ids, topk_w, rw, lists, shared_coef) and
+    returns y (T, hidden) fp32 = moe_forward over those lists
+    (graph_decode._moe_branch, graph_decode.py:669-700).  Up to 16 tokens
+    the decode kernels; above, the router's last workgroup builds the lists
+    and the grouped GEMMs follow (three launches), which keeps an arrival
+    counter in the workspace: a ``workspace`` passed in must have been
+    zero-filled before its first use (calls leave the counter at zero).
     ``route`` / ``workspace`` / ``out`` may carry persistent buffers for
     graph capture.  ``deterministic``: the ordered combine of moe_forward
     (bit-identical repeats, one more launch)."""
@@ -460,9 +464,6 @@ def moe_route_forward(x, logits, stacked, top_k, E, hidden, inter, *, norm_topk_
     xd = nat.to_device(x, t.float32)
     x2 = xd.reshape(-1, hidden).contiguous()
     T = x2.shape[0]
-    if T > 16:
-        raise ValueError("moe_route_forward: at most 16 tokens (route_topk_device + moe_forward "
-                         "take larger batches)")
     s = nat.to_device(logits)
     if s.dtype != t.float32:
         s = s.to(t.float32)
@@ -494,7 +495,7 @@ def moe_route_forward(x, logits, stacked, top_k, E, hidden, inter, *, norm_topk_
     need = moe_workspace_bytes(T, hidden, inter, sint, T * top_k, deterministic)
     ws = workspace
     if ws is None or ws.numel() * ws.element_size() < need or not ws.is_contiguous():
-        ws = t.empty((need,), dtype=t.uint8, device=dev)
+        ws = t.zeros((need,), dtype=t.uint8, device=dev)  # zero: the router's counter
     y = out if out is not None else t.empty((T, hidden), dtype=t.float32, device=dev)
     h = nat.stream_handle(stream) if stream is not None else nat.current_stream_handle()
     args = _routed_args(s, top_k, scoring, norm_topk_prob, routed_scaling, bias, n_group,
@@ -565,9 +566,9 @@ def moe_route_forward_noalloc(x, logits, stacked, top_k, E, hidden, inter, *, ro
             raise ValueError(f"moe_route_forward_noalloc: {name} must be a contiguous fp32 "
                              f"device tensor")
     T = x.numel() // hidden
-    if T > 16 or x.numel() != T * hidden or logits.numel() != T * E or out.numel() != T * hidden:
+    if T < 1 or x.numel() != T * hidden or logits.numel() != T * E or out.numel() != T * hidden:
         raise ValueError("moe_route_forward_noalloc: x (T, hidden), logits (T, E) and out "
-                         "(T, hidden) with T <= 16")
+                         "(T, hidden)")
     # the optional per-token / per-expert vectors reach the kernel as raw
     # pointers too: same checks, with their lengths
     for name, v, n in (("shared_logit", shared_logit, T), ("e_score_bias", e_score_bias, E)):
@@ -662,13 +663,10 @@ def moe_branch(x, gate_w, stacked, top_k, *, E, hidden, inter, norm=False, scale
                shared=None, shared_inter=0, shared_gate_w=None, bufs=None, stream=None):
     """One fused MoE layer, all on the device with no host sync
     (graph_decode._moe_branch, graph_decode.py:669-700): gate matvec (+
-    shared gate) -> router -> fused routed + shared FFN (one native call for
-    T <= 16 tokens).
+    shared gate) -> router -> fused routed + shared FFN (one native call).
     Returns (T, hidden) fp32.  ``bufs`` may carry persistent buffers for
     graph capture (keys of route_topk_device plus logits, slogit, workspace,
     out); missing ones are allocated and stored there."""
-    from ..expert_router import route_topk_device
-
     t = nat.torch()
     xd = nat.to_device(x, t.float32).reshape(-1, hidden).contiguous()
     T = xd.shape[0]
@@ -689,26 +687,14 @@ def moe_branch(x, gate_w, stacked, top_k, *, E, hidden, inter, norm=False, scale
                                        nat.ptr(logits), nat.ptr(sl) if sl is not None else None,
                                        T, E, hidden, h)
     nat.check_rc(rc, "fastllm_gate_matvec")
-    if T <= 16:
-        if "workspace" not in b:
-            b["workspace"] = t.empty((moe_workspace_bytes(T, hidden, inter,
-                                                          shared_inter if shared is not None else 0,
-                                                          T * top_k),),
-                                     dtype=t.uint8, device=xd.device)
-        if "out" not in b:
-            b["out"] = t.empty((T, hidden), dtype=t.float32, device=xd.device)
-        return moe_route_forward(xd, logits, stacked, top_k, E, hidden, inter,
-                                 norm_topk_prob=norm, routed_scaling=scale, shared=shared,
-                                 shared_inter=shared_inter, shared_logit=sl, route=b,
-                                 out=b["out"], workspace=b["workspace"], stream=stream)
-    r = route_topk_device(logits, top_k, norm_topk_prob=norm, routed_scaling=scale,
-                          shared_logit=sl, out=b, stream=stream)
-    if "workspace" not in b:
-        b["workspace"] = t.empty((moe_workspace_bytes(T, hidden, inter,
+    if "workspace" not in b:  # zero-filled: the router's arrival counter above 16 tokens
+        b["workspace"] = t.zeros((moe_workspace_bytes(T, hidden, inter,
                                                       shared_inter if shared is not None else 0,
                                                       T * top_k),),
                                  dtype=t.uint8, device=xd.device)
-    return moe_forward(xd, stacked, E, hidden, inter, r, max_slots=min(E, T * top_k),
-                       max_entries=T * top_k, shared=shared, shared_inter=shared_inter,
-                       shared_coef=r.get("shared_coef") if shared_gate_w is not None else None,
-                       out=b.get("out"), workspace=b["workspace"], stream=stream)
+    if "out" not in b:
+        b["out"] = t.empty((T, hidden), dtype=t.float32, device=xd.device)
+    return moe_route_forward(xd, logits, stacked, top_k, E, hidden, inter,
+                             norm_topk_prob=norm, routed_scaling=scale, shared=shared,
+                             shared_inter=shared_inter, shared_logit=sl, route=b,
+                             out=b["out"], workspace=b["workspace"], stream=stream)

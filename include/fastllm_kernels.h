@@ -512,13 +512,18 @@ int fastllm_moe_int4_fused(const float *x, int T, int hidden, int group_size,
                            int max_entries, void *workspace,
                            size_t workspace_bytes, float *y, void *stream);
 
-/* Router + fused MoE of T <= 16 tokens in one call: fastllm_route_topk
- * (same arguments, same outputs topk_ids/topk_w/rw/shared_coef and lists,
- * bit for bit) followed by fastllm_moe_int4_fused over its lists with
- * max_slots = min(E, T * top_k), max_entries = T * top_k and, when
- * shared_logit is given, shared_coef = sigmoid(shared_logit) (shared_coef
- * must then be given).  Every argument is checked before the first launch.
- * Expert arguments and workspace as fastllm_moe_int4_fused.
+/* Router + fused MoE in one call: fastllm_route_topk (same arguments, same
+ * outputs topk_ids/topk_w/rw/shared_coef and lists, bit for bit) followed by
+ * fastllm_moe_int4_fused over its lists with max_slots = min(E, T * top_k),
+ * max_entries = T * top_k and, when shared_logit is given, shared_coef =
+ * sigmoid(shared_logit) (shared_coef must then be given).  Every argument is
+ * checked before the first launch.  Expert arguments and workspace as
+ * fastllm_moe_int4_fused.  Above 16 tokens (T * top_k <= 4096,
+ * E * ceil(T / 32) <= 4096) the router's last workgroup builds the lists and
+ * its spare workgroups write the fp16 copy of x, so the call is three
+ * launches; the workspace then holds the router's arrival counter and must
+ * be zero-filled before its first use (every call leaves the counter at
+ * zero).
  * Replaces: the router + routed/shared expert launches of _moe_branch
  * (fastllm_py/graph_decode.py:669-700). */
 int fastllm_moe_int4_routed(const float *logits, int top_k, int scoring,
@@ -542,7 +547,7 @@ int fastllm_moe_int4_routed(const float *logits, int top_k, int scoring,
 /* The fused MoE with FP8 or MXFP4 expert weights: the decode kernels up to
  * 16 tokens, the grouped MFMA kernels above (the workspace is sized as for
  * INT4 by fastllm_moe_int4_workspace_bytes; fastllm_moe_lowp_routed takes
- * T <= 16 like fastllm_moe_int4_routed).  format FASTLLM_MOE_FP8 (group_size
+ * the batches of fastllm_moe_int4_routed, with the same workspace rule).  format FASTLLM_MOE_FP8 (group_size
  * must be 128): gq/uq/dq are the FP8 tiles and gsz/usz/dsz the f32 block
  * scales (passed as uint32 pointers); FASTLLM_MOE_MXFP4 (group_size 32):
  * the MXFP4 tiles and scale words.  The codes become fp16 exactly and run on

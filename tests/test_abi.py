@@ -47,7 +47,7 @@ def test_moe_entry_argument_checks():
     lib = _native.lib()
     p = 1 << 20  # never dereferenced: validation fails or stops at the device check
     ws = lib.fastllm_moe_int4_workspace_bytes(1, 2048, 1408, 5632, 4)
-    assert ws == (4 + 1) * 5632 * 2
+    assert ws == 256 + (4 + 1) * 5632 * 2  # the counter region, then inter_buf
     # T > 16 takes the grouped kernels (hidden % 256 == 0)
     assert lib.fastllm_moe_int4_workspace_bytes(17, 2048, 1408, 0, 68) > 0
     assert lib.fastllm_moe_int4_workspace_bytes(17, 384, 1408, 0, 68) == 0

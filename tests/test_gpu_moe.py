@@ -748,3 +748,83 @@ def test_moe_prefill_config5(torch_gpu):
                              max_slots=E, max_entries=T * K)
     ref = OM.moe_ref_grouped(x, OM.dequant_stacked(st_o, 128), ids, w)
     assert Q.max_abs_rel(y.cpu().numpy(), ref) < 5e-3
+    # the one-call routed entry (router's last workgroup builds the lists):
+    # the same routing and lists bit for bit, y up to the atomic order
+    o = {}
+    ws = torch.zeros(moe_int4.moe_workspace_bytes(T, hidden, inter, 0, T * K), dtype=torch.uint8,
+                     device="cuda")
+    for _ in range(2):  # the second call finds the arrival counter back at zero
+        y2 = moe_int4.moe_route_forward(torch.from_numpy(x).cuda(), torch.from_numpy(g["logits"]).cuda(),
+                                        st, K, E, hidden, inter, norm_topk_prob=True, route=o,
+                                        workspace=ws)
+        torch.cuda.synchronize()
+        _assert_same_lists(o, r)
+        assert Q.max_abs_rel(y2.cpu().numpy(), y.cpu().numpy()) < 1e-6
+
+
+def _assert_same_lists(a, b):
+    """Router outputs and MoE lists of two routings are identical."""
+    for k in ("topk_ids", "topk_w", "n_active"):
+        np.testing.assert_array_equal(a[k].cpu().numpy(), b[k].cpu().numpy(), err_msg=k)
+    na = int(a["n_active"].item())
+    np.testing.assert_array_equal(a["active"].cpu().numpy()[:na], b["active"].cpu().numpy()[:na])
+    off = a["offsets"].cpu().numpy()[:na + 1]
+    np.testing.assert_array_equal(off, b["offsets"].cpu().numpy()[:na + 1])
+    n = int(off[-1])
+    np.testing.assert_array_equal(a["tok"].cpu().numpy()[:n], b["tok"].cpu().numpy()[:n])
+    np.testing.assert_array_equal(a["tokw"].cpu().numpy()[:n], b["tokw"].cpu().numpy()[:n])
+
+
+@pytest.mark.parametrize("T,E,K,hidden,inter,sinter,gs,norm", [
+    (17, 8, 2, 256, 256, 0, 128, True),      # five routing workgroups, the last holds one token
+    (64, 16, 4, 512, 384, 1024, 64, False),  # shared expert with its sigmoid gate, group 64
+    (300, 60, 4, 512, 256, 512, 128, False),  # E = 60 (one expert per lane)
+    (200, 256, 8, 256, 256, 0, 128, True),   # E = 256, ragged 32-token bitmap words
+])
+def test_routed_prefill(torch_gpu, T, E, K, hidden, inter, sinter, gs, norm):
+    """moe_route_forward above 16 tokens (one native call: router whose last
+    workgroup builds the lists while spare workgroups write the fp16 copy of
+    x, then the grouped GEMMs) against route_topk_device + moe_forward: the
+    same router outputs and lists bit for bit, y up to the atomic order, on
+    three calls through one workspace (the arrival counter is left at zero);
+    the deterministic combine bit-identical on a repeat; the no-alloc entry
+    equal to the allocating one."""
+    from fastllm_py.expert_router import route_topk_device
+    from fastllm_py.kernels import moe_int4
+
+    torch = torch_gpu
+    rng = np.random.default_rng(T * 7 + E + hidden)
+    st, st_o = _stacked(_experts(rng, E, hidden, inter, 0.05), gs)
+    sh, _ = _stacked(_experts(rng, 1, hidden, sinter, 0.05), gs) if sinter else (None, None)
+    x = torch.from_numpy((rng.standard_normal((T, hidden)) * 0.5).astype(np.float32)).cuda()
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float16).astype(np.float32)).cuda()
+    sl = torch.from_numpy(rng.standard_normal(T).astype(np.float32)).cuda() if sinter else None
+    r = route_topk_device(logits, K, norm_topk_prob=norm, shared_logit=sl)
+    kw = dict(shared=sh, shared_inter=sinter)
+    y_ref = moe_int4.moe_forward(x, st, E, hidden, inter, r, max_slots=min(E, T * K),
+                                 max_entries=T * K, shared_coef=r.get("shared_coef"), **kw)
+    ws = torch.zeros(moe_int4.moe_workspace_bytes(T, hidden, inter, sinter, T * K), dtype=torch.uint8,
+                     device="cuda")
+    o = {}
+    for _ in range(3):
+        y = moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, norm_topk_prob=norm,
+                                       shared_logit=sl, route=o, workspace=ws, **kw)
+        torch.cuda.synchronize()
+        _assert_same_lists(o, r)
+        if sinter:
+            np.testing.assert_array_equal(o["shared_coef"].cpu().numpy(), r["shared_coef"].cpu().numpy())
+        assert Q.max_abs_rel(y.cpu().numpy(), y_ref.cpu().numpy()) < 1e-6
+    od = {}
+    yd = [moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, norm_topk_prob=norm,
+                                     shared_logit=sl, route=od, deterministic=True, **kw)
+          for _ in range(2)]
+    torch.cuda.synchronize()
+    assert torch.equal(yd[0], yd[1])
+    assert Q.max_abs_rel(yd[0].cpu().numpy(), y_ref.cpu().numpy()) < 1e-5
+    bufs = moe_int4.alloc_route_buffers(T, E, K)
+    out = torch.empty((T, hidden), dtype=torch.float32, device="cuda")
+    moe_int4.moe_route_forward_noalloc(x, logits, st, K, E, hidden, inter, route=bufs, out=out,
+                                       norm_topk_prob=norm, shared_logit=sl, **kw)
+    torch.cuda.synchronize()
+    _assert_same_lists(bufs, r)
+    assert Q.max_abs_rel(out.cpu().numpy(), y_ref.cpu().numpy()) < 1e-6
