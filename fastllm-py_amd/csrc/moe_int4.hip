@@ -787,67 +787,80 @@ FL_DEV float bperm_f(float v, int src_lane) {
     return bitcast<float>(__builtin_amdgcn_ds_bpermute(src_lane << 2, bitcast<int>(v)));
 }
 
-// One network step.  part(c, &pc, &pl, &mx): partner slot pc (uniform) and
-// lane pl of this lane's slot-c position, mx = keep the max.
-template <typename Part>
-FL_DEV void net_step(float (&kf)[4], int (&ix)[4], int nsl, Part part) {
-    float nk[4];
-    int ni[4];
+// One cross-register network step over the NSL slots in use: part(c, &pc,
+// &pl, &mx) gives the partner slot pc (uniform) and lane pl of this lane's
+// slot-c position, mx = keep the max.  Every slot's partner reads issue
+// before the first compare.
+template <int NSL, typename Part>
+FL_DEV void net_step(float (&kf)[4], int (&ix)[4], Part part) {
+    float ok[NSL];
+    int oi[NSL];
+    bool mxv[NSL];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        nk[c] = kf[c];
-        ni[c] = ix[c];
-        if (c < nsl) {
-            int pc, pl;
-            bool mx;
-            part(c, pc, pl, mx);
-            const float sk = pc == 0 ? kf[0] : pc == 1 ? kf[1] : pc == 2 ? kf[2] : kf[3];
-            const int si = pc == 0 ? ix[0] : pc == 1 ? ix[1] : pc == 2 ? ix[2] : ix[3];
-            const float ok = bperm_f(sk, pl);
-            const int oi = __builtin_amdgcn_ds_bpermute(pl << 2, si);
-            const float r = mx ? fmaxf(kf[c], ok) : fminf(kf[c], ok);
-            nk[c] = r;
-            ni[c] = r == kf[c] ? ix[c] : oi;
-        }
+    for (int c = 0; c < NSL; ++c) {
+        int pc, pl;
+        bool mx;
+        part(c, pc, pl, mx);
+        const float sk = pc == 0 ? kf[0] : pc == 1 ? kf[1] : pc == 2 ? kf[2] : kf[3];
+        const int si = pc == 0 ? ix[0] : pc == 1 ? ix[1] : pc == 2 ? ix[2] : ix[3];
+        ok[c] = bperm_f(sk, pl);
+        oi[c] = __builtin_amdgcn_ds_bpermute(pl << 2, si);
+        mxv[c] = mx;
     }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        kf[c] = nk[c];
-        ix[c] = ni[c];
+    for (int c = 0; c < NSL; ++c) {
+        const float r = mxv[c] ? fmaxf(kf[c], ok[c]) : fminf(kf[c], ok[c]);
+        ix[c] = r == kf[c] ? ix[c] : oi[c];
+        kf[c] = r;
     }
 }
 
-// In-register step: partner lane l -> perm(l) inside each 8-lane register,
-// max where `mask` has bit l.
-template <typename Perm>
-FL_DEV void net_lane_step(float (&kf)[4], int (&ix)[4], int nsl, int lane, Perm perm, int mask) {
-    const int l = lane & 7;
-    const int pl = (lane & ~7) | perm(l);
-    const bool mx = (mask >> l) & 1;
-    net_step(kf, ix, nsl, [&](int c, int& pc, int& plo, bool& m) {
-        pc = c;
-        plo = pl;
-        m = mx;
-    });
+// Partners inside 8-lane registers by DPP: l ^ 1, l ^ 2, 3 - l within four,
+// 7 - l (half-row mirror), l ^ 4 (a shift left or right by four inside the
+// 16-lane row, picked by lane bit 2).
+enum { kNetX1, kNetX2, kNetR4, kNetR8, kNetX4 };
+template <int P>
+FL_DEV int net_dpp(int v, int lane) {
+    if constexpr (P == kNetX1) return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm 1,0,3,2
+    else if constexpr (P == kNetX2) return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+    else if constexpr (P == kNetR4) return __builtin_amdgcn_update_dpp(0, v, 0x1B, 0xF, 0xF, false);  // quad_perm 3,2,1,0
+    else if constexpr (P == kNetR8) return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    else {
+        const int up = __builtin_amdgcn_update_dpp(0, v, 0x104, 0xF, 0xF, false);  // row_shl:4: lane l + 4
+        const int dn = __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4: lane l - 4
+        return (lane & 4) ? dn : up;
+    }
 }
 
-// Full network over maxN (8..256) positions held as described above.
+// In-register step: partner P inside each 8-lane register, max where
+// `mask` has bit l % 8.
+template <int NSL, int P>
+FL_DEV void net_lane_step(float (&kf)[4], int (&ix)[4], int lane, int mask) {
+    const bool mx = (mask >> (lane & 7)) & 1;
+#pragma unroll
+    for (int c = 0; c < NSL; ++c) {
+        const float ok = bitcast<float>(net_dpp<P>(bitcast<int>(kf[c]), lane));
+        const int oi = net_dpp<P>(ix[c], lane);
+        const float r = mx ? fmaxf(kf[c], ok) : fminf(kf[c], ok);
+        ix[c] = r == kf[c] ? ix[c] : oi;
+        kf[c] = r;
+    }
+}
+
+// Full network over maxN (8..64 NSL) positions held as described above.
+template <int NSL>
 FL_DEV void net_argsort(float (&kf)[4], int (&ix)[4], int maxN, int lane) {
-    const int nsl = (maxN + 63) >> 6;
     const int nv = maxN >> 3;
-    auto sort8 = [&]() {
-        net_lane_step(kf, ix, nsl, lane, [](int l) { return l ^ 1; }, 0xAA);
-        net_lane_step(kf, ix, nsl, lane, [](int l) { return (l & 4) | (3 - (l & 3)); }, 0xCC);
-        net_lane_step(kf, ix, nsl, lane, [](int l) { return l ^ 1; }, 0xAA);
-        net_lane_step(kf, ix, nsl, lane, [](int l) { return 7 - l; }, 0xF0);
-        net_lane_step(kf, ix, nsl, lane, [](int l) { return l ^ 2; }, 0xCC);
-        net_lane_step(kf, ix, nsl, lane, [](int l) { return l ^ 1; }, 0xAA);
-    };
-    sort8();
+    net_lane_step<NSL, kNetX1>(kf, ix, lane, 0xAA);
+    net_lane_step<NSL, kNetR4>(kf, ix, lane, 0xCC);
+    net_lane_step<NSL, kNetX1>(kf, ix, lane, 0xAA);
+    net_lane_step<NSL, kNetR8>(kf, ix, lane, 0xF0);
+    net_lane_step<NSL, kNetX2>(kf, ix, lane, 0xCC);
+    net_lane_step<NSL, kNetX1>(kf, ix, lane, 0xAA);
     const int l = lane & 7;
     for (int n = 2; n <= nv; n <<= 1) {
         // register R against register g + n - 1 - (R - g), lanes reversed
-        net_step(kf, ix, nsl, [&](int c, int& pc, int& pl, bool& mx) {
+        net_step<NSL>(kf, ix, [&](int c, int& pc, int& pl, bool& mx) {
             const int R = 8 * c + (lane >> 3);
             const int g = R & ~(n - 1), a = R - g;
             const int R2 = g + n - 1 - a;
@@ -857,7 +870,7 @@ FL_DEV void net_argsort(float (&kf)[4], int (&ix)[4], int maxN, int lane) {
         });
         for (int m = n >> 1; m >= 2; m >>= 1) {
             const int d = m >> 1;
-            net_step(kf, ix, nsl, [&](int c, int& pc, int& pl, bool& mx) {
+            net_step<NSL>(kf, ix, [&](int c, int& pc, int& pl, bool& mx) {
                 const int R = 8 * c + (lane >> 3);
                 const bool hi = (R & (m - 1)) >= d;  // m: a power of two
                 const int R2 = hi ? R - d : R + d;
@@ -866,16 +879,17 @@ FL_DEV void net_argsort(float (&kf)[4], int (&ix)[4], int maxN, int lane) {
                 pl = ((R2 & 7) << 3) | l;
             });
         }
-        net_lane_step(kf, ix, nsl, lane, [](int q) { return q ^ 4; }, 0xF0);
-        net_lane_step(kf, ix, nsl, lane, [](int q) { return q ^ 2; }, 0xCC);
-        net_lane_step(kf, ix, nsl, lane, [](int q) { return q ^ 1; }, 0xAA);
+        net_lane_step<NSL, kNetX4>(kf, ix, lane, 0xF0);
+        net_lane_step<NSL, kNetX2>(kf, ix, lane, 0xCC);
+        net_lane_step<NSL, kNetX1>(kf, ix, lane, 0xAA);
     }
 }
 
-// Keys -v (numpy's -select) of n values (lane + 64 c), padded to the
-// network's size, sorted; returns maxN.  Inlined: called out of line it cost
-// config 5's router (T = 512, 18 tied tokens) 7.6 us, and the smaller routing
-// code it gave the one-token path measured no faster.
+// Keys -v (numpy's -select) of n <= 64 NSL values (lane + 64 c), padded to
+// the network's size, sorted; returns maxN.  Inlined: called out of line it
+// cost config 5's router (T = 512, 18 tied tokens) 7.6 us, and the smaller
+// routing code it gave the one-token path measured no faster.
+template <int NSL>
 FL_DEV int net_load_sort(const float (&v)[4], int n, int lane, float (&kf)[4], int (&ix)[4]) {
     int maxN = 8;
     while (maxN < n) maxN <<= 1;
@@ -885,7 +899,7 @@ FL_DEV int net_load_sort(const float (&v)[4], int n, int lane, float (&kf)[4], i
         kf[c] = x < n ? -v[c] : __builtin_inff();
         ix[c] = x < n ? x : 0;
     }
-    net_argsort(kf, ix, maxN, lane);
+    net_argsort<NSL>(kf, ix, maxN, lane);
     return maxN;
 }
 
@@ -996,7 +1010,7 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
         if (__ballot(lane < a.n_group && same > 0)) {
             float gv[4] = {gscore, 0.f, 0.f, 0.f}, kf[4];
             int ix[4];
-            net_load_sort(gv, a.n_group, lane, kf, ix);
+            net_load_sort<1>(gv, a.n_group, lane, kf, ix);
             unsigned long long km = 0ull;
             for (int j = 0; j < a.topk_group; ++j) km |= 1ull << __builtin_amdgcn_readlane(ix[0], j);
             keep = (lane < a.n_group && ((km >> lane) & 1ull)) ? 1 : 0;
@@ -1071,7 +1085,7 @@ FL_DEV void route_token(const RouteArgs& a, int t, int tl, int lane, float* exw,
         float sv[4];
 #pragma unroll
         for (int c = 0; c < 4; ++c) sv[c] = sel[c];
-        net_load_sort(sv, E, lane, kf, ix);
+        net_load_sort<(NC < 4 ? NC : 4)>(sv, E, lane, kf, ix);
         my_id = ix[0];
         float w = 0.f;
 #pragma unroll
