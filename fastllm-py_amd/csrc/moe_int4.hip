@@ -2858,18 +2858,24 @@ __global__ __launch_bounds__(64 * kMgWaves, 2) void moe_gemm_rk(MoeArgs a) {
             ao[i] = 2u * ((uint32_t)row * astride + a_koff<kFmtInt4>(kq, f & 3));
         }
         // block b: activation copies into stage b % NS, then the wave's weight
-        // and scale loads into r.  Blocks past the end keep the load count
-        // (so the compiler's waits stay exact) with lane offsets past every
-        // buffer's range: the loads return zeros without touching memory,
-        // into a retired stage and a ring slot nobody reads.
+        // and scale loads into r.  Blocks past the end keep the weight and
+        // scale load count (so the compiler's waits stay exact) with lane
+        // offsets past every buffer's range: the loads return zeros without
+        // touching memory, into a ring slot nobody reads.  They issue no
+        // activation copy: with fewer blocks than the ring is deep, no
+        // barrier separates a past-end block's stage from the waves still
+        // reading an earlier block there (the copies come from inline asm,
+        // which the compiler's waits do not count).
         auto issue = [&](MrBlk& r, int b) {
             const int kb = b < nkb ? b : nkb - 1;
             const uint32_t oob = b < nkb ? 0u : 0x80000000u;
             const uint32_t st = lds0 + (uint32_t)(b % NS) * kMgABytes;
+            if (b < nkb) {
 #pragma unroll
-            for (int i = 0; i < FPW; ++i)
-                if (wave * FPW + i < 4 * mt_live)  // dead m-tiles: no copy
-                    lds_copy(rA, st + (wave * FPW + i) * 1024, ao[i] | oob, kb * 256);
+                for (int i = 0; i < FPW; ++i)
+                    if (wave * FPW + i < 4 * mt_live)  // dead m-tiles: no copy
+                        lds_copy(rA, st + (wave * FPW + i) * 1024, ao[i], kb * 256);
+            }
 #pragma unroll
             for (int t = 0; t < 2; ++t)
                 r.w[t] = bitcast<u32x4>(__builtin_amdgcn_raw_buffer_load_b128(rq[t], (int)(16u * lane | oob),
