@@ -714,8 +714,12 @@ def test_fused_moe_prefill(torch_gpu, T, E, K, hidden, inter, sinter, gs, norm):
     kw = dict(max_slots=min(E, T * K), max_entries=T * K, shared=sh, shared_inter=sinter,
               shared_coef=r.get("shared_coef"))
     y = moe_int4.moe_forward(xd, st, E, hidden, inter, r, **kw)
-    y2 = moe_int4.moe_forward(xd, st, E, hidden, inter, r, **kw)
-    assert Q.max_abs_rel(y2.cpu().numpy(), y.cpu().numpy()) < 1e-6
+    # repeats agree up to the atomic order (the activation ring of the
+    # grouped INT4 GEMM once let a past-end copy overwrite the last block's
+    # stage under slower waves; run-to-run differences showed it)
+    for _ in range(4):
+        y2 = moe_int4.moe_forward(xd, st, E, hidden, inter, r, **kw)
+        assert Q.max_abs_rel(y2.cpu().numpy(), y.cpu().numpy()) < 1e-6
     ids, w = r["topk_ids"].cpu().numpy(), r["topk_w"].cpu().numpy()
     coef = 1.0 / (1.0 + np.exp(-sl)) if sinter else None
     ref = OM.moe_ref_grouped(x, OM.dequant_stacked(st_o, gs), ids, w,
