@@ -766,6 +766,46 @@ def test_moe_prefill_config5(torch_gpu):
         assert Q.max_abs_rel(y2.cpu().numpy(), y.cpu().numpy()) < 1e-6
 
 
+def test_routed_prefill_graph_replays(torch_gpu):
+    """The routed entry above 16 tokens captured in a HIP graph: every replay
+    (eager work and synchronisations between them) gives the eager call's
+    lists bit for bit and its y up to the atomic order -- the router's
+    arrival counter is back at zero after each replay."""
+    from fastllm_py.kernels import moe_int4
+
+    torch = torch_gpu
+    T, E, K, hidden, inter = 96, 16, 4, 512, 256
+    rng = np.random.default_rng(9601)
+    st, _ = _stacked(_experts(rng, E, hidden, inter, 0.05), 128)
+    x = torch.from_numpy((rng.standard_normal((T, hidden)) * 0.5).astype(np.float32)).cuda()
+    logits = torch.from_numpy(rng.standard_normal((T, E)).astype(np.float16).astype(np.float32)).cuda()
+    ws = torch.zeros(moe_int4.moe_workspace_bytes(T, hidden, inter, 0, T * K), dtype=torch.uint8,
+                     device="cuda")
+    eager_r = {}
+    eager = moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, route=eager_r, workspace=ws)
+    torch.cuda.synchronize()
+    r = moe_int4.alloc_route_buffers(T, E, K)
+    out = torch.empty((T, hidden), dtype=torch.float32, device="cuda")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):  # warm-up outside capture (workspace and buffers exist)
+        moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, route=r, out=out, workspace=ws,
+                                   stream=s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, route=r, out=out, workspace=ws,
+                                   stream=s)
+    for _ in range(3):
+        out.zero_()
+        for k in ("tok", "tokw", "active", "offsets"):
+            r[k].fill_(-1)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        _assert_same_lists(r, eager_r)
+        assert Q.max_abs_rel(out.cpu().numpy(), eager.cpu().numpy()) < 1e-6
+
+
 def _assert_same_lists(a, b):
     """Router outputs and MoE lists of two routings are identical."""
     for k in ("topk_ids", "topk_w", "n_active"):

@@ -211,7 +211,9 @@ def test_lowp_moe_config4_shape(torch_gpu, fmt, T):
 ])
 def test_lowp_moe_prefill_parity(torch_gpu, fmt, T, E, K, hidden, inter, sinter, norm):
     """More than 16 tokens: the grouped MFMA kernels with FP8 / MXFP4 experts
-    (router lists from route_topk_device) vs the fp32 oracle."""
+    (router lists from route_topk_device) vs the fp32 oracle, and the routed
+    entry (moe_route_forward: lists built in the router launch) against
+    them."""
     from fastllm_py.expert_router import route_topk_device
     from fastllm_py.kernels import moe_int4
 
@@ -229,6 +231,13 @@ def test_lowp_moe_prefill_parity(torch_gpu, fmt, T, E, K, hidden, inter, sinter,
                              shared_inter=sinter, shared_coef=r.get("shared_coef"))
     torch.cuda.synchronize()
     assert Q.max_abs_rel(y.cpu().numpy(), ref) < TOL, fmt
+    # the one-call routed entry: the same picks, y up to the atomic order
+    o = {}
+    y2 = moe_int4.moe_route_forward(x, logits, st, K, E, hidden, inter, norm_topk_prob=norm,
+                                    shared=sh, shared_inter=sinter, shared_logit=sl, route=o)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(o["topk_ids"].cpu().numpy(), ids)
+    assert Q.max_abs_rel(y2.cpu().numpy(), y.cpu().numpy()) < 1e-6, fmt
 
 
 def test_lowp_rejects(torch_gpu):
