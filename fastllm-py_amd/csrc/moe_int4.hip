@@ -2754,8 +2754,12 @@ __global__ __launch_bounds__(64 * kMgWaves) void moe_gemm_k(MoeArgs a) {
 // wave's copies and retires the stage of block c - 1, which the copies of
 // block c + kMrD (issued after the barrier) overwrite.
 constexpr int kMrD = 3;              // blocks in flight ahead
-constexpr int kMrStages = kMrD + 1;  // activation stages
-constexpr size_t kMrLds = (size_t)kMrStages * kMgABytes;
+// Waves per workgroup and blocks ahead of each launch.  Config 5 (INT4):
+// 8 / 3 for both 111-112 us per layer; four-wave workgroups two blocks ahead
+// (three per CU, 95 / 82 VGPRs) 119 us for down alone, 124 for gate/up
+// alone, 131 for both; three ahead at four waves 129 us.
+constexpr int kMrGuWaves = 8, kMrGuD = 3;  // gate/up: waves (16 columns each), blocks ahead
+constexpr int kMrDnWaves = 8, kMrDnD = 3;  // down: waves (32 columns each), blocks ahead
 
 template <int V>
 struct IntC {
@@ -2767,10 +2771,10 @@ struct MrBlk {
     uint32_t sz[2];  // this lane's scale|zero word of each tile
 };
 
-template <int PHASE, bool G128>
-__global__ __launch_bounds__(64 * kMgWaves, 2) void moe_gemm_rk(MoeArgs a) {
+template <int PHASE, bool G128, int NW = kMgWaves, int D = kMrD>
+__global__ __launch_bounds__(64 * NW) void moe_gemm_rk(MoeArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
-    constexpr int D = kMrD, NS = kMrStages, NW = kMgWaves, FPW = 16 / NW;
+    constexpr int NS = D + 1, FPW = 16 / NW;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, kq = lane >> 4;
@@ -3246,8 +3250,11 @@ void launch_down_ns(const MoeArgs& a, const MoePlan& p, hipStream_t st) {
 template <int FMT, bool G128>
 void launch_grouped_pair(const MoeArgs& a, dim3 gu, dim3 dn, hipStream_t st) {
     if constexpr (FMT == kFmtInt4) {
-        hipLaunchKernelGGL((moe_gemm_rk<0, G128>), gu, dim3(64 * kMgWaves), kMrLds, st, a);
-        hipLaunchKernelGGL((moe_gemm_rk<1, G128>), dn, dim3(64 * kMgWaves), kMrLds, st, a);
+        constexpr int GW = kMrGuWaves, GD = kMrGuD, DW = kMrDnWaves, DD = kMrDnD;
+        hipLaunchKernelGGL((moe_gemm_rk<0, G128, GW, GD>), dim3(gu.x * kMgWaves / GW, gu.y), dim3(64 * GW),
+                           (size_t)(GD + 1) * kMgABytes, st, a);
+        hipLaunchKernelGGL((moe_gemm_rk<1, G128, DW, DD>), dim3(dn.x * kMgWaves / DW, dn.y), dim3(64 * DW),
+                           (size_t)(DD + 1) * kMgABytes, st, a);
     } else {
         hipLaunchKernelGGL((moe_gemm_k<0, G128, FMT>), gu, dim3(64 * kMgWaves), mg_lds(FMT), st, a);
         hipLaunchKernelGGL((moe_gemm_k<1, G128, FMT>), dn, dim3(64 * kMgWaves), mg_lds(FMT), st, a);
