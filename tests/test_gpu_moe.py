@@ -586,11 +586,12 @@ def test_moe_route_forward(torch_gpu, T, E, K, hidden, inter, sinter, gs, norm):
         assert Q.max_abs_rel(yc, ref) < 5e-3, call
 
 
-@pytest.mark.parametrize("T", [1, 4])
+@pytest.mark.parametrize("T", [1, 4, 12, 40, 130])
 def test_moe_route_forward_sigmoid_groups(torch_gpu, T):
     """Sigmoid scoring with a score bias, group-limited selection and routed
     scaling through the one-call path (T = 1 routes inside the gate/up
-    launch): routing bit-exact vs the router entry, y vs the two-call path."""
+    launch; above 16 tokens the router's last workgroup builds the lists):
+    routing bit-exact vs the router entry, y vs the two-call path."""
     from fastllm_py.expert_router import route_topk_device
     from fastllm_py.kernels import moe_int4
 
