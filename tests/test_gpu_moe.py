@@ -533,7 +533,9 @@ def test_fused_moe_shapes(torch_gpu, T, E, K, hidden, inter, sinter, gs):
     (3, 16, 4, 512, 768, 1536, 128, True),
     (16, 128, 16, 256, 256, 0, 64, True),        # 256 entries, group 64
     (5, 6, 3, 384, 384, 3200, 32, False),         # group 32, shared in 9 pieces
-    # one token: routed inside the gate/up launch
+    # one token: routed inside the gate/up launch (the Qwen3-30B-A3B decode
+    # shape: eight slots, down with one block per wave)
+    (1, 128, 8, 2048, 768, 0, 128, True),
     (1, 16, 4, 512, 768, 1536, 128, True),
     (1, 128, 16, 256, 256, 0, 64, True),
     (1, 6, 3, 384, 384, 3200, 32, False),
