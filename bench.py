@@ -500,6 +500,58 @@ def run_fp8_inline(torch, lib, stream, M_list=(1, 8), shapes=(("2048x2048", 2048
     return res
 
 
+def mxfp4_bytes(M, N, K):
+    """Bytes one dense MXFP4 GEMV call moves: codes (N K / 2), E8M0 scale
+    words (N K / 32), fp16 A and C."""
+    return N * K // 2 + N * K // 32 + 2 * M * K + 2 * M * N
+
+
+def run_mxfp4(torch, lib, stream, M_list=(1, 8, 16)):
+    """Dense MXFP4 GEMV (fastllm_mxfp4_gemv) at the Qwen3-8B decode shapes,
+    weights quantized on the GPU (OCP MXFP4) into the MoE tile layout and
+    rotated through HBM; the per-call times and one layer's sum."""
+    from fastllm_py.kernels import mxfp4
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3200)
+    res = {}
+    layer = {M: 0.0 for M in M_list}
+    layer_bytes = {M: 0 for M in M_list}
+    for name, N, K in QWEN3_8B:
+        W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+        base = mxfp4.quantize(W)
+        del W
+        wb = N * K // 2 + N * K // 32
+        n = copies_for(wb)
+        cps = [base] + [{"qtile": base["qtile"].clone(), "e8w": base["e8w"].clone(), "shape": base["shape"]}
+                        for _ in range(n - 1)]
+        for M in M_list:
+            x = torch.randn((M, K), generator=gen, device="cuda").half()
+            y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+            f = lib.fastllm_mxfp4_gemv
+
+            def mk(w, x=x, y=y, M=M):
+                def go(h):
+                    if f(x.data_ptr(), w["qtile"].data_ptr(), w["e8w"].data_ptr(), y.data_ptr(), M, N, K, h):
+                        raise RuntimeError("mxfp4 gemv failed")
+                return go
+            rounds = max(1, -(-96 // n))
+            seq = [mk(w) for _ in range(rounds) for w in cps]
+            us = graph_time(torch, stream, seq, 4) / len(seq) * 1e3
+            nb = mxfp4_bytes(M, N, K)
+            res[f"{name}/M{M}"] = {"us_per_call": round(us, 3), "GB/s": round(nb / us / 1e3, 1),
+                                   "pct_of_hbm_peak": round(nb / us / 1e3 / HBM_PEAK_GBS * 100, 2),
+                                   "bytes": nb, **cycle(n * wb)}
+            layer[M] += us
+            layer_bytes[M] += nb
+        del cps, base
+        torch.cuda.empty_cache()
+    for M in M_list:
+        res[f"layer/M{M}"] = {"us": round(layer[M], 3), "GB/s": round(layer_bytes[M] / layer[M] / 1e3, 1),
+                              "pct_of_hbm_peak": round(layer_bytes[M] / layer[M] / 1e3 / HBM_PEAK_GBS * 100, 2)}
+    return res
+
+
 def run_stream_probe(torch, lib, stream, sizes):
     """Per-launch floor of a streaming read of each byte count: the library's
     HBM read probe (fastllm_hbm_read_probe: every wave load a contiguous 1 KB,
@@ -979,7 +1031,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--ms", default="1,4,8,16")
-    ap.add_argument("--only", default="int4,swiglu,layer,probe,group,rm,fp8,fp8i,fp8p,moe,moelp,"
+    ap.add_argument("--only", default="int4,swiglu,layer,probe,group,rm,fp8,fp8i,fp8p,mx4,moe,moelp,"
                                       "moe30,moedet,gemm,moelpp")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy a 64 MiB buffer 5 times (a known-size kernel that "
@@ -1065,6 +1117,9 @@ def main():
     if "fp8i" in only:
         breakdown["fp8_inline_1x128_abi_fp16"] = run_fp8_inline(torch, lib, stream)
         log(f"FP8 inline ABI: {breakdown['fp8_inline_1x128_abi_fp16']}")
+    if "mx4" in only:
+        breakdown["mxfp4_gemv_qwen3_8b"] = run_mxfp4(torch, lib, stream)
+        log(f"MXFP4 GEMV: {breakdown['mxfp4_gemv_qwen3_8b']}")
     if "moe" in only:
         breakdown["moe_qwen15_a27b_int4"] = run_moe(torch, lib, stream)
         log(f"MoE: {breakdown['moe_qwen15_a27b_int4']}")
@@ -1093,6 +1148,7 @@ def main():
         # GEMVs as a fraction of it
         sizes = {f"int4_{n}_M1": marlin_bytes(1, N, K) for n, N, K in QWEN3_8B}
         sizes.update({f"fp8_{n}_M1": fp8_block_bytes(1, N, K) for n, N, K in FP8_SHAPES})
+        sizes.update({f"mxfp4_{n}_M1": mxfp4_bytes(1, N, K) for n, N, K in QWEN3_8B})
         sizes["peak_512MiB"] = 512 * 2 ** 20
         pr = run_stream_probe(torch, lib, stream, sizes)
         if 1 in per_m:
@@ -1118,6 +1174,12 @@ def main():
                 pr[f"fp8_{n}_M1"]["gemv_minus_probe_us"] = round(g - pr[f"fp8_{n}_M1"]["us_per_launch"], 3)
                 pr[f"fp8_{n}_M1"]["gemv_minus_probe_with_store_us"] = round(
                     g - pr[f"fp8_{n}_M1"]["us_per_launch_with_store"], 3)
+        if "mxfp4_gemv_qwen3_8b" in breakdown:
+            for n, N, K in QWEN3_8B:
+                g = breakdown["mxfp4_gemv_qwen3_8b"][f"{n}/M1"]["us_per_call"]
+                pr[f"mxfp4_{n}_M1"]["gemv_us"] = g
+                pr[f"mxfp4_{n}_M1"]["gemv_pct_of_probe"] = round(pr[f"mxfp4_{n}_M1"]["us_per_launch"] / g * 100, 1)
+                pr[f"mxfp4_{n}_M1"]["gemv_minus_probe_us"] = round(g - pr[f"mxfp4_{n}_M1"]["us_per_launch"], 3)
         breakdown["hbm_read_probe"] = pr
         log(f"HBM read probe: {pr}")
 

@@ -2014,6 +2014,95 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
     }
 }
 
+// ---- dense MXFP4 GEMV / small-M GEMM
+// C[M, N] = A[M, K] @ dequant(W)^T, W in the MXFP4 tile layout of the MoE
+// experts (one expert: qtile [N/16, K/128, 1KB], e8w [N/16, K/128, 16]).
+// Workgroup (bx, by): TR 16-row tiles of W (bx) against the 16 rows of A
+// from 16 by; its waves split the K blocks, NB each (moe_kb), every lane
+// loading its activation fragments (L2 hits) and then its weight blocks, so
+// each block waits only for its own weights; per MX block j of a 128-k
+// block, one MFMA on the exact fp16 codes, scaled by the block's E8M0 scale
+// in fp32, like the MoE kernels; the waves' partials are summed in wave
+// order (deterministic) and stored as fp16.
+template <int NB, int TR, int PH>
+__global__ __launch_bounds__(1024) void mx4_gemv_k(const uint16_t* __restrict__ A, const uint8_t* __restrict__ q,
+                                                   const uint32_t* __restrict__ e8w, uint16_t* __restrict__ C,
+                                                   int M, int N, int K) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int nwaves = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, kq = lane >> 4;
+    const int nkb = K >> 7;
+    const int m0 = blockIdx.y * 16;
+    const int Mc = M - m0 < 16 ? M - m0 : 16;
+    const uint16_t* arow = A + (size_t)(m0 + (col < Mc ? col : Mc - 1)) * K;
+    const size_t t0 = (size_t)blockIdx.x * TR;  // first 16-row tile of W
+    f32x4 acc[TR];
+#pragma unroll
+    for (int r = 0; r < TR; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // PH phases of NB blocks (the 128-VGPR budget of 16-wave workgroups
+    // holds the registers of up to four blocks at once)
+#pragma unroll
+    for (int ph = 0; ph < PH; ++ph) {
+        u32x4 av[NB][4];
+        WBlk<kFmtMx4> wv[NB][TR];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            int kb = moe_kb<NB * PH>(wave, ph * NB + i, nwaves);
+            kb = kb < nkb ? kb : nkb - 1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                av[i][j] = *reinterpret_cast<const u32x4*>(arow + kb * 128 + a_koff<kFmtMx4>(kq, j));
+        }
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            int kb = moe_kb<NB * PH>(wave, ph * NB + i, nwaves);
+            kb = kb < nkb ? kb : nkb - 1;
+#pragma unroll
+            for (int r = 0; r < TR; ++r) wv[i][r] = wblk_load<kFmtMx4>(q, e8w, t0 + r, nkb, kb, 0, 0, lane, col);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const float live = moe_kb<NB * PH>(wave, ph * NB + i, nwaves) < nkb ? 1.0f : 0.0f;
+#pragma unroll
+            for (int r = 0; r < TR; ++r) wblk_mma<kFmtMx4, true>(acc[r], av[i], wv[i][r], live);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    reduce_and_store<TR>(reinterpret_cast<float*>(smem), acc, Mc, wave, nwaves, lane,
+                         [&](int m, int t, int c, float v) {
+                             C[(size_t)(m0 + m) * N + (t0 + t) * 16 + c] = bitcast<uint16_t>((f16)v);
+                         });
+}
+
+// Launch shape of mx4_gemv_k: blocks per wave so that at most 16 waves cover
+// K (1, 2 or 4 in one phase, 6 in two phases of 3), two tiles per workgroup
+// from 384 tiles on (never with the two-phase blocks).  Measured at the
+// Qwen3-8B shapes, M = 1 (us): qkv 6144x4096 two tiles, 16 waves of two
+// blocks 5.3 (one tile 6.0); gate_up 24576x4096 8 waves of four blocks 11.9
+// (16 of two 12.8); o 4096x4096 one tile, 16 waves of two 4.4.
+struct Mx4Cfg {
+    int nb, waves, tr;
+};
+Mx4Cfg mx4_cfg(int N, int K) {
+    const int nkb = K / 128, tiles = N / 16;
+    Mx4Cfg c;
+    c.nb = nkb <= 16 ? 1 : (nkb <= 32 ? (tiles >= 1024 ? 4 : 2) : (nkb <= 64 ? 4 : 6));
+    c.waves = (nkb + c.nb - 1) / c.nb;
+    c.tr = (c.nb <= 4 && tiles >= 384 && tiles % 2 == 0) ? 2 : 1;
+    return c;
+}
+
+template <int NB, int TR, int PH>
+void launch_mx4_gemv(const Mx4Cfg& c, const uint16_t* A, const uint8_t* q, const uint32_t* e8w, uint16_t* C, int M,
+                     int N, int K, hipStream_t st) {
+    const dim3 grid(N / (16 * TR), (M + 15) / 16);
+    hipLaunchKernelGGL((mx4_gemv_k<NB, TR, PH>), grid, dim3(64 * c.waves), (size_t)c.waves * TR * 1024, st, A,
+                       q, e8w, C, M, N, K);
+}
+
 // Weight loads of the column-split down kernel: compiler-visible buffer
 // loads, so the compiler tracks their destination registers and places the
 // waits itself (loads issued from inline asm are invisible to it, and it may
@@ -3438,6 +3527,31 @@ int fastllm_moe_mxfp4_tile_repack(const uint8_t* codes, const uint8_t* e8, uint8
     hipLaunchKernelGGL(moe_mxfp4_tile_repack_k, dim3(grid), dim3(256), 0, (hipStream_t)stream, codes, e8,
                        qtile, e8w, rows, in_f);
     return finish("fastllm_moe_mxfp4_tile_repack");
+}
+
+int fastllm_mxfp4_gemv(const void* A, const uint8_t* qtile, const uint32_t* e8w, void* C, int M, int N, int K,
+                       void* stream) {
+    if (!A || !qtile || !e8w || !C || M <= 0 || N <= 0 || N % 16 || K <= 0 || K % 128) return 1;
+    if (K > 16 * 6 * 128) return 1;  // at most 16 waves of 6 blocks
+    if (!fl_aligned(A, 16) || !fl_aligned(qtile, 16) || !fl_aligned(e8w, 4) || !fl_aligned(C, 2)) return 1;
+    if (!fl_current_device_supported()) return 2;
+    const Mx4Cfg c = mx4_cfg(N, K);
+    const uint16_t* a = static_cast<const uint16_t*>(A);
+    uint16_t* y = static_cast<uint16_t*>(C);
+    hipStream_t st = (hipStream_t)stream;
+#define MX4_CASE(nb)                                                           \
+    case nb:                                                                   \
+        if (c.tr == 2)                                                         \
+            launch_mx4_gemv<nb, 2, 1>(c, a, qtile, e8w, y, M, N, K, st);       \
+        else                                                                   \
+            launch_mx4_gemv<nb, 1, 1>(c, a, qtile, e8w, y, M, N, K, st);       \
+        break;
+    switch (c.nb) {
+        MX4_CASE(1) MX4_CASE(2) MX4_CASE(4)
+        default: launch_mx4_gemv<3, 1, 2>(c, a, qtile, e8w, y, M, N, K, st); break;
+    }
+#undef MX4_CASE
+    return finish("fastllm_mxfp4_gemv");
 }
 
 int fastllm_moe_int4_tile_unpack(const uint8_t* qtile, const uint32_t* sz, uint8_t* qweight,

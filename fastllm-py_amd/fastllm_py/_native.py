@@ -86,6 +86,7 @@ SIGNATURES: dict[str, tuple] = {
     "fastllm_dequantize_mxfp4": (_I, [_P, _P, _P, ctypes.c_long, _I, _P]),
     "fastllm_moe_fp8_tile_repack": (_I, [_P, _P, ctypes.c_long, _I, _P]),
     "fastllm_moe_mxfp4_tile_repack": (_I, [_P, _P, _P, _P, ctypes.c_long, _I, _P]),
+    "fastllm_mxfp4_gemv": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "fastllm_moe_lowp_fused": (_I, [_I, _P, _I, _I, _I, _I, _I] + [_P] * 6 + [_I] + [_P] * 6 +
                                [_P] * 6 + [_I, _I, _P, _SZ, _P, _P]),
     "fastllm_moe_lowp_routed": (_I, [_I, _P, _I, _I, _I, _F, _P, _I, _I, _P] + [_P] * 9 +

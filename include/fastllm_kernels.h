@@ -472,6 +472,21 @@ int fastllm_moe_mxfp4_tile_repack(const uint8_t *codes, const uint8_t *e8,
                                   uint8_t *qtile, uint32_t *e8w, long rows,
                                   int in_f, void *stream);
 
+/* Dense MXFP4 GEMV: C[M, N] = A[M, K] @ dequant(W)^T with W in the MXFP4
+ * tile layout above (qtile [N/16, K/128, 1024], e8w [N/16, K/128, 16], one
+ * expert's worth), A and C fp16 row-major.  N % 16 == 0, K % 128 == 0, K <=
+ * 12288, any M (the weights are read once per 16 rows of A: this is the
+ * decode path, M <= 16; larger M is correct but re-reads them).  Each output is the fp32 sum, in a fixed order, of per-32-block
+ * MFMA products of the exact fp16 codes scaled by their E8M0 scale, rounded
+ * once to fp16.  Returns 0, 1 for bad arguments, 2 for a device or launch
+ * error.  Asynchronous on `stream`.
+ * No reference counterpart: the dense decode GEMV of the MXFP4 weights
+ * that docs/next-optimizations.md:160-184 plans (MXFP4 exists in the
+ * reference only as that plan). */
+int fastllm_mxfp4_gemv(const void *A, const uint8_t *qtile,
+                       const uint32_t *e8w, void *C, int M, int N, int K,
+                       void *stream);
+
 /* Bytes of device workspace fastllm_moe_int4_fused needs for this shape
  * (0 when the shape is unsupported). */
 size_t fastllm_moe_int4_workspace_bytes(int T, int hidden, int inter,
