@@ -549,6 +549,31 @@ def run_mxfp4(torch, lib, stream, M_list=(1, 8, 16)):
     for M in M_list:
         res[f"layer/M{M}"] = {"us": round(layer[M], 3), "GB/s": round(layer_bytes[M] / layer[M] / 1e3, 1),
                               "pct_of_hbm_peak": round(layer_bytes[M] / layer[M] / 1e3 / HBM_PEAK_GBS * 100, 2)}
+    # the prefill GEMM (M > 64: mx4_gemm_mfma) at the dense INT4 GEMM's shape
+    M, N, K = 512, 8192, 2048
+    W = torch.randn((N, K), generator=gen, device="cuda") * 0.02
+    base = mxfp4.quantize(W)
+    del W
+    wb = N * K // 2 + N * K // 32
+    n = copies_for(wb)
+    cps = [base] + [{"qtile": base["qtile"].clone(), "e8w": base["e8w"].clone(), "shape": base["shape"]}
+                    for _ in range(n - 1)]
+    x = torch.randn((M, K), generator=gen, device="cuda").half()
+    y = torch.empty((M, N), dtype=torch.float16, device="cuda")
+
+    def mkp(w):
+        def go(h):
+            if lib.fastllm_mxfp4_gemv(x.data_ptr(), w["qtile"].data_ptr(), w["e8w"].data_ptr(), y.data_ptr(),
+                                      M, N, K, h):
+                raise RuntimeError("mxfp4 gemm failed")
+        return go
+    rounds = max(1, -(-64 // n))
+    us = graph_time(torch, stream, [mkp(w) for _ in range(rounds) for w in cps], 4) / (rounds * n) * 1e3
+    tf = 2.0 * M * N * K / (us * 1e-6) / 1e12
+    res["prefill_gemm"] = {"shape": f"M{M} N{N} K{K}", "us_per_call": round(us, 3), "TFLOP/s": round(tf, 1),
+                           "mfma_util_fp16_dense": round(tf / MFMA_F16_PEAK_TFLOPS, 4), **cycle(n * wb)}
+    del cps, base
+    torch.cuda.empty_cache()
     return res
 
 

@@ -2077,6 +2077,148 @@ __global__ __launch_bounds__(1024) void mx4_gemv_k(const uint16_t* __restrict__ 
                          });
 }
 
+// Dense MXFP4 prefill GEMM (M > 64) on the matrix cores.  Workgroup tile 64
+// (m) x 256 (n), eight waves side by side along n, each 64 x 32 (4 m-tiles x
+// 2 n-tiles of 16 x 16 fp32 accumulators); the 128-k blocks stream through
+// two LDS stages by buffer_load ... lds copies (one block in flight while
+// the other is computed, one vmcnt wait and one barrier per block).  A
+// stage holds, for one 128-k block:
+//   * A (16 KB): the 64 x 128 fp16 rows, 256 B per row, the 16-byte k
+//     chunks of row r XOR-swizzled by r % 16 (conflict-free MFMA reads);
+//   * B (16 KB): the strip's 16 tile blocks as they lie (1 KB each);
+//   * E (1 KB): the strip's 16 tiles' e8w words for the block (64 B each).
+// MFMA step j of a block covers MX block 4 kb + j: the lane's word j of its
+// tile block is converted with the block's scale in the conversion itself
+// (v_cvt_scalef32_pk_f16_fp4: fp16(code * 2^(e - 127)), exact while that
+// value is an fp16 normal, i.e. for scales from 2^-14 up -- weights below
+// ~1e-4 in magnitude round; the decode GEMV keeps the scale in fp32), and
+// the four steps of a block accumulate in one MFMA chain per tile.  Rows >=
+// M read row M - 1 and are not stored; n-tiles >= N / 16 read the last
+// n-tile and are not stored.  Workgroup order as the INT4 GEMM: the tiles of
+// one XCD are a contiguous (n-block major, m-block minor) run.
+constexpr int kMxBM = 64, kMxBN = 256;
+constexpr int kMxStA = 0, kMxStB = 16384, kMxStE = 32768, kMxStage = kMxStE + 1024;
+
+__global__ __launch_bounds__(512) void mx4_gemm_mfma(const f16* __restrict__ A, const uint8_t* __restrict__ Wq,
+                                                     const uint32_t* __restrict__ E, f16* __restrict__ C, int M,
+                                                     int N, int K) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, kq = lane >> 4;
+    const int nkb = K >> 7;
+    const int ntiles = N >> 4;
+    const int nblk = (N + kMxBN - 1) / kMxBN, mblk = (M + kMxBM - 1) / kMxBM;
+    const int total = nblk * mblk;
+    int lin = blockIdx.x;
+    if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
+    const int nb_i = lin / mblk, mb_i = lin - nb_i * mblk;
+    const int m0 = mb_i * kMxBM;
+    const int nt_base = nb_i * 16;
+
+    const i32x4_t rA = raw_rsrc(A, (uint32_t)M * K * 2);
+    const i32x4_t rW = raw_rsrc(Wq, (uint32_t)ntiles * nkb * 1024);
+    const i32x4_t rE = raw_rsrc(E, (uint32_t)ntiles * nkb * 64);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
+
+    // copy sources of this wave: A rows 4 q .. 4 q + 3 (q = 2 wave + i) as
+    // whole 256-byte rows, lane l of a copy landing at row 4 q + l / 16,
+    // position l % 16 with the row's k chunk (l % 16) ^ (row % 16); B tiles
+    // 2 wave + i of the strip; wave 0 also the strip's E words (lane l: tile
+    // l / 4, 16 bytes (l % 4) of its 64).
+    uint32_t ao[2], bo[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = 4 * (wave * 2 + i) + (lane >> 4);
+        int m = m0 + r;
+        m = m < M ? m : M - 1;
+        ao[i] = 2u * ((uint32_t)m * K) + 16u * ((lane & 15) ^ (r & 15));
+        int nt = nt_base + wave * 2 + i;
+        nt = nt < ntiles ? nt : ntiles - 1;
+        bo[i] = (uint32_t)nt * (uint32_t)nkb * 1024u + lane * 16;
+    }
+    int et = nt_base + (lane >> 2);
+    et = et < ntiles ? et : ntiles - 1;
+    const uint32_t eo = (uint32_t)et * (uint32_t)nkb * 64u + 16u * (lane & 3);
+
+    auto issue = [&](int kb, int slot) {
+        const uint32_t st = lds0 + (uint32_t)slot * kMxStage;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) lds_copy(rA, st + kMxStA + (wave * 2 + i) * 1024, ao[i], kb * 256);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) lds_copy(rW, st + kMxStB + (wave * 2 + i) * 1024, bo[i], kb * 1024);
+        if (wave == 0) lds_copy(rE, st + kMxStE, eo, kb * 64);
+    };
+
+    f32x4 acc[4][2];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) acc[mt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    issue(0, 0);
+    // A operand of m-tile mt, step j for lane (col, kq): row 16 mt + col, k
+    // chunk 4 j + kq (k 32 j + 8 kq, the MX tile's order), stored at
+    // position (4 j + kq) ^ col of that row
+    const int afrag = kMxStA + col * 256 + 16 * (kq ^ (col & 3));
+    const int ajx = col >> 2;
+    for (int kb = 0; kb < nkb; ++kb) {
+        const int u = kb & 1;
+        wait_vmcnt<0>();  // this wave's copies of block kb have landed
+        lds_barrier();    // ... and every wave's; block kb - 1's stage is free
+        if (kb + 1 < nkb) issue(kb + 1, u ^ 1);
+        const unsigned char* st = smem + (size_t)u * kMxStage;
+        u32x4 wv[2];
+        uint32_t ew[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            wv[t] = *reinterpret_cast<const u32x4*>(st + kMxStB + (wave * 2 + t) * 1024 + lane * 16);
+            ew[t] = *reinterpret_cast<const uint32_t*>(st + kMxStE + (wave * 2 + t) * 64 + col * 4);
+        }
+        const unsigned char* as = st + afrag;
+        f16x8 a[2][4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) a[0][mt] = *reinterpret_cast<const f16x8*>(as + mt * 4096 + 64 * ajx);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (j < 3) {
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt)
+                    a[(j + 1) & 1][mt] = *reinterpret_cast<const f16x8*>(as + mt * 4096 + 64 * ((j + 1) ^ ajx));
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const float s = e8m0_float((ew[t] >> (8 * j)) & 0xFFu);
+                const uint32_t w = wv[t][j];
+                const f16x8 b = bitcast<f16x8>(u32x4{
+                    bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 0)),
+                    bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 1)),
+                    bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 2)),
+                    bitcast<uint32_t>(__builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, s, 3))});
+#pragma unroll
+                for (int mt = 0; mt < 4; ++mt) acc[mt][t] = mfma_f16(a[j & 1][mt], b, acc[mt][t]);
+            }
+        }
+    }
+    wait_vmcnt<0>();  // no copy may still be in flight when the workgroup ends
+
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int nt = nt_base + wave * 2 + t;
+        if (nt >= ntiles) continue;
+        const int n = nt * 16 + col;
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = m0 + mt * 16 + 4 * kq + e;
+                if (m < M) C[(size_t)m * N + n] = (f16)acc[mt][t][e];
+            }
+    }
+}
+constexpr size_t kMxGemmLds = 2 * (size_t)kMxStage;
+constexpr int kMxGemmMinM = 64;  // M above this takes the MFMA GEMM
+
 // Launch shape of mx4_gemv_k: blocks per wave so that at most 16 waves cover
 // K (1, 2 or 4 in one phase, 6 in two phases of 3), two tiles per workgroup
 // from 384 tiles on (never with the two-phase blocks).  Measured at the
@@ -3532,13 +3674,20 @@ int fastllm_moe_mxfp4_tile_repack(const uint8_t* codes, const uint8_t* e8, uint8
 int fastllm_mxfp4_gemv(const void* A, const uint8_t* qtile, const uint32_t* e8w, void* C, int M, int N, int K,
                        void* stream) {
     if (!A || !qtile || !e8w || !C || M <= 0 || N <= 0 || N % 16 || K <= 0 || K % 128) return 1;
-    if (K > 16 * 6 * 128) return 1;  // at most 16 waves of 6 blocks
+    if (M <= kMxGemmMinM && K > 16 * 6 * 128) return 1;  // the GEMV: at most 16 waves of 6 blocks
     if (!fl_aligned(A, 16) || !fl_aligned(qtile, 16) || !fl_aligned(e8w, 4) || !fl_aligned(C, 2)) return 1;
     if (!fl_current_device_supported()) return 2;
-    const Mx4Cfg c = mx4_cfg(N, K);
     const uint16_t* a = static_cast<const uint16_t*>(A);
     uint16_t* y = static_cast<uint16_t*>(C);
     hipStream_t st = (hipStream_t)stream;
+    if (M > kMxGemmMinM) {
+        if ((size_t)M * K * 2 >= (1ull << 31) || (size_t)N * K / 2 >= (1ull << 31)) return 1;  // 32-bit buffer ranges
+        const int tiles = ((N + kMxBN - 1) / kMxBN) * ((M + kMxBM - 1) / kMxBM);
+        hipLaunchKernelGGL(mx4_gemm_mfma, dim3(tiles), dim3(512), kMxGemmLds, st, reinterpret_cast<const f16*>(a),
+                           qtile, e8w, reinterpret_cast<f16*>(y), M, N, K);
+        return finish("fastllm_mxfp4_gemv");
+    }
+    const Mx4Cfg c = mx4_cfg(N, K);
 #define MX4_CASE(nb)                                                           \
     case nb:                                                                   \
         if (c.tr == 2)                                                         \

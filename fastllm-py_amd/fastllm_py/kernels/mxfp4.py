@@ -1,8 +1,8 @@
-"""Dense MXFP4 GEMV (decode path) on gfx950.
+"""Dense MXFP4 GEMV (decode) and GEMM (prefill) on gfx950.
 
 The reference plans MXFP4 weights for both its expert kernels and a dense
 decode GEMV / prefill GEMM (docs/next-optimizations.md:160-184) without a
-format or kernel of its own; this module is the dense decode half.  Weights
+format or kernel of its own; this module is the dense pair.  Weights
 use the same OCP MXFP4 quantization (``fastllm_quantize_mxfp4``: E2M1 codes,
 one E8M0 scale per 32 inputs) and the same MFMA tile layout as this
 library's MXFP4 experts (``moe_int4.stack_lowp``), one matrix instead of a
@@ -29,9 +29,10 @@ def quantize(W) -> dict:
 
 
 def gemv(A, wq: dict, out=None, stream=None):
-    """C = A @ dequant(W).T for A (M, K) fp16 on the GPU (any M; M <= 16 is
-    the fast path, larger M re-reads the weights per 16 rows) and ``wq``
-    from :func:`quantize`.  Returns C (M, N) fp16; ``out`` may be given."""
+    """C = A @ dequant(W).T for A (M, K) fp16 on the GPU and ``wq`` from
+    :func:`quantize`: up to 64 rows the decode GEMV (fast for M <= 16; it
+    reads the weights once per 16 rows), above the MFMA prefill GEMM.
+    Returns C (M, N) fp16; ``out`` may be given."""
     t = nat.torch()
     N, K = wq["shape"]
     a = nat.to_device(A, t.float16)

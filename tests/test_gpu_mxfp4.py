@@ -1,12 +1,13 @@
-"""Dense MXFP4 GEMV (fastllm_mxfp4_gemv) on the GPU vs the oracle.
+"""Dense MXFP4 GEMV / prefill GEMM (fastllm_mxfp4_gemv) on the GPU vs the oracle.
 
 The weights go through the GPU quantizer and tile repack (both pinned
 bit-exact against oracle/mx.py in test_gpu_moe_lowp.py); the reference is the
 fp64 product of the fp16 activations with oracle/mx.py's dequantization of
 the same weights.  The kernel multiplies the exact fp16 codes by the fp16
-activations in fp32 MFMAs and scales each 32-block sum by its E8M0 scale, so
-its only deviations are the fp32 summation order and the final fp16
-rounding (2^-11 relative): max-abs-rel 2e-3.
+activations in fp32 MFMAs and scales each 32-block sum by its E8M0 scale
+(the GEMM above 64 rows converts code x scale to fp16 instead, exact at these
+weights' scales), so its only deviations are the fp32 summation order and
+the final fp16 rounding (2^-11 relative): max-abs-rel 2e-3.
 """
 import numpy as np
 import pytest
@@ -40,6 +41,11 @@ def _case(torch, rng, N, K, M, scale=0.05):
     (256, 4224, 4),       # 33 blocks: the last wave's blocks partly past K
     (640, 1152, 20),      # two 16-row groups, the second ragged
     (128, 256, 33),
+    # above 64 rows: the MFMA GEMM (64 x 256 workgroup tiles)
+    (512, 1024, 65),      # one row past a tile
+    (384, 2048, 130),     # a 256-column strip only partly inside N
+    (2048, 4096, 512),    # prefill-sized
+    (256, 12288, 100),
 ])
 def test_mxfp4_gemv_matches_oracle(torch_gpu, N, K, M):
     from fastllm_py.kernels import mxfp4
