@@ -1356,8 +1356,8 @@ GemvCfg default_gemv_cfg(int M, int N, int K, bool g32, bool can_split = false) 
     const int cap = g32 ? 4 : 8;
     // eight waves of four blocks beat sixteen of two where K <= 4096 (M <= 4:
     // qkv 5.85 -> 5.40 us, o 4.36 -> 4.26; one tile at any M: o 5.67 -> 5.52
-    // at M = 8)
-    int waves = ((N >= 16384 && M <= 8) || (nfull <= 32 && (M <= 4 || c.tiles == 1))) ? 8 : 16;
+    // at M = 8; above eight rows: qkv 6.51 -> 6.34 at M = 16)
+    int waves = ((N >= 16384 && M <= 8) || (nfull <= 32 && (M <= 4 || M > 8 || c.tiles == 1))) ? 8 : 16;
     while (waves > 1 && nfull < waves) waves /= 2;  // at least one block per wave
     while ((nfull + waves - 1) / waves > cap && waves < 16) waves *= 2;
     c.waves = waves;
