@@ -476,11 +476,10 @@ int fastllm_moe_mxfp4_tile_repack(const uint8_t *codes, const uint8_t *e8,
  * MXFP4 tile layout above (qtile [N/16, K/128, 1024], e8w [N/16, K/128, 16],
  * one expert's worth), A and C fp16 row-major.  N % 16 == 0, K % 128 == 0.
  * Up to 64 rows (K <= 12288) the decode GEMV, which reads the weights once
- * per 16 rows of A (fast for M <= 16): each output is the fp32 sum, in a
- * fixed order, of per-32-block MFMA products of the exact fp16 codes scaled
- * by their E8M0 scale, rounded once to fp16.  Above 64 rows (M K and N K / 2
- * below 2^31 bytes) the prefill GEMM on the matrix cores, whose B operand is
- * fp16(code * scale): exact for scales from 2^-14 up, rounded below.
+ * per 16 rows of A (fast for M <= 16), above 64 rows (M K and N K / 2 below
+ * 2^31 bytes) the prefill GEMM on the matrix cores.  Both feed the MFMAs
+ * fp16(code * scale) (exact for E8M0 scales from 2^-14 up, rounded below)
+ * and accumulate in fp32 in a fixed order, rounded once to fp16.
  * Returns 0, 1 for bad arguments, 2 for a device or launch error.
  * Asynchronous on `stream`.
  * No reference counterpart: the dense decode GEMV and prefill GEMM of the

@@ -5,7 +5,9 @@ Packers bit-exact (the MXFP4 quantizer against oracle/mx.py's OCP
 restatement, the FP8 codes against quantize_fp8_block, both tile layouts
 against their restated packers); the MoE output within max-abs-rel 1e-2 of
 the fp32 oracle evaluated on the oracle's own quantization of the same
-weights (its only deviations are the fp16 activations and fp16 h).
+weights (its only deviations are the fp16 activations and fp16 h; MXFP4
+codes enter the MFMAs as fp16(code x scale), exact at these weights' block
+scales, all >= 2^-14).
 """
 import numpy as np
 import pytest

@@ -3,11 +3,10 @@
 The weights go through the GPU quantizer and tile repack (both pinned
 bit-exact against oracle/mx.py in test_gpu_moe_lowp.py); the reference is the
 fp64 product of the fp16 activations with oracle/mx.py's dequantization of
-the same weights.  The kernel multiplies the exact fp16 codes by the fp16
-activations in fp32 MFMAs and scales each 32-block sum by its E8M0 scale
-(the GEMM above 64 rows converts code x scale to fp16 instead, exact at these
-weights' scales), so its only deviations are the fp32 summation order and
-the final fp16 rounding (2^-11 relative): max-abs-rel 2e-3.
+the same weights.  The kernels feed the MFMAs fp16(code x scale), exact at
+these weights' scales (>= 2^-14), and accumulate in fp32, so their only
+deviations are the fp32 summation order and the final fp16 rounding (2^-11
+relative): max-abs-rel 2e-3.
 """
 import numpy as np
 import pytest
