@@ -273,5 +273,8 @@ def test_decode_layer_graph_replays(torch_gpu, M, fuse):
         np.testing.assert_array_equal(x1, x + pend.astype(np.float32))
         np.testing.assert_array_equal(gx, x1 + L.o.float().cpu().numpy())
         ox, op = _oracle_layer(hat, x, pend, q_dim, inter, L.eps)
-        assert Q.max_abs_rel(gx, ox) < 1e-2, r
-        assert Q.max_abs_rel(gp, op) < 2e-2, r
+        # the chain and the oracle round the same fp16 intermediates, only
+        # their fp32 summation orders differ (measured: at most 2.6e-4 on x,
+        # 7.1e-4 on the MLP output over 20 replays at each of these shapes)
+        assert Q.max_abs_rel(gx, ox) < 5e-3, r
+        assert Q.max_abs_rel(gp, op) < 5e-3, r
