@@ -96,3 +96,36 @@ def test_mxfp4_gemv_argument_checks(torch_gpu):
     assert lib.fastllm_mxfp4_gemv(*args, 1, 256, 12416, None) == 1    # K > 12288
     assert lib.fastllm_mxfp4_gemv(*args, 0, 256, 256, None) == 1      # M
     assert lib.fastllm_mxfp4_gemv(None, *args[1:], 1, 256, 256, None) == 1
+
+
+def test_mxfp4_graph_replays(torch_gpu):
+    """Capturable (the roadmap's requirement for these kernels): the decode
+    GEMV and the prefill GEMM captured in one HIP graph replay bit-identical
+    to eager calls, three replays with fresh inputs and eager work between."""
+    from fastllm_py.kernels import mxfp4
+
+    torch = torch_gpu
+    rng = np.random.default_rng(21)
+    wq, _, _ = _case(torch, rng, 1024, 2048, 1)
+    a1 = torch.zeros((4, 2048), dtype=torch.float16, device="cuda")
+    a2 = torch.zeros((200, 2048), dtype=torch.float16, device="cuda")
+    y1 = torch.empty((4, 1024), dtype=torch.float16, device="cuda")
+    y2 = torch.empty((200, 1024), dtype=torch.float16, device="cuda")
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):  # warm the allocator and the library off-capture
+        mxfp4.gemv(a1, wq, out=y1, stream=st)
+        mxfp4.gemv(a2, wq, out=y2, stream=st)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        mxfp4.gemv(a1, wq, out=y1, stream=torch.cuda.current_stream())
+        mxfp4.gemv(a2, wq, out=y2, stream=torch.cuda.current_stream())
+    for r in range(3):
+        a1.copy_(torch.from_numpy((rng.standard_normal((4, 2048)) * 0.5).astype(np.float16)))
+        a2.copy_(torch.from_numpy((rng.standard_normal((200, 2048)) * 0.5).astype(np.float16)))
+        g.replay()
+        torch.cuda.synchronize()
+        e1, e2 = mxfp4.gemv(a1, wq), mxfp4.gemv(a2, wq)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(y1.cpu().numpy().view(np.uint16), e1.cpu().numpy().view(np.uint16), err_msg=f"replay {r}")
+        np.testing.assert_array_equal(y2.cpu().numpy().view(np.uint16), e2.cpu().numpy().view(np.uint16), err_msg=f"replay {r}")
