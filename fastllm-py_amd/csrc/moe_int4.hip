@@ -2033,7 +2033,7 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
 // block chain their MFMAs on fp16(code * scale), like the MoE kernels; the
 // waves' partials are summed in wave order (deterministic) and stored as
 // fp16.
-template <int NB, int TR, int PH>
+template <int NB, int TR, int PH, bool LDSA>
 __global__ __launch_bounds__(1024) void mx4_gemv_k(const uint16_t* __restrict__ A, const uint8_t* __restrict__ q,
                                                    const uint32_t* __restrict__ e8w, uint16_t* __restrict__ C,
                                                    int M, int N, int K) {
@@ -2047,6 +2047,16 @@ __global__ __launch_bounds__(1024) void mx4_gemv_k(const uint16_t* __restrict__ 
     const int Mc = M - m0 < 16 ? M - m0 : 16;
     const uint16_t* arow = A + (size_t)(m0 + (col < Mc ? col : Mc - 1)) * K;
     const size_t t0 = (size_t)blockIdx.x * TR;  // first 16-row tile of W
+    // LDSA (above four rows): each wave first copies the 16 activation rows
+    // of its blocks into its own LDS slots as whole 256-byte rows (block i:
+    // [row][256 B], the 16-byte k chunks of row r XOR-swizzled by r, so the
+    // 16 rows of an MFMA operand read hit 16 bank groups), four rows per
+    // copy, issued before its weight loads and waited for with a count that
+    // leaves those in flight; no barrier (only the wave reads its slots).
+    // Register fragments would load every activation byte once per lane
+    // quarter that needs it.
+    unsigned char* aslot = smem + (size_t)wave * NB * 4096;
+    const size_t abytes = LDSA ? (size_t)nwaves * NB * 4096 : 0;
     f32x4 acc[TR];
 #pragma unroll
     for (int r = 0; r < TR; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -2056,14 +2066,32 @@ __global__ __launch_bounds__(1024) void mx4_gemv_k(const uint16_t* __restrict__ 
     for (int ph = 0; ph < PH; ++ph) {
         u32x4 av[NB][4];
         WBlk<kFmtMx4> wv[NB][TR];
+        if (LDSA) {
+            const i32x4_t rA = raw_rsrc(A + (size_t)m0 * K, (uint32_t)Mc * (uint32_t)K * 2u);
+            const uint32_t lds = (uint32_t)(uintptr_t)aslot;
 #pragma unroll
-        for (int i = 0; i < NB; ++i) {
-            int kb = moe_kb<NB * PH>(wave, ph * NB + i, nwaves);
-            kb = kb < nkb ? kb : nkb - 1;
+            for (int i = 0; i < NB; ++i) {
+                int kb = moe_kb<NB * PH>(wave, ph * NB + i, nwaves);
+                kb = kb < nkb ? kb : nkb - 1;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                av[i][j] = *reinterpret_cast<const u32x4*>(arow + kb * 128 + a_koff<kFmtMx4>(kq, j));
+                for (int p = 0; p < 4; ++p) {
+                    const int r = 4 * p + (lane >> 4);
+                    const int m = r < Mc ? r : Mc - 1;
+                    lds_copy(rA, lds + (uint32_t)(i * 4 + p) * 1024u,
+                             2u * (uint32_t)m * (uint32_t)K + 16u * (uint32_t)((lane & 15) ^ r), (uint32_t)kb * 256u);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < NB; ++i) {
+                int kb = moe_kb<NB * PH>(wave, ph * NB + i, nwaves);
+                kb = kb < nkb ? kb : nkb - 1;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    av[i][j] = *reinterpret_cast<const u32x4*>(arow + kb * 128 + a_koff<kFmtMx4>(kq, j));
+            }
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             int kb = moe_kb<NB * PH>(wave, ph * NB + i, nwaves);
@@ -2072,6 +2100,18 @@ __global__ __launch_bounds__(1024) void mx4_gemv_k(const uint16_t* __restrict__ 
             for (int r = 0; r < TR; ++r) wv[i][r] = wblk_load<kFmtMx4>(q, e8w, t0 + r, nkb, kb, 0, 0, lane, col);
         }
         __builtin_amdgcn_sched_barrier(0);
+        if (LDSA) {
+            // the copies are older than the NB * TR 16-byte weight loads
+            // (and their scale words): done once at most that many are left
+            wait_vmcnt<(NB * TR < 63 ? NB * TR : 63)>();
+            asm volatile("" ::: "memory");  // no LDS read moves above the wait
+#pragma unroll
+            for (int i = 0; i < NB; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    av[i][j] = *reinterpret_cast<const u32x4*>(aslot + i * 4096 + col * 256 +
+                                                               16 * ((4 * j + kq) ^ col));
+        }
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             const float live = moe_kb<NB * PH>(wave, ph * NB + i, nwaves) < nkb ? 1.0f : 0.0f;
@@ -2080,7 +2120,7 @@ __global__ __launch_bounds__(1024) void mx4_gemv_k(const uint16_t* __restrict__ 
             __builtin_amdgcn_sched_barrier(0);
         }
     }
-    reduce_and_store<TR>(reinterpret_cast<float*>(smem), acc, Mc, wave, nwaves, lane,
+    reduce_and_store<TR>(reinterpret_cast<float*>(smem + abytes), acc, Mc, wave, nwaves, lane,
                          [&](int m, int t, int c, float v) {
                              C[(size_t)(m0 + m) * N + (t0 + t) * 16 + c] = bitcast<uint16_t>((f16)v);
                          });
@@ -2250,8 +2290,14 @@ template <int NB, int TR, int PH>
 void launch_mx4_gemv(const Mx4Cfg& c, const uint16_t* A, const uint8_t* q, const uint32_t* e8w, uint16_t* C, int M,
                      int N, int K, hipStream_t st) {
     const dim3 grid(N / (16 * TR), (M + 15) / 16);
-    hipLaunchKernelGGL((mx4_gemv_k<NB, TR, PH>), grid, dim3(64 * c.waves), (size_t)c.waves * TR * 1024, st, A,
-                       q, e8w, C, M, N, K);
+    const size_t red = (size_t)c.waves * TR * 1024, slots = (size_t)c.waves * NB * 4096;
+    // above four rows the activations go through LDS where the slots fit
+    if (PH == 1 && M > 4 && slots + red <= 160 * 1024)
+        hipLaunchKernelGGL((mx4_gemv_k<NB, TR, PH, true>), grid, dim3(64 * c.waves), slots + red, st, A, q, e8w,
+                           C, M, N, K);
+    else
+        hipLaunchKernelGGL((mx4_gemv_k<NB, TR, PH, false>), grid, dim3(64 * c.waves), red, st, A, q, e8w, C, M,
+                           N, K);
 }
 
 // Weight loads of the column-split down kernel: compiler-visible buffer
