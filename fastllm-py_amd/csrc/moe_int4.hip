@@ -2033,7 +2033,7 @@ __global__ __launch_bounds__(512) void moe_down_k(MoeArgs a) {
 // block chain their MFMAs on fp16(code * scale), like the MoE kernels; the
 // waves' partials are summed in wave order (deterministic) and stored as
 // fp16.
-template <int NB, int TR, int PH, bool LDSA>
+template <int NB, int TR, int PH, int RS>
 __global__ __launch_bounds__(1024) void mx4_gemv_k(const uint16_t* __restrict__ A, const uint8_t* __restrict__ q,
                                                    const uint32_t* __restrict__ e8w, uint16_t* __restrict__ C,
                                                    int M, int N, int K) {
@@ -2047,16 +2047,20 @@ __global__ __launch_bounds__(1024) void mx4_gemv_k(const uint16_t* __restrict__ 
     const int Mc = M - m0 < 16 ? M - m0 : 16;
     const uint16_t* arow = A + (size_t)(m0 + (col < Mc ? col : Mc - 1)) * K;
     const size_t t0 = (size_t)blockIdx.x * TR;  // first 16-row tile of W
-    // LDSA (above four rows): each wave first copies the 16 activation rows
-    // of its blocks into its own LDS slots as whole 256-byte rows (block i:
-    // [row][256 B], the 16-byte k chunks of row r XOR-swizzled by r, so the
-    // 16 rows of an MFMA operand read hit 16 bank groups), four rows per
-    // copy, issued before its weight loads and waited for with a count that
-    // leaves those in flight; no barrier (only the wave reads its slots).
-    // Register fragments would load every activation byte once per lane
-    // quarter that needs it.
-    unsigned char* aslot = smem + (size_t)wave * NB * 4096;
-    const size_t abytes = LDSA ? (size_t)nwaves * NB * 4096 : 0;
+    // RS = 4, 8 or 16 (the rows of A rounded up): each wave first copies RS
+    // activation rows of its blocks into its own LDS slots as whole 256-byte rows
+    // (block i: [row][256 B], the 16-byte k chunks of row r XOR-swizzled by
+    // r, so the rows of an MFMA operand read hit distinct bank groups), four
+    // rows per copy, issued before its weight loads and waited for with a
+    // count that leaves those in flight; no barrier (only the wave reads its
+    // slots).  With RS < 16 the lanes of MFMA rows RS..15 read rows 0..RS-1
+    // again (their outputs are not stored).  RS = 0 (the two-phase long-K
+    // shape, whose slots do not fit): register fragments, which load every
+    // activation byte once per lane quarter that uses it.
+    constexpr bool LDSA = RS > 0;
+    constexpr int SB = RS * 256;  // slot bytes per block
+    unsigned char* aslot = smem + (size_t)wave * NB * SB;
+    const size_t abytes = LDSA ? (size_t)nwaves * NB * SB : 0;
     f32x4 acc[TR];
 #pragma unroll
     for (int r = 0; r < TR; ++r) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -2074,10 +2078,10 @@ __global__ __launch_bounds__(1024) void mx4_gemv_k(const uint16_t* __restrict__ 
                 int kb = moe_kb<NB * PH>(wave, ph * NB + i, nwaves);
                 kb = kb < nkb ? kb : nkb - 1;
 #pragma unroll
-                for (int p = 0; p < 4; ++p) {
+                for (int p = 0; p < RS / 4; ++p) {
                     const int r = 4 * p + (lane >> 4);
                     const int m = r < Mc ? r : Mc - 1;
-                    lds_copy(rA, lds + (uint32_t)(i * 4 + p) * 1024u,
+                    lds_copy(rA, lds + (uint32_t)(i * SB + p * 1024),
                              2u * (uint32_t)m * (uint32_t)K + 16u * (uint32_t)((lane & 15) ^ r), (uint32_t)kb * 256u);
                 }
             }
@@ -2109,8 +2113,8 @@ __global__ __launch_bounds__(1024) void mx4_gemv_k(const uint16_t* __restrict__ 
             for (int i = 0; i < NB; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    av[i][j] = *reinterpret_cast<const u32x4*>(aslot + i * 4096 + col * 256 +
-                                                               16 * ((4 * j + kq) ^ col));
+                    av[i][j] = *reinterpret_cast<const u32x4*>(aslot + i * SB + (col & (RS - 1)) * 256 +
+                                                               16 * ((4 * j + kq) ^ (col & (RS - 1))));
         }
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
@@ -2290,14 +2294,24 @@ template <int NB, int TR, int PH>
 void launch_mx4_gemv(const Mx4Cfg& c, const uint16_t* A, const uint8_t* q, const uint32_t* e8w, uint16_t* C, int M,
                      int N, int K, hipStream_t st) {
     const dim3 grid(N / (16 * TR), (M + 15) / 16);
-    const size_t red = (size_t)c.waves * TR * 1024, slots = (size_t)c.waves * NB * 4096;
-    // above four rows the activations go through LDS where the slots fit
-    if (PH == 1 && M > 4 && slots + red <= 160 * 1024)
-        hipLaunchKernelGGL((mx4_gemv_k<NB, TR, PH, true>), grid, dim3(64 * c.waves), slots + red, st, A, q, e8w,
-                           C, M, N, K);
-    else
-        hipLaunchKernelGGL((mx4_gemv_k<NB, TR, PH, false>), grid, dim3(64 * c.waves), red, st, A, q, e8w, C, M,
-                           N, K);
+    const size_t red = (size_t)c.waves * TR * 1024;
+    const int rs = M > 8 ? 16 : (M > 4 ? 8 : 4);  // rows staged per block
+    const size_t slots = (size_t)c.waves * NB * rs * 256;
+    // the activations go through LDS where the slots fit
+    if (PH == 1 && slots + red <= 160 * 1024) {
+        if (rs == 4)
+            hipLaunchKernelGGL((mx4_gemv_k<NB, TR, PH, 4>), grid, dim3(64 * c.waves), slots + red, st, A, q, e8w,
+                               C, M, N, K);
+        else if (rs == 8)
+            hipLaunchKernelGGL((mx4_gemv_k<NB, TR, PH, 8>), grid, dim3(64 * c.waves), slots + red, st, A, q, e8w,
+                               C, M, N, K);
+        else
+            hipLaunchKernelGGL((mx4_gemv_k<NB, TR, PH, 16>), grid, dim3(64 * c.waves), slots + red, st, A, q,
+                               e8w, C, M, N, K);
+    } else {
+        hipLaunchKernelGGL((mx4_gemv_k<NB, TR, PH, 0>), grid, dim3(64 * c.waves), red, st, A, q, e8w, C, M, N,
+                           K);
+    }
 }
 
 // Weight loads of the column-split down kernel: compiler-visible buffer
