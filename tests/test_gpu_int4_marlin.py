@@ -133,6 +133,34 @@ def test_gemm_parity_qwen3_8b(torch_gpu, name, M):
     assert err < TOL, (name, M, err)
 
 
+def test_gemv_scales_off_16_byte_alignment(torch_gpu):
+    """The ABI takes a scale array at any 2-byte alignment
+    (marlin.py:250-299 passes whatever the caller's tensor holds): a scale
+    pointer 2 bytes past a 16-byte boundary, at the two- and four-tile
+    launches (N = 16384), gives the aligned call's results bit for bit."""
+    from fastllm_py.kernels import marlin
+
+    torch = torch_gpu
+    N, K = 16384, 1024  # two tiles up to M = 8, four above
+    rng = np.random.default_rng(77)
+    W = (rng.standard_normal((N, K)) * 0.02).astype(np.float32)
+    pay, w_hat, _ = _prep(torch, W, 128)
+    s = pay["scales"]
+    buf = torch.empty(s.numel() + 8, dtype=s.dtype, device=s.device)
+    su = buf[1:1 + s.numel()].view(s.shape)
+    su.copy_(s)
+    assert su.data_ptr() % 16 != 0
+    for M in (1, 4, 8, 16):
+        a = rng.standard_normal((M, K)).astype(np.float16)
+        ad = torch.from_numpy(a).cuda()
+        ref_dev = marlin.marlin_gemm_int4(ad, pay["qweight"], s, pay["zeros"], marlin.make_workspace(N))
+        out = marlin.marlin_gemm_int4(ad, pay["qweight"], su, pay["zeros"], marlin.make_workspace(N))
+        ref = Q.matmul_ref(a.astype(np.float32), w_hat)
+        err = Q.max_abs_rel(out.float().cpu().numpy(), ref)
+        assert err < TOL, (M, err)
+        assert torch.equal(out, ref_dev), M  # the same kernels, fixed reduction order
+
+
 @pytest.mark.parametrize("M", [17, 33, 64, 100, 130])
 def test_gemm_parity_larger_m(torch_gpu, M):
     from fastllm_py.kernels import marlin
