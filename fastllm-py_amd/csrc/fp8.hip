@@ -736,9 +736,10 @@ Fp8Cfg fp8_cfg(int M, int N, int K) {
     const int nfull = K / 128 > 0 ? K / 128 : 1;
     // one 16-row tile per workgroup (twice the workgroups of two: 10944 x 2048
     // measured 7.4 us against 8.2 at M = 1); on wide N eight waves up to
-    // M = 4 and four above (10944 x 2048, M = 8: 8.8 us against 9.0 with 16)
+    // M = 8 and four above (10944 x 2048, M = 8: 6.9-7.1 us against 7.4-7.5
+    // with four, 9.0 with sixteen)
     c.tiles = 1;
-    int waves = N >= 8192 ? (M <= 4 ? 8 : 4) : 16;
+    int waves = N >= 8192 ? (M <= 8 ? 8 : 4) : 16;
     while (waves > 1 && nfull < waves) waves /= 2;
     while ((nfull + waves - 1) / waves > 6 && waves < 16) waves *= 2;
     c.waves = waves;
