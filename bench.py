@@ -62,7 +62,7 @@ MEASURED_TRAFFIC = {("int4_gemv_nb<2,4,false,0>", 1): 52_495_211}
 # Average duration of the roofline kernel in the committed rocprofv3 kernel
 # trace of this bench (profiles/bench_kernel_trace_full.md), beside the
 # graph-timed figure the line computes live.  Keyed by (kernel, M).
-ROCPROF_US = {("int4_gemv_nb<2,4,false,0>", 1): (11.43, "profiles/bench_kernel_trace_full.md")}
+ROCPROF_US = {("int4_gemv_nb<2,4,false,0>", 1): (11.48, "profiles/bench_kernel_trace_full.md")}
 QWEN3_8B = [("qkv", 6144, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096),
             ("down", 4096, 12288)]
 FP8_SHAPES = [("2048x2048", 2048, 2048), ("10944x2048", 10944, 2048), ("2048x10944", 2048, 10944)]
